@@ -1,0 +1,164 @@
+/* nnc_hip.h — the C ABI of libnnc_hip.so: nnc's attention op on one AMD
+ * Instinct MI355X (gfx950) GPU.
+ *
+ * nnc has no op registry: its attention "op" is the trio
+ * nnc_attn_block / nnc_attn_merge / nnc_attn_finish (reference
+ * src/libnnc/nn_ops.h:31-61) driven by the attention core of
+ * attention_forward (reference src/libnnc/model.cpp:1693-1761) over the
+ * per-layer K/V buffers that model_kv_init sizes (reference
+ * src/libnnc/model.h:226-326, model.cpp:1891-2041). A per-block call is too
+ * fine-grained for a GPU, so this library replaces that core at layer
+ * granularity: one call per (layer, forward pass) computes, for every query
+ * token t of the batch and every query head h,
+ *
+ *   out[t][h] = sum over k in span(pos0 + t) of softmax_k(scale * q[t][h] . K[k]) * V[k]
+ *
+ * with the span of model_attn_span (reference model.cpp:2300-2316), KV head
+ * h / (n_head / n_kv), and key k stored in row k % rows of the layer's
+ * buffer. The K/V layout and element types are nnc's own, unchanged:
+ * token-major rows of kv_dim = n_kv * head_dim elements, BF16 (uint16 bit
+ * patterns, round-to-nearest-even from F32) or F32 (reference nnc.h:199-203,
+ * runtime.h:97-113).
+ *
+ * Errors follow nnc's convention (reference nnc.cpp:24-43, runtime.h:29-46):
+ * every call returns an nnc_status, a failure records a message readable with
+ * nnc_hip_last_error() on the calling thread, and nothing throws across the
+ * ABI. The status values are nnc.h's own; no new status is added.
+ *
+ * Threading: one nnc_hip_kv belongs to one session, which one thread drives
+ * at a time (reference nnc.h:27-32). Each cache owns one HIP stream; calls on
+ * one cache are ordered on it. Separate caches may be used from separate
+ * threads at once.
+ */
+#ifndef NNC_HIP_H
+#define NNC_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef NNC_H
+/* The status codes of reference nnc.h:50-61, same names and values. When
+ * nnc.h is included first, its own definition is used. */
+typedef enum nnc_status
+{
+	NNC_OK = 0,
+	NNC_ERR_INVALID_ARGUMENT = 1,
+	NNC_ERR_UNSUPPORTED_CPU = 2,
+	NNC_ERR_IO = 3,
+	NNC_ERR_BAD_FORMAT = 4,
+	NNC_ERR_UNSUPPORTED_MODEL = 5,
+	NNC_ERR_OUT_OF_MEMORY = 6,
+	NNC_ERR_CONTEXT_FULL = 7,
+	NNC_ERR_CANCELLED = 8,
+} nnc_status;
+#endif
+
+/* A session's K/V cache in device memory: one buffer per cache-owning layer,
+ * as in model_kv_cache::bufs (reference model.h:252-326). */
+typedef struct nnc_hip_kv nnc_hip_kv;
+
+/* Allocates n_buf K/V buffers in HBM, buffer i holding rows[i] rows of
+ * kv_dim[i] elements (BF16 when bf16, else F32), zero-filled, plus one HIP
+ * stream. Mirrors model_kv_init's buffer allocation (reference
+ * model.cpp:1908-1957; rows come from the same rule: n_ctx, or a ring of
+ * round_up(window + n_batch, 256) rows for a sliding layer).
+ * NNC_ERR_INVALID_ARGUMENT: n_buf <= 0, a NULL pointer, rows or kv_dim <= 0.
+ * NNC_ERR_OUT_OF_MEMORY: the device allocation failed.
+ * NNC_ERR_UNSUPPORTED_CPU: no usable HIP device (the nearest existing status:
+ * this machine cannot run the op). */
+nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* kv_dim, bool bf16,
+                             nnc_hip_kv** out);
+
+/* Frees the buffers, the scratch and the stream. NULL is a no-op. */
+void nnc_hip_kv_free(nnc_hip_kv* kv);
+
+/* Total device bytes held by the K/V buffers (reference model.h:325, bytes). */
+uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv);
+
+/* Writes n_tok rows for positions pos0 .. pos0 + n_tok - 1 into buffer
+ * `buf`, position p to row p % rows, from host memory already in the cache's
+ * element type (the KV append of reference model.cpp:1662-1691, whose BF16
+ * rounding is nnc_f32_to_bf16). k_rows and v_rows hold n_tok * kv_dim
+ * elements each. Asynchronous on the cache's stream; the host rows may be
+ * reused when the call returns (they are staged).
+ * NNC_ERR_INVALID_ARGUMENT: bad buffer index, n_tok <= 0, pos0 < 0, NULL rows,
+ * or n_tok > rows (the batch would overwrite itself). */
+nnc_status nnc_hip_kv_append(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const void* k_rows,
+                             const void* v_rows);
+
+/* As nnc_hip_kv_append, from F32 rows in host memory; a BF16 cache rounds
+ * them on the device with round-to-nearest-even, giving the bits of
+ * nnc_f32_to_bf16 (reference runtime.h:106-113). */
+nnc_status nnc_hip_kv_append_f32(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const float* k_rows,
+                                 const float* v_rows);
+
+/* As nnc_hip_kv_append_f32 with k_rows / v_rows in device memory. */
+nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok,
+                                        const float* k_rows, const float* v_rows);
+
+/* Copies rows row0 .. row0 + n_rows - 1 of buffer `buf` (raw element bits)
+ * to host memory and waits. Either output may be NULL. */
+nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_rows, void* k_out, void* v_out);
+
+/* The attention core of attention_forward (reference model.cpp:1693-1761)
+ * for one layer whose K/V live in buffer `buf`:
+ *   q   [n_tok][n_head * head_dim] F32, host memory;
+ *   out [n_tok][n_head * head_dim] F32, host memory, written when the call
+ *       returns (the call waits for the stream).
+ * Token t sits at position pos0 + t and attends to the keys of
+ * model_attn_span(causal, window, pos0 + t, n_seq): n_seq is pos0 + n_tok for
+ * a session, window is the layer's sliding window or 0. scale is
+ * hparams.attention_scale (reference model.cpp:613-624). An empty span gives
+ * zeros (the l == 0 rule of reference nn_ops.cpp:492).
+ * n_tok == 1 runs the split-K decode kernel, n_tok > 1 the MFMA prefill
+ * kernel. Supported shapes: head_dim 64, 128 or 256; group n_head / n_kv in
+ * {1, 2, 4, 8}.
+ * NNC_ERR_INVALID_ARGUMENT: bad buffer index, NULL pointers, n_tok <= 0,
+ * pos0 < 0, n_seq < 1, n_head not a multiple of n_kv, n_kv * head_dim not the
+ * buffer's kv_dim.
+ * NNC_ERR_CONTEXT_FULL: a key the batch needs lies outside what the buffer
+ * can hold (a full buffer with pos0 + n_tok > rows, or a ring too small for
+ * the window plus the batch).
+ * NNC_ERR_UNSUPPORTED_MODEL: a head_dim or group outside the supported set. */
+nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
+                          int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+                          int32_t head_dim, float scale);
+
+/* As nnc_hip_attend with q and out in device memory; asynchronous on the
+ * cache's stream (wait with nnc_hip_kv_sync). */
+nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok,
+                                 int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
+                                 int32_t n_kv, int32_t head_dim, float scale);
+
+/* Waits for all work queued on the cache's stream. */
+nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv);
+
+/* The cache's hipStream_t, for callers that order their own work on it. */
+void* nnc_hip_kv_stream(nnc_hip_kv* kv);
+
+/* Fills n elements at device address dst with N(0,1) values from the
+ * counter-based generator splitmix64 + Box-Muller (element i comes from
+ * draws 2*(i/2) and 2*(i/2)+1 of the stream `seed`), then, when norm_dim > 0,
+ * RMS-normalises each run of norm_dim elements (eps 1e-6), then stores them
+ * as F32 (bf16 == false) or BF16 rounded to nearest even (bf16 == true).
+ * Queued on `stream` (a hipStream_t; NULL is the null stream). This is the
+ * synthetic-input generator of the benchmark and has no counterpart in the
+ * reference. */
+nnc_status nnc_hip_fill_normal(void* dst, uint64_t n, uint64_t seed, int32_t norm_dim, bool bf16, void* stream);
+
+/* Detail of the most recent failure on the calling thread; never NULL. */
+const char* nnc_hip_last_error(void);
+
+/* A short description of `status` (the strings of nnc_status_string). */
+const char* nnc_hip_status_string(nnc_status status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NNC_HIP_H */

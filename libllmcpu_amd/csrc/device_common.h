@@ -1,0 +1,68 @@
+// Device-side helpers shared by the attention kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace nnchip
+{
+	// MFMA operand and accumulator types. v_mfma_f32_16x16x32_bf16 takes
+	// 8 bf16 of A and 8 of B per lane and accumulates 4 fp32 per lane:
+	//   A: lane l holds A[l % 16][8 * (l / 16) + j], j = 0..7   (M x K = 16 x 32)
+	//   B: lane l holds B[8 * (l / 16) + j][l % 16]              (K x N = 32 x 16)
+	//   D: lane l holds D[4 * (l / 16) + i][l % 16], i = 0..3    (M x N = 16 x 16)
+	typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+	typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+	typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+	__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c)
+	{
+		return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+	}
+
+	// nnc's BF16 contract (reference runtime.h:97-113): widen by a 16-bit
+	// shift, narrow with round-to-nearest-even on the bit pattern.
+	__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+	__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+	{
+		const uint32_t u = __float_as_uint(f);
+		return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+	}
+
+	// The two bf16 halves of one dword as fp32.
+	__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+	__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+	__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+	{
+		return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+	}
+
+	__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+	// Splits 8 fp32 values into bf16 hi + lo parts with x ~= hi + lo to about
+	// 16 significant bits, so two bf16 MFMAs give a near-fp32 product against
+	// an exact bf16 operand.
+	__device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo)
+	{
+		uint4 h, l;
+		uint32_t* hp = reinterpret_cast<uint32_t*>(&h);
+		uint32_t* lp = reinterpret_cast<uint32_t*>(&l);
+#pragma unroll
+		for (int j = 0; j < 4; ++j)
+		{
+			const float a = x[2 * j], b = x[2 * j + 1];
+			const uint32_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
+			hp[j] = ha | (hb << 16);
+			lp[j] = pack_bf16x2(a - bf16_bits_to_f32(ha), b - bf16_bits_to_f32(hb));
+		}
+		hi = as_bf16x8(h);
+		lo = as_bf16x8(l);
+	}
+
+	__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+	constexpr float kLog2e = 1.4426950408889634f;
+}

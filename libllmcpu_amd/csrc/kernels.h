@@ -1,0 +1,84 @@
+// Host-side declarations of the attention kernels' launchers and their
+// parameter blocks. Shared by the bridge (nnc_hip.hip) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace nnchip
+{
+	// Split-K attention of each query token independently (one token: the
+	// decode step; several: the fp32-exact batch path) over one layer's K/V.
+	struct decode_params
+	{
+		const float* q; // [n_tok][n_head * head_dim]
+		float* out; // [n_tok][n_head * head_dim]
+		const void* K; // [rows][kv_dim], BF16 bits or F32
+		const void* V;
+		float* part; // [n_tok][n_kv][n_split][group][head_dim + 2]: o, then m (log2 units), then l
+		unsigned* count; // [n_tok][n_kv] arrival counters, zero between launches
+		int rows, kv_dim, n_head;
+		int pos0, n_seq, window, causal; // token t sits at pos0 + t
+		int split_base; // first key of split 0, a multiple of split_keys
+		int split_keys; // keys per work-group, a multiple of decode_wg_keys()
+		int n_split; // work-groups per (token, KV head)
+		float qscale; // scale * log2(e)
+	};
+
+	// Keys one decode work-group consumes per iteration, for a head size and
+	// element type; split_keys must be a multiple of it.
+	int decode_wg_keys(int head_dim, bool bf16);
+
+	// Launches the decode kernel over an (n_split, n_kv, n_tok) grid; returns
+	// false when (head_dim, group, bf16) has no instantiation.
+	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
+	                   hipStream_t stream);
+
+	// Tiled MFMA attention for a batch of query tokens.
+	struct prefill_params
+	{
+		const float* q; // [n_tok][n_head * head_dim]
+		float* out; // [n_tok][n_head * head_dim]
+		const void* K; // [rows][kv_dim]
+		const void* V;
+		int rows, kv_dim, n_head, n_kv;
+		int n_tok, pos0, n_seq, window;
+		int causal;
+		int n_qtiles; // query tiles per KV head
+		float qscale; // scale * log2(e)
+	};
+
+	// Query rows ((token, head) pairs of one KV head) per prefill work-group.
+	int prefill_tile_rows(int head_dim, int group);
+
+	bool launch_prefill(const prefill_params& p, int head_dim, int group, bool bf16, hipStream_t stream);
+
+	// F32 rows -> the cache's element type, row (pos0 + t) % rows.
+	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
+	                       int n_tok, bool bf16, hipStream_t stream);
+
+	bool launch_fill_normal(void* dst, uint64_t n, uint64_t seed, int norm_dim, bool bf16, hipStream_t stream);
+
+	bool launch_zero(float* dst, size_t n, hipStream_t stream);
+
+	// The span of keys position `pos` attends to (reference model.cpp:2300-2316).
+	__host__ __device__ inline void attn_span(int causal, int window, int pos, int n_seq, int& first, int& last)
+	{
+		if (causal)
+		{
+			first = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+			last = pos < n_seq - 1 ? pos : n_seq - 1;
+		}
+		else if (window > 0)
+		{
+			first = pos - window / 2 > 0 ? pos - window / 2 : 0;
+			last = pos + window / 2 < n_seq - 1 ? pos + window / 2 : n_seq - 1;
+		}
+		else
+		{
+			first = 0;
+			last = n_seq - 1;
+		}
+	}
+}

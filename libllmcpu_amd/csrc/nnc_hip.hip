@@ -1,0 +1,491 @@
+// The C-ABI bridge declared in include/nnc_hip.h: device K/V buffers that
+// mirror model_kv_init's (reference src/libnnc/model.cpp:1891-1957), the
+// append of reference model.cpp:1662-1691, and one attention call per layer
+// in place of the attention core of reference model.cpp:1693-1761.
+//
+// Every entry point checks its arguments before touching the device, so a
+// refused call changes nothing (the "fail before it changes anything" rule of
+// reference model.cpp:2046-2057). Failures set a thread-local message and
+// return an nnc_status; no C++ exception crosses the ABI.
+#include "../../include/nnc_hip.h"
+#include "kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace
+{
+	thread_local std::string g_last_error = "";
+
+	nnc_status fail(nnc_status status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+	nnc_status fail(nnc_status status, const char* fmt, ...)
+	{
+		char buf[512];
+		va_list ap;
+		va_start(ap, fmt);
+		std::vsnprintf(buf, sizeof buf, fmt, ap);
+		va_end(ap);
+		g_last_error = buf;
+		return status;
+	}
+
+	// A device runtime failure. Out-of-memory maps to nnc's own status; any
+	// other fault of the device runtime is reported as an I/O failure of the
+	// device, with the runtime's text.
+	nnc_status hip_fail(hipError_t e, const char* what)
+	{
+		if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+			return fail(NNC_ERR_OUT_OF_MEMORY, "%s: device out of memory", what);
+		return fail(NNC_ERR_IO, "%s: %s", what, hipGetErrorString(e));
+	}
+
+#define NNC_HIP_TRY(expr, what)                                                                                     \
+	do                                                                                                                \
+	{                                                                                                                 \
+		const hipError_t e_ = (expr);                                                                                 \
+		if (e_ != hipSuccess) return hip_fail(e_, what);                                                             \
+	} while (0)
+
+	struct kv_buffer
+	{
+		void* k = nullptr;
+		void* v = nullptr;
+		int32_t rows = 0;
+		int32_t kv_dim = 0;
+	};
+
+	// Grow-only device scratch.
+	struct dev_scratch
+	{
+		void* ptr = nullptr;
+		size_t bytes = 0;
+	};
+
+	constexpr int kAttnBlock = 256; // reference model.h:229
+	constexpr int kMaxSplits = 256; // the decode kernel's final merge holds 256 weights per head
+	constexpr int32_t kDecodeChunk = 1024; // tokens per split-K launch
+}
+
+struct nnc_hip_kv
+{
+	int device = 0;
+	int n_cu = 256;
+	bool bf16 = true;
+	hipStream_t stream = nullptr;
+	std::vector<kv_buffer> bufs;
+	uint64_t bytes = 0;
+	dev_scratch part; // decode partials
+	dev_scratch count; // decode arrival counters (kept zero between launches)
+	dev_scratch q; // staging of host q / out / append rows
+	dev_scratch out;
+	dev_scratch rows_k;
+	dev_scratch rows_v;
+};
+
+namespace
+{
+	void release(nnc_hip_kv* kv)
+	{
+		if (!kv) return;
+		if (kv->stream) (void)hipStreamSynchronize(kv->stream);
+		for (auto& b : kv->bufs)
+		{
+			if (b.k) (void)hipFree(b.k);
+			if (b.v) (void)hipFree(b.v);
+		}
+		for (dev_scratch* s : {&kv->part, &kv->count, &kv->q, &kv->out, &kv->rows_k, &kv->rows_v})
+			if (s->ptr) (void)hipFree(s->ptr);
+		if (kv->stream) (void)hipStreamDestroy(kv->stream);
+		delete kv;
+	}
+
+	// Makes s at least `bytes` long. A new allocation is zeroed on the stream
+	// (the decode counters rely on it); the old one is freed after the stream
+	// has drained.
+	nnc_status reserve(nnc_hip_kv* kv, dev_scratch& s, size_t bytes, const char* what)
+	{
+		if (s.bytes >= bytes) return NNC_OK;
+		NNC_HIP_TRY(hipStreamSynchronize(kv->stream), what);
+		if (s.ptr) NNC_HIP_TRY(hipFree(s.ptr), what);
+		s.ptr = nullptr;
+		s.bytes = 0;
+		const size_t n = (std::max<size_t>(bytes, 256) + 255) & ~static_cast<size_t>(255);
+		NNC_HIP_TRY(hipMalloc(&s.ptr, n), what);
+		s.bytes = n;
+		NNC_HIP_TRY(hipMemsetAsync(s.ptr, 0, n, kv->stream), what);
+		return NNC_OK;
+	}
+
+	nnc_status check_kv(const nnc_hip_kv* kv, int32_t buf)
+	{
+		if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the cache is NULL");
+		if (buf < 0 || buf >= static_cast<int32_t>(kv->bufs.size()))
+			return fail(NNC_ERR_INVALID_ARGUMENT, "buffer %d outside [0, %zu)", buf, kv->bufs.size());
+		return NNC_OK;
+	}
+
+	nnc_status check_append(const nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const void* k,
+	                        const void* v)
+	{
+		if (nnc_status s = check_kv(kv, buf)) return s;
+		if (!k || !v) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL K/V rows");
+		if (n_tok <= 0 || pos0 < 0) return fail(NNC_ERR_INVALID_ARGUMENT, "append of %d rows at position %d", n_tok, pos0);
+		if (n_tok > kv->bufs[buf].rows)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "%d rows do not fit a buffer of %d rows", n_tok, kv->bufs[buf].rows);
+		return NNC_OK;
+	}
+
+	// Raw rows already in the element type: copy in at most two pieces
+	// (before and after the ring's wrap).
+	nnc_status append_raw(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const void* k_rows,
+	                      const void* v_rows, hipMemcpyKind kind)
+	{
+		const kv_buffer& b = kv->bufs[buf];
+		const size_t row_bytes = static_cast<size_t>(b.kv_dim) * (kv->bf16 ? 2 : 4);
+		int32_t done = 0;
+		while (done < n_tok)
+		{
+			const int32_t row = (pos0 + done) % b.rows;
+			const int32_t n = std::min(n_tok - done, b.rows - row);
+			const size_t off = static_cast<size_t>(row) * row_bytes, src = static_cast<size_t>(done) * row_bytes;
+			NNC_HIP_TRY(hipMemcpyAsync(static_cast<char*>(b.k) + off, static_cast<const char*>(k_rows) + src,
+			                           n * row_bytes, kind, kv->stream),
+			            "K/V append");
+			NNC_HIP_TRY(hipMemcpyAsync(static_cast<char*>(b.v) + off, static_cast<const char*>(v_rows) + src,
+			                           n * row_bytes, kind, kv->stream),
+			            "K/V append");
+			done += n;
+		}
+		return NNC_OK;
+	}
+
+	// Split size: about two work-groups per CU over all (token, KV head)
+	// pairs, a multiple of what one work-group iteration consumes, and at
+	// most kMaxSplits splits.
+	nnc_status decode_chunk(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, int32_t n_tok, int32_t pos0,
+	                        int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
+	                        float scale)
+	{
+		const int group = n_head / n_kv;
+		const bool bf16 = kv->bf16;
+		int kmin, kmax, unused;
+		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, kmin, unused);
+		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, unused, kmax);
+		if (kmax < kmin) return nnchip::launch_zero(out, static_cast<size_t>(n_tok) * n_head * head_dim, kv->stream)
+			                       ? NNC_OK
+			                       : NNC_ERR_IO;
+		const int wgk = nnchip::decode_wg_keys(head_dim, bf16);
+		const int span = kmax - kmin + 1;
+		const long long pairs = static_cast<long long>(n_tok) * n_kv;
+		const long long want = std::max<long long>(1, 2LL * kv->n_cu / std::max<long long>(pairs, 1));
+		long long sk = (span + want - 1) / want;
+		sk = std::max<long long>(wgk, (sk + wgk - 1) / wgk * wgk);
+		while ((kmax / sk) - (kmin / sk) + 1 > kMaxSplits) sk += wgk;
+		const int split_keys = static_cast<int>(sk);
+		const int split_base = (kmin / split_keys) * split_keys;
+		const int n_split = kmax / split_keys - kmin / split_keys + 1;
+
+		const size_t part_floats = static_cast<size_t>(pairs) * n_split * group * (head_dim + 2);
+		if (nnc_status s = reserve(kv, kv->part, part_floats * sizeof(float), "decode scratch")) return s;
+		if (nnc_status s = reserve(kv, kv->count, static_cast<size_t>(pairs) * sizeof(unsigned), "decode counters"))
+			return s;
+
+		nnchip::decode_params p{};
+		p.q = q;
+		p.out = out;
+		p.K = b.k;
+		p.V = b.v;
+		p.part = static_cast<float*>(kv->part.ptr);
+		p.count = static_cast<unsigned*>(kv->count.ptr);
+		p.rows = b.rows;
+		p.kv_dim = b.kv_dim;
+		p.n_head = n_head;
+		p.pos0 = pos0;
+		p.n_seq = n_seq;
+		p.window = window;
+		p.causal = causal ? 1 : 0;
+		p.split_base = split_base;
+		p.split_keys = split_keys;
+		p.n_split = n_split;
+		p.qscale = scale * 1.4426950408889634f;
+		if (!nnchip::launch_decode(p, n_kv, n_tok, head_dim, group, bf16, kv->stream))
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no decode kernel for head_dim %d, group %d", head_dim, group);
+		NNC_HIP_TRY(hipGetLastError(), "decode launch");
+		return NNC_OK;
+	}
+
+	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
+	                       int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
+	                       float scale)
+	{
+		const kv_buffer& b = kv->bufs[buf];
+		const int group = n_head / n_kv;
+		const bool bf16 = kv->bf16;
+		const size_t q_floats = static_cast<size_t>(n_tok) * n_head * head_dim;
+
+		int first0, last0, first1, last1;
+		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, first0, last0);
+		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, first1, last1);
+		(void)last0;
+		(void)first1;
+		const int kmin = first0, kmax = last1;
+		if (kmax < kmin) return nnchip::launch_zero(out, q_floats, kv->stream) ? NNC_OK : NNC_ERR_IO;
+
+		// Prefill kernel for BF16 batches; the split-K kernel for decode and for
+		// F32 batches (exact fp32 products against F32 K/V).
+		if (n_tok > 1 && bf16)
+		{
+			nnchip::prefill_params p{};
+			p.q = q;
+			p.out = out;
+			p.K = b.k;
+			p.V = b.v;
+			p.rows = b.rows;
+			p.kv_dim = b.kv_dim;
+			p.n_head = n_head;
+			p.n_kv = n_kv;
+			p.n_tok = n_tok;
+			p.pos0 = pos0;
+			p.n_seq = n_seq;
+			p.window = window;
+			p.causal = causal ? 1 : 0;
+			const int tile = nnchip::prefill_tile_rows(head_dim, group);
+			p.n_qtiles = (n_tok * group + tile - 1) / tile;
+			p.qscale = scale * 1.4426950408889634f;
+			if (!nnchip::launch_prefill(p, head_dim, group, bf16, kv->stream))
+				return fail(NNC_ERR_UNSUPPORTED_MODEL, "no prefill kernel for head_dim %d, group %d", head_dim, group);
+			NNC_HIP_TRY(hipGetLastError(), "prefill launch");
+			return NNC_OK;
+		}
+
+		// The split-K kernel, over chunks of at most kDecodeChunk tokens (a
+		// grid z-extent and a scratch size that stay small).
+		for (int32_t t0 = 0; t0 < n_tok; t0 += kDecodeChunk)
+		{
+			const int32_t nt = std::min(kDecodeChunk, n_tok - t0);
+			const size_t off = static_cast<size_t>(t0) * n_head * head_dim;
+			if (nnc_status s = decode_chunk(kv, b, q + off, out + off, nt, pos0 + t0, n_seq, window, causal, n_head, n_kv,
+			                                head_dim, scale))
+				return s;
+		}
+		return NNC_OK;
+	}
+
+	nnc_status check_attend(const nnc_hip_kv* kv, int32_t buf, const float* q, const float* out, int32_t n_tok,
+	                        int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+	                        int32_t head_dim)
+	{
+		if (nnc_status s = check_kv(kv, buf)) return s;
+		if (!q || !out) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL q or out");
+		if (n_tok <= 0 || pos0 < 0 || n_seq < 1 || window < 0)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "bad batch: %d tokens at %d, n_seq %d, window %d", n_tok, pos0, n_seq,
+			            window);
+		if (n_kv <= 0 || n_head <= 0 || n_head % n_kv != 0 || head_dim <= 0)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "bad heads: %d query heads over %d KV heads, head_dim %d", n_head,
+			            n_kv, head_dim);
+		const kv_buffer& b = kv->bufs[buf];
+		if (static_cast<long long>(n_kv) * head_dim != b.kv_dim)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "%d KV heads of %d do not make the buffer's kv_dim %d", n_kv, head_dim,
+			            b.kv_dim);
+		const int group = n_head / n_kv;
+		if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+		    (group != 1 && group != 2 && group != 4 && group != 8))
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "head_dim %d with group %d is not supported on the GPU", head_dim,
+			            group);
+		if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
+		// Every key the batch reads must still be in the buffer: the newest
+		// position written is n_seq - 1, and the buffer keeps the last `rows`.
+		int first0, last0;
+		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, first0, last0);
+		(void)last0;
+		if (static_cast<long long>(n_seq) - first0 > b.rows)
+			return fail(NNC_ERR_CONTEXT_FULL, "keys %d .. %d do not fit a buffer of %d rows", first0, n_seq - 1, b.rows);
+		return NNC_OK;
+	}
+}
+
+extern "C" {
+
+nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* kv_dim, bool bf16, nnc_hip_kv** out)
+{
+	if (!out) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL output handle");
+	*out = nullptr;
+	if (n_buf <= 0 || !rows || !kv_dim) return fail(NNC_ERR_INVALID_ARGUMENT, "%d buffers, rows or kv_dim NULL", n_buf);
+	for (int32_t i = 0; i < n_buf; ++i)
+		if (rows[i] <= 0 || kv_dim[i] <= 0 || kv_dim[i] % 8 != 0)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "buffer %d: %d rows of %d elements (kv_dim must be a positive multiple of 8)",
+			            i, rows[i], kv_dim[i]);
+	int n_dev = 0;
+	if (hipGetDeviceCount(&n_dev) != hipSuccess || n_dev <= 0)
+		return fail(NNC_ERR_UNSUPPORTED_CPU, "no HIP device is available");
+
+	nnc_hip_kv* kv = new (std::nothrow) nnc_hip_kv();
+	if (!kv) return fail(NNC_ERR_OUT_OF_MEMORY, "out of host memory");
+	kv->bf16 = bf16;
+	auto bail = [&](nnc_status s)
+	{
+		release(kv);
+		return s;
+	};
+	hipError_t e = hipGetDevice(&kv->device);
+	if (e == hipSuccess) e = hipDeviceGetAttribute(&kv->n_cu, hipDeviceAttributeMultiprocessorCount, kv->device);
+	if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking);
+	if (e != hipSuccess) return bail(hip_fail(e, "device setup"));
+	const size_t esize = bf16 ? 2 : 4;
+	kv->bufs.resize(static_cast<size_t>(n_buf));
+	for (int32_t i = 0; i < n_buf; ++i)
+	{
+		kv_buffer& b = kv->bufs[i];
+		b.rows = rows[i];
+		b.kv_dim = kv_dim[i];
+		const size_t n = static_cast<size_t>(rows[i]) * kv_dim[i] * esize;
+		e = hipMalloc(&b.k, n);
+		if (e == hipSuccess) e = hipMalloc(&b.v, n);
+		if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, n, kv->stream);
+		if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, n, kv->stream);
+		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
+		kv->bytes += 2 * n;
+	}
+	e = hipStreamSynchronize(kv->stream);
+	if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
+	*out = kv;
+	return NNC_OK;
+}
+
+void nnc_hip_kv_free(nnc_hip_kv* kv) { release(kv); }
+
+uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv) { return kv ? kv->bytes : 0; }
+
+nnc_status nnc_hip_kv_append(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const void* k_rows,
+                             const void* v_rows)
+{
+	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
+	// Stage through device scratch so the host rows are free on return.
+	const size_t bytes = static_cast<size_t>(n_tok) * kv->bufs[buf].kv_dim * (kv->bf16 ? 2 : 4);
+	if (nnc_status s = reserve(kv, kv->rows_k, bytes, "append staging")) return s;
+	if (nnc_status s = reserve(kv, kv->rows_v, bytes, "append staging")) return s;
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_k.ptr, k_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_v.ptr, v_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	return append_raw(kv, buf, pos0, n_tok, kv->rows_k.ptr, kv->rows_v.ptr, hipMemcpyDeviceToDevice);
+}
+
+nnc_status nnc_hip_kv_append_f32(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const float* k_rows,
+                                 const float* v_rows)
+{
+	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
+	const size_t bytes = static_cast<size_t>(n_tok) * kv->bufs[buf].kv_dim * sizeof(float);
+	if (nnc_status s = reserve(kv, kv->rows_k, bytes, "append staging")) return s;
+	if (nnc_status s = reserve(kv, kv->rows_v, bytes, "append staging")) return s;
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_k.ptr, k_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_v.ptr, v_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	return nnc_hip_kv_append_f32_device(kv, buf, pos0, n_tok, static_cast<const float*>(kv->rows_k.ptr),
+	                                    static_cast<const float*>(kv->rows_v.ptr));
+}
+
+nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const float* k_rows,
+                                        const float* v_rows)
+{
+	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
+	const kv_buffer& b = kv->bufs[buf];
+	nnchip::launch_append_f32(b.k, b.v, k_rows, v_rows, b.rows, b.kv_dim, pos0, n_tok, kv->bf16, kv->stream);
+	NNC_HIP_TRY(hipGetLastError(), "K/V append");
+	return NNC_OK;
+}
+
+nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_rows, void* k_out, void* v_out)
+{
+	if (nnc_status s = check_kv(kv, buf)) return s;
+	const kv_buffer& b = kv->bufs[buf];
+	if (row0 < 0 || n_rows < 0 || row0 + static_cast<long long>(n_rows) > b.rows)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "rows %d .. %d outside a buffer of %d", row0, row0 + n_rows - 1, b.rows);
+	const size_t row_bytes = static_cast<size_t>(b.kv_dim) * (kv->bf16 ? 2 : 4);
+	const size_t off = static_cast<size_t>(row0) * row_bytes, n = static_cast<size_t>(n_rows) * row_bytes;
+	if (k_out && n)
+		NNC_HIP_TRY(hipMemcpyAsync(k_out, static_cast<char*>(b.k) + off, n, hipMemcpyDeviceToHost, kv->stream), "K/V read");
+	if (v_out && n)
+		NNC_HIP_TRY(hipMemcpyAsync(v_out, static_cast<char*>(b.v) + off, n, hipMemcpyDeviceToHost, kv->stream), "K/V read");
+	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "K/V read");
+	return NNC_OK;
+}
+
+nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
+                          int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
+                          float scale)
+{
+	// Host pointers need no alignment: they are staged.
+	static const float aligned_probe[4] = {0, 0, 0, 0};
+	if (nnc_status s = check_attend(kv, buf, q ? aligned_probe : nullptr, out ? aligned_probe : nullptr, n_tok, pos0,
+	                                n_seq, window, causal, n_head, n_kv, head_dim))
+		return s;
+	const size_t bytes = static_cast<size_t>(n_tok) * n_head * head_dim * sizeof(float);
+	if (nnc_status s = reserve(kv, kv->q, bytes, "q staging")) return s;
+	if (nnc_status s = reserve(kv, kv->out, bytes, "out staging")) return s;
+	NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, q, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
+	if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), static_cast<float*>(kv->out.ptr),
+	                               n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale))
+		return s;
+	NNC_HIP_TRY(hipMemcpyAsync(out, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
+	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "attention");
+	return NNC_OK;
+}
+
+nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
+                                 int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+                                 int32_t head_dim, float scale)
+{
+	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
+		return s;
+	return attend_impl(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+}
+
+nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv)
+{
+	if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the cache is NULL");
+	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+	return NNC_OK;
+}
+
+void* nnc_hip_kv_stream(nnc_hip_kv* kv) { return kv ? static_cast<void*>(kv->stream) : nullptr; }
+
+nnc_status nnc_hip_fill_normal(void* dst, uint64_t n, uint64_t seed, int32_t norm_dim, bool bf16, void* stream)
+{
+	if (!dst && n) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL destination");
+	if (norm_dim < 0 || (norm_dim > 0 && n % static_cast<uint64_t>(norm_dim) != 0))
+		return fail(NNC_ERR_INVALID_ARGUMENT, "%llu elements are not whole runs of %d", static_cast<unsigned long long>(n),
+		            norm_dim);
+	if (n == 0) return NNC_OK;
+	nnchip::launch_fill_normal(dst, n, seed, norm_dim, bf16, static_cast<hipStream_t>(stream));
+	NNC_HIP_TRY(hipGetLastError(), "fill");
+	return NNC_OK;
+}
+
+const char* nnc_hip_last_error(void) { return g_last_error.c_str(); }
+
+const char* nnc_hip_status_string(nnc_status status)
+{
+	switch (status)
+	{
+	case NNC_OK: return "ok";
+	case NNC_ERR_INVALID_ARGUMENT: return "invalid argument";
+	case NNC_ERR_UNSUPPORTED_CPU: return "unsupported CPU";
+	case NNC_ERR_IO: return "I/O error";
+	case NNC_ERR_BAD_FORMAT: return "bad file format";
+	case NNC_ERR_UNSUPPORTED_MODEL: return "unsupported model";
+	case NNC_ERR_OUT_OF_MEMORY: return "out of memory";
+	case NNC_ERR_CONTEXT_FULL: return "context full";
+	case NNC_ERR_CANCELLED: return "cancelled";
+	}
+	return "unknown status";
+}
+
+} // extern "C"

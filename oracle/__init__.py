@@ -1,0 +1,205 @@
+"""TEST INFRASTRUCTURE — ctypes bindings of the CPU oracle.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this package, and only as the checker (or, in the bench, as the timed CPU
+baseline): the product path never calls it.
+
+- ``Oracle`` binds liboracle.so, this repository's restatement of nnc's
+  attention core (nnc_oracle.cpp; each function cites the reference lines it
+  follows) plus the double-precision textbook checker.
+- ``Reference`` binds _ref/libnnc_ref.so: the reference's own libnnc sources,
+  compiled from /root/reference by oracle/Makefile, behind a small C driver
+  (ref_driver.cpp). It exists only where it was built; it travels to the GPU
+  box as a built file.
+
+Build both with ``make -C oracle`` (``build()`` below).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libnnc_ref.so"
+REF_SRC = Path("/root/reference/src/libnnc")
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+_I = C.c_int
+_F = C.c_float
+
+
+def build(verbose: bool = False) -> None:
+    """make -B -C oracle: rebuilds liboracle.so, and _ref/libnnc_ref.so when
+    the reference sources are present."""
+    r = subprocess.run(["make", "-B", "-C", str(HERE), "-j8"], capture_output=True, text=True)
+    if verbose:
+        print(r.stdout)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{r.stdout}\n{r.stderr}")
+
+
+def _p(a: np.ndarray | None) -> int | None:
+    return None if a is None else a.ctypes.data
+
+
+_LAYER_ARGS = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F]
+
+
+class _Lib:
+    prefix = ""
+
+    def __init__(self, path: Path):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} is not built (make -C oracle)")
+        self.lib = C.CDLL(str(path))
+        f = self._fn
+        f("attn_block", None, [_P, _SZ, _P, _P, _I, _SZ, _SZ, _SZ, _SZ, _F, _P, _P])
+        f("attn_merge", None, [_P, _P, _SZ, _SZ])
+        f("attn_finish", None, [_P, _SZ, _P, _SZ, _SZ])
+        f("attn_span", None, [_I, _I, _I, _I, C.POINTER(_I), C.POINTER(_I)])
+        f("bf16_round", None, [_P, _P, _SZ])
+        f("rope", None, [_P, _I, _I, _I, _F, _F, _I])
+        f("rmsnorm_groups", None, [_P, _SZ, _SZ, _F])
+
+    def _fn(self, name, res, args):
+        fn = getattr(self.lib, self.prefix + name)
+        fn.restype = res
+        fn.argtypes = args
+        setattr(self, "_" + name, fn)
+        return fn
+
+    # -- the op's pieces --------------------------------------------------------------
+    def attn_block(self, q, K, V, kv_bf16, kv_stride, n_keys, head_dim, n_heads, scale, q_stride=None):
+        """One block's partial [n_heads, head_dim + 2] (o, m, l)."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        scores = np.zeros(n_heads * max(n_keys, 1), dtype=np.float32)
+        part = np.zeros(n_heads * (head_dim + 2), dtype=np.float32)
+        self._attn_block(_p(q), q_stride or head_dim, _p(K), _p(V), int(kv_bf16), kv_stride, n_keys, head_dim,
+                         n_heads, scale, _p(scores), _p(part))
+        return part.reshape(n_heads, head_dim + 2)
+
+    def attn_merge(self, acc, part, head_dim, n_heads):
+        acc = np.ascontiguousarray(acc, dtype=np.float32).copy()
+        part = np.ascontiguousarray(part, dtype=np.float32)
+        self._attn_merge(_p(acc), _p(part), head_dim, n_heads)
+        return acc
+
+    def attn_finish(self, acc, head_dim, n_heads):
+        acc = np.ascontiguousarray(acc, dtype=np.float32)
+        out = np.zeros(n_heads * head_dim, dtype=np.float32)
+        self._attn_finish(_p(out), head_dim, _p(acc), head_dim, n_heads)
+        return out.reshape(n_heads, head_dim)
+
+    def attn_span(self, causal, window, pos, n_seq):
+        a, b = _I(), _I()
+        self._attn_span(int(causal), window, pos, n_seq, C.byref(a), C.byref(b))
+        return a.value, b.value
+
+    def bf16_round(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(x.shape, dtype=np.uint16)
+        self._bf16_round(_p(x), _p(y), x.size)
+        return y
+
+    def rope(self, x, n_heads, head_dim, n_rot, pos, base, mode):
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        self._rope(_p(x), n_heads, head_dim, n_rot, pos, base, mode)
+        return x
+
+    def rmsnorm_groups(self, x, dim, eps=1e-6):
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        self._rmsnorm_groups(_p(x), x.size // dim, dim, eps)
+        return x
+
+
+def _layer_call(fn, extra, q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_tok = q.size // (n_head * head_dim)
+    out = np.zeros((n_tok, n_head * head_dim), dtype=np.float32)
+    if n_seq is None:
+        n_seq = pos0 + n_tok
+    K = np.ascontiguousarray(K)
+    V = np.ascontiguousarray(V)
+    rc = fn(_p(q), _p(out), _p(K), _p(V), int(kv_bf16), rows, n_tok, pos0, n_seq, window, int(causal), n_head, n_kv,
+            head_dim, scale, *extra)
+    if rc not in (None, 0):
+        raise ValueError("oracle refused the arguments")
+    return out
+
+
+class Oracle(_Lib):
+    """This repository's C++ restatement of nnc's attention core."""
+
+    prefix = "orc_"
+
+    def __init__(self, path: Path = ORACLE_SO):
+        super().__init__(path)
+        self._fn("attend_layer", _I, _LAYER_ARGS + [_I])
+        self._fn("textbook_attend", None, _LAYER_ARGS)
+        self._fn("kv_rows", _I, [_I, _I, _I])
+        self._fn("max_rewind", _I, [_I, _I])
+        self._fn("f32_from_bf16", _F, [C.c_uint16])
+        self._fn("bf16_from_f32", C.c_uint16, [_F])
+        self._fn("ref_fixture_attn_blocks", _I, [_I, _P, _P, _P])
+
+    def attend_layer(self, q, K, V, *, kv_bf16, rows, pos0, n_seq=None, window=0, causal=True, n_head, n_kv,
+                     head_dim, scale, threads=8):
+        """Layer-granularity attention: nnc's dispatch over this file's kernels."""
+        return _layer_call(self._attend_layer, [threads], q, K, V, kv_bf16, rows, pos0, n_seq, window, causal,
+                           n_head, n_kv, head_dim, scale)
+
+    def textbook(self, q, K, V, *, kv_bf16, rows, pos0, n_seq=None, window=0, causal=True, n_head, n_kv, head_dim,
+                 scale):
+        """Double-precision softmax attention per query head over its span."""
+        return _layer_call(self._textbook_attend, [], q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head,
+                           n_kv, head_dim, scale)
+
+    def kv_rows(self, n_ctx, window, n_batch):
+        return self._kv_rows(n_ctx, window, n_batch)
+
+    def max_rewind(self, rows, window):
+        return self._max_rewind(rows, window)
+
+    def ref_fixture_attn_blocks(self, which):
+        """Inputs of case `which` of the reference's test_nnc_attn_blocks."""
+        q = np.zeros(3 * 64, dtype=np.float32)
+        K = np.zeros(600 * 2 * 64, dtype=np.float32)
+        V = np.zeros(600 * 2 * 64, dtype=np.float32)
+        hd = self._ref_fixture_attn_blocks(which, _p(q), _p(K), _p(V))
+        if hd < 0:
+            raise ValueError(which)
+        return hd, q[: 3 * hd], K[: 600 * 2 * hd].reshape(600, 2 * hd), V[: 600 * 2 * hd].reshape(600, 2 * hd)
+
+
+class Reference(_Lib):
+    """The reference's own compiled attention kernels, thread pool and helpers."""
+
+    prefix = "ref_"
+
+    def __init__(self, path: Path = REF_SO):
+        super().__init__(path)
+        self._fn("attend_layer", _I, _LAYER_ARGS)
+        self._fn("set_threads", None, [_I])
+        self._fn("threads", _I, [])
+
+    def set_threads(self, n: int) -> None:
+        self._set_threads(n)
+
+    def threads(self) -> int:
+        return self._threads()
+
+    def attend_layer(self, q, K, V, *, kv_bf16, rows, pos0, n_seq=None, window=0, causal=True, n_head, n_kv,
+                     head_dim, scale):
+        """nnc_attn_block/merge/finish through nnc's own worker pool, with the
+        dispatch of reference model.cpp:1229-1317, 1693-1757 restated."""
+        return _layer_call(self._attend_layer, [], q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head, n_kv,
+                           head_dim, scale)
+
+
+def reference_available() -> bool:
+    return REF_SO.exists()

@@ -1,0 +1,236 @@
+"""Parity of the HIP attention op against nnc's CPU attention (the oracle,
+itself pinned against the reference in test_oracle.py), through the C ABI.
+
+Bounds (max-abs over all outputs): 1e-3 for F32 K/V, 5e-3 for BF16 K/V.
+Each test prints its case before the GPU call."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import libllmcpu_amd as nh
+from libllmcpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def errors(got, want):
+    d = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    rel = d / np.maximum(np.abs(want), 1e-6)
+    return float(d.max()), float(rel.max())
+
+
+def run_case(orc, cfg, layer, *, n_seq, pos0, n_tok, n_batch=16, rows=None, threads=8, causal=True):
+    """Fills one layer's cache as a session would have (positions 0..n_seq-1),
+    runs the op for tokens pos0 .. pos0 + n_tok - 1 on the GPU and on the oracle."""
+    window = cfg.layer_window(layer)
+    if rows is None:
+        rows = cfg.layer_rows(layer, n_seq, n_batch)
+    K, V = synth.cache_buffer(cfg, layer, rows, n_seq)
+    q = synth.qk_rows(cfg, layer, 0, np.arange(pos0, pos0 + n_tok), cfg.n_head)
+    kw = dict(window=window, causal=causal, n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim,
+              scale=cfg.attn_scale)
+    say(f"case {cfg.name} layer {layer}: n_seq {n_seq} rows {rows} window {window} tokens {pos0}+{n_tok}")
+    with nh.KVCache([rows], [cfg.kv_dim], bf16=cfg.kv_bf16) as kv:
+        kv.append(0, 0, K, V)
+        got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+    want = orc.attend_layer(q, K, V, kv_bf16=cfg.kv_bf16, rows=rows, pos0=pos0, n_seq=n_seq, threads=threads, **kw)
+    return got, want
+
+
+# ---- decode -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("key,layers,ctx", [
+    ("A", (0, 1, 17), 1024),       # Gemma-3-270M: F32 K/V, hd 256, 1024 keys
+    ("B", (0, 15), 512),           # Llama-3.2-1B with RoPE NORM, hd 64
+    ("B", (3,), 4096),
+    ("C", (0, 5), 8192),           # Gemma-3-1B: a local (ring 2560) and a global layer
+    ("D", (0,), 4096),             # Qwen3-4B, RMS-normed Q/K, hd 128
+    ("E", (0, 5), 16640),          # Gemma-3-4B: local ring (window 1024) and global, g = 2
+])
+def test_decode_parity(orc, key, layers, ctx):
+    cfg = synth.CONFIGS[key]
+    for layer in layers:
+        got, want = run_case(orc, cfg, layer, n_seq=ctx, pos0=ctx - 1, n_tok=1, n_batch=2048 if key == "C" else 1024)
+        ea, er = errors(got, want)
+        say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+        assert ea <= cfg.tol, (key, layer, ea)
+
+
+def test_decode_qwen3_32k_full_size(orc):
+    """Config D at its headline context: one layer, 32768 cached keys."""
+    cfg = synth.CONFIGS["D"]
+    got, want = run_case(orc, cfg, 7, n_seq=32768, pos0=32767, n_tok=1)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= cfg.tol
+
+
+def test_decode_is_deterministic_and_matches_textbook(orc):
+    cfg = synth.CONFIGS["D"]
+    n_seq = 3000
+    K, V = synth.cache_buffer(cfg, 2, n_seq, n_seq)
+    q = synth.qk_rows(cfg, 2, 0, np.array([n_seq - 1]), cfg.n_head)
+    kw = dict(n_head=32, n_kv=8, head_dim=128, scale=cfg.attn_scale)
+    say("case decode determinism, D, 3000 keys")
+    with nh.KVCache([n_seq], [cfg.kv_dim]) as kv:
+        kv.append(0, 0, K, V)
+        a = kv.attend(0, q, pos0=n_seq - 1, **kw)
+        b = kv.attend(0, q, pos0=n_seq - 1, **kw)
+    assert np.array_equal(a, b)
+    t = orc.textbook(q, K, V, kv_bf16=True, rows=n_seq, pos0=n_seq - 1, **kw)
+    assert errors(a, t)[0] <= 5e-4  # the split-Q MFMA scores are near-fp32
+
+
+def test_decode_edge_spans(orc):
+    """One key (position 0), a ring that wraps inside a split, a span that
+    starts mid-block, and an empty span (an MTP drafter's query past the
+    keys its target evaluated: zeros, the l == 0 rule)."""
+    cfg = synth.AttnConfig(7, "edge", 8, 2, 128, 1, window=300, swa_period=6)
+    kw = dict(n_head=8, n_kv=2, head_dim=128, scale=0.09)
+    rows = 512
+    n_seq = 1700  # ring of 512 rows holds positions 1188..1699; row 0 is position 1536
+    K, V = synth.cache_buffer(cfg, 0, rows, n_seq)
+    with nh.KVCache([rows, 64], [256, 256]) as kv:
+        kv.append(0, 0, K, V)
+        for pos, n_s, w in ((1699, 1700, 300), (1699, 1700, 512), (1600, 1700, 300), (1650, 1700, 0)):
+            say(f"case ring decode pos {pos} window {w}")
+            q = synth.qk_rows(cfg, 0, 0, np.array([pos]), 8)
+            if w == 0:
+                with pytest.raises(nh.NncError) as e:  # keys 0.. are long gone from a 512-row ring
+                    kv.attend(0, q, pos0=pos, n_seq=n_s, window=w, **kw)
+                assert e.value.status == nh.NncStatus.CONTEXT_FULL
+                continue
+            got = kv.attend(0, q, pos0=pos, n_seq=n_s, window=w, **kw)
+            want = orc.attend_layer(q, K, V, kv_bf16=True, rows=rows, pos0=pos, n_seq=n_s, window=w, **kw)
+            assert errors(got, want)[0] <= 5e-3
+        # position 0: one key, the output is that key's V row for every head
+        k1, v1 = synth.kv_rows_f32(cfg, 0, np.array([0]))
+        kv.append_f32(1, 0, k1, v1)
+        q = synth.qk_rows(cfg, 0, 0, np.array([0]), 8)
+        say("case single key")
+        got = kv.attend(1, q, pos0=0, **kw)
+        vb = nh.bf16_to_f32(nh.bf16_round(v1)).reshape(2, 128)
+        assert np.array_equal(got.reshape(8, 128), np.repeat(vb, 4, axis=0))
+        say("case empty span")
+        got = kv.attend(1, q, pos0=10, n_seq=5, window=3, **kw)
+        assert np.all(got == 0.0)
+
+
+# ---- prefill ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("key,layer,n_seq,chunk", [
+    ("D", 0, 4096, 512),    # Qwen3-4B: the last 512-token chunk of a 4096 prompt
+    ("D", 1, 512, 512),     # the first chunk: the causal triangle only
+    ("C", 0, 6144, 2048),   # Gemma-3-1B local layer: ring 2560, window 512
+    ("C", 5, 4096, 2048),   # Gemma-3-1B global layer
+    ("E", 0, 3072, 1024),   # Gemma-3-4B local layer: ring 2048, window 1024, g = 2
+    ("B", 0, 700, 300),     # Llama shape, hd 64, a ragged chunk
+])
+def test_prefill_parity(orc, key, layer, n_seq, chunk):
+    cfg = synth.CONFIGS[key]
+    got, want = run_case(orc, cfg, layer, n_seq=n_seq, pos0=n_seq - chunk, n_tok=chunk, n_batch=chunk)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= cfg.tol, (key, layer, ea)
+
+
+def test_prefill_odd_batches(orc):
+    """Batches of 2, 5 and 37 tokens (rows that do not fill a tile), and a
+    bidirectional batch (the embedding path's spans) with and without a window."""
+    cfg = synth.CONFIGS["D"]
+    for n_tok in (2, 5, 37):
+        got, want = run_case(orc, cfg, 3, n_seq=900, pos0=900 - n_tok, n_tok=n_tok)
+        assert errors(got, want)[0] <= cfg.tol, n_tok
+    ecfg = synth.AttnConfig(8, "embed", 4, 1, 256, 1)
+    for w in (0, 128):
+        n = 300
+        K, V = synth.cache_buffer(ecfg, 0, n, n)
+        q = synth.qk_rows(ecfg, 0, 0, np.arange(n), 4)
+        kw = dict(window=w, causal=False, n_head=4, n_kv=1, head_dim=256, scale=1 / 16)
+        say(f"case bidirectional window {w}")
+        with nh.KVCache([n], [256]) as kv:
+            kv.append(0, 0, K, V)
+            got = kv.attend(0, q, pos0=0, n_seq=n, **kw)
+        want = orc.attend_layer(q, K, V, kv_bf16=True, rows=n, pos0=0, n_seq=n, **kw)
+        assert errors(got, want)[0] <= 5e-3, w
+
+
+def test_f32_batch_uses_exact_path(orc):
+    """F32 K/V batches run the split-K kernel per token: the F32 bound holds."""
+    cfg = synth.CONFIGS["A"]
+    got, want = run_case(orc, cfg, 2, n_seq=1024, pos0=1000, n_tok=24)
+    assert errors(got, want)[0] <= 1e-3
+
+
+# ---- append, fill, errors ---------------------------------------------------------------
+
+def test_append_rounds_like_nnc_and_wraps():
+    rng = np.random.default_rng(11)
+    rows, kv_dim = 256, 64
+    with nh.KVCache([rows], [kv_dim], bf16=True) as kv:
+        k = rng.standard_normal((40, kv_dim)).astype(np.float32) * 3
+        v = rng.standard_normal((40, kv_dim)).astype(np.float32)
+        k[0, :4] = np.array([0x3F808000, 0x3F818000, 0x7F800000, 0x80000000], np.uint32).view(np.float32)
+        say("case append_f32 with a wrap at row 256")
+        kv.append_f32(0, 230, k, v)  # positions 230..269: rows 230..255 then 0..13
+        K, V = kv.read(0, 0, rows)
+        idx = np.arange(230, 270) % rows
+        assert np.array_equal(K[idx], nh.bf16_round(k)) and np.array_equal(V[idx], nh.bf16_round(v))
+        kb, vb = nh.bf16_round(k * 2), nh.bf16_round(v * 2)
+        kv.append(0, 250, kb, vb)  # raw BF16 rows, wrapping too
+        K, V = kv.read(0, 0, rows)
+        idx = np.arange(250, 290) % rows
+        assert np.array_equal(K[idx], kb) and np.array_equal(V[idx], vb)
+    with nh.KVCache([64], [64], bf16=False) as kv:
+        kv.append_f32(0, 3, k[:10], v[:10])
+        K, _ = kv.read(0, 3, 10)
+        assert np.array_equal(K, k[:10])
+
+
+def test_device_fill_matches_host_generator():
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    n = 1 << 16
+    ptr = C.c_void_p()
+    assert hip.hipMalloc(C.byref(ptr), C.c_size_t(n * 4)) == 0
+    try:
+        out = np.empty(n, dtype=np.float32)
+        for norm in (0, 128):
+            say(f"case fill_normal norm_dim {norm}")
+            nh.fill_normal(ptr.value, n, 777, norm, False)
+            assert hip.hipDeviceSynchronize() == 0
+            assert hip.hipMemcpy(C.c_void_p(out.ctypes.data), ptr, C.c_size_t(n * 4), 2) == 0
+            want = synth.normal(777, n)
+            if norm:
+                want = synth.rmsnorm_heads(want.reshape(1, -1), norm).reshape(-1)
+            assert np.allclose(out, want, rtol=1e-5, atol=1e-5)
+    finally:
+        hip.hipFree(ptr)
+
+
+def test_device_errors_map_to_nnc_statuses():
+    with nh.KVCache([300], [1024]) as kv:
+        cases = [
+            (dict(pos0=300, n_seq=301, n_head=32, n_kv=8, head_dim=128), nh.NncStatus.CONTEXT_FULL),
+            (dict(pos0=0, n_head=30, n_kv=8, head_dim=128), nh.NncStatus.INVALID_ARGUMENT),
+            (dict(pos0=0, n_head=32, n_kv=4, head_dim=128), nh.NncStatus.INVALID_ARGUMENT),
+            (dict(pos0=0, n_head=64, n_kv=2, head_dim=512), nh.NncStatus.UNSUPPORTED_MODEL),
+            (dict(pos0=-1, n_head=32, n_kv=8, head_dim=128), nh.NncStatus.INVALID_ARGUMENT),
+        ]
+        for kw, status in cases:
+            q = np.zeros((1, kw["n_head"] * kw["head_dim"]), dtype=np.float32)
+            with pytest.raises(nh.NncError) as e:
+                kv.attend(0, q, scale=0.1, **kw)
+            assert e.value.status == status, kw
+        q = np.zeros((1, 4096), dtype=np.float32)
+        with pytest.raises(nh.NncError) as e:
+            kv.attend(1, q, pos0=0, n_head=32, n_kv=8, head_dim=128, scale=0.1)
+        assert e.value.status == nh.NncStatus.INVALID_ARGUMENT
+        with pytest.raises(nh.NncError):
+            kv.append(0, 0, np.zeros((301, 1024), np.uint16), np.zeros((301, 1024), np.uint16))
