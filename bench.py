@@ -1,0 +1,262 @@
+"""Benchmark of nnc's attention hot path on one MI355X, at the Qwen3-4B shape
+(32 query heads, 8 KV heads, head_dim 128, 36 layers, BF16 K/V).
+
+A decode step is one query token through the attention of all 36 layers at
+32768 cached positions, each layer reading its own K/V buffer (36 x 128 MiB,
+so the working set is far past the 256 MB Infinity Cache). A prefill step is
+a 4096-token prompt through all 36 layers in 512-token chunks (8 calls per
+layer, chunk c attending to keys 0 .. 512c + 511). Inputs are synthetic and
+resident in HBM before timing: K/V/Q ~ N(0,1) from the splitmix64 +
+Box-Muller generator, Q and K RMS-normalised per head as Qwen3 does.
+
+Prints one JSON line. `value` is decode K/V bytes per second (the algorithmic
+2 * S * n_kv * head_dim * 2 + 2 * n_head * head_dim * 4 bytes per layer);
+prefill TFLOP/s (4 * head_dim * n_head * sum of span lengths) rides in
+`prefill`. `roofline` is the decode kernel's (HBM bound),
+`prefill.roofline` the prefill kernel's (MFMA bound, dense fp16/bf16 peak),
+both from HIP events on the op's stream. `cpu_baseline` times nnc's own CPU
+attention (oracle/_ref: the reference's kernels and worker pool) on a bounded
+sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
+ATTR_CU, ATTR_CLOCK = 63, 5  # hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeClockRate
+
+N_HEAD, N_KV, HD, N_LAYER = 32, 8, 128, 36
+KV_DIM = N_KV * HD
+CTX = 32768
+PROMPT, CHUNK = 4096, 512
+SCALE = 1.0 / np.sqrt(HD)
+
+
+def decode_bytes(span: int) -> int:
+    return 2 * span * KV_DIM * 2 + 2 * N_HEAD * HD * 4
+
+
+def prefill_flops(pos0: int, n_tok: int) -> int:
+    spans = np.arange(pos0 + 1, pos0 + n_tok + 1, dtype=np.int64)  # causal: key 0 .. pos
+    return int(4 * HD * N_HEAD * spans.sum())
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(kv, target_s: float) -> dict:
+    """nnc's CPU attention on this host: one Qwen3-4B layer at 32768 keys,
+    repeated for about target_s seconds (threads = min(8, nproc), the
+    reference default)."""
+    import oracle
+
+    K, V = kv.read(0, 0, CTX)
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, N_HEAD * HD)).astype(np.float32)
+    q /= np.sqrt((q.reshape(N_HEAD, HD) ** 2).mean(axis=1)).repeat(HD)[None, :]
+    nproc = os.cpu_count() or 1
+    threads = min(8, nproc)
+    kw = dict(kv_bf16=True, rows=CTX, pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+    if oracle.reference_available():
+        lib = oracle.Reference()
+        lib.set_threads(threads)
+        kind = "reference"
+        run = lambda: lib.attend_layer(q, K, V, **kw)  # noqa: E731
+    else:
+        lib = oracle.Oracle()
+        kind = "port"
+        run = lambda: lib.attend_layer(q, K, V, threads=threads, **kw)  # noqa: E731
+    run()
+    n, t0 = 0, time.perf_counter()
+    best = float("inf")
+    while time.perf_counter() - t0 < target_s:
+        t = time.perf_counter()
+        run()
+        best = min(best, time.perf_counter() - t)
+        n += 1
+    gbs = decode_bytes(CTX) / best / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"decode of one Qwen3-4B layer at {CTX} keys, best of {n} runs over {target_s:.0f} s "
+                      f"(nproc {nproc}; the reference's kernels and worker pool)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prefill-steps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill"], default=None,
+                    help="time one mode only (profiling runs); the JSON line needs both")
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
+                    help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
+              "multi-GPU path; see DESIGN.md for how the op would shard)", file=sys.stderr)
+        return 2
+
+    import libllmcpu_amd as nh
+    from libllmcpu_amd import hip_rt
+
+    if hip_rt.device_count() < 1:
+        print("no HIP device", file=sys.stderr)
+        return 1
+    n_cu = hip_rt.attribute(ATTR_CU)
+    clock_mhz = hip_rt.attribute(ATTR_CLOCK) / 1000.0
+
+    log(f"[bench] allocating {N_LAYER} x {CTX}-row K/V buffers")
+    kv = nh.KVCache([CTX] * N_LAYER, [KV_DIM] * N_LAYER, bf16=True)
+    stream = kv.stream
+    lib = nh.load_library()
+    import ctypes as C
+
+    for li in range(N_LAYER):
+        # The cache's own buffers are filled through the device generator:
+        # positions 0..CTX-1 of K (RMS-normed per head) and V, as appended.
+        k_dev = hip_rt.malloc(CTX * KV_DIM * 4)
+        v_dev = hip_rt.malloc(CTX * KV_DIM * 4)
+        nh.fill_normal(k_dev, CTX * KV_DIM, (1234 + 3000 + li) * 256 + 1, HD, False, stream)
+        nh.fill_normal(v_dev, CTX * KV_DIM, (1234 + 3000 + li) * 256 + 2, 0, False, stream)
+        st = lib.nnc_hip_kv_append_f32_device(kv.handle, li, 0, CTX, C.c_void_p(k_dev), C.c_void_p(v_dev))
+        if st:
+            raise nh.NncError(st, lib.nnc_hip_last_error().decode())
+        kv.sync()
+        hip_rt.free(k_dev)
+        hip_rt.free(v_dev)
+    q_dec = hip_rt.malloc(N_LAYER * N_HEAD * HD * 4)
+    o_dec = hip_rt.malloc(N_LAYER * N_HEAD * HD * 4)
+    q_pre = hip_rt.malloc(N_LAYER * PROMPT * N_HEAD * HD * 4)
+    o_pre = hip_rt.malloc(PROMPT * N_HEAD * HD * 4)
+    for li in range(N_LAYER):
+        nh.fill_normal(q_dec + li * N_HEAD * HD * 4, N_HEAD * HD, (1234 + 3000 + li) * 256, HD, False, stream)
+        nh.fill_normal(q_pre + li * PROMPT * N_HEAD * HD * 4, PROMPT * N_HEAD * HD, (1234 + 3000 + li) * 256 + 3, HD,
+                       False, stream)
+    kv.sync()
+
+    def decode_step():
+        for li in range(N_LAYER):
+            kv.attend_device(li, q_dec + li * N_HEAD * HD * 4, o_dec + li * N_HEAD * HD * 4, n_tok=1, pos0=CTX - 1,
+                             n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+
+    def prefill_step():
+        for li in range(N_LAYER):
+            qb = q_pre + li * PROMPT * N_HEAD * HD * 4
+            for c in range(PROMPT // CHUNK):
+                kv.attend_device(li, qb + c * CHUNK * N_HEAD * HD * 4, o_pre + c * CHUNK * N_HEAD * HD * 4,
+                                 n_tok=CHUNK, pos0=c * CHUNK, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+
+    def timed(step, n):
+        e0, e1 = hip_rt.Event(), hip_rt.Event()
+        hip_rt.sync()
+        w0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(n):
+            step()
+        e1.record(stream)
+        e1.synchronize()
+        hip_rt.sync()
+        return e1.ms_since(e0), (time.perf_counter() - w0) * 1e3
+
+    if args.only == "prefill":
+        prefill_step()
+        hip_rt.sync()
+        pre_ms, _ = timed(prefill_step, args.prefill_steps)
+        log(f"[bench] prefill {pre_ms / args.prefill_steps:.3f} ms/step")
+        return 0
+    log(f"[bench] decode warmup {args.warmup}")
+    for _ in range(args.warmup):
+        decode_step()
+    hip_rt.sync()
+    log(f"[bench] decode timed {args.steps} steps")
+    dec_ms, dec_wall = timed(decode_step, args.steps)
+    if args.only == "decode":
+        log(f"[bench] decode {dec_ms / args.steps:.4f} ms/step")
+        return 0
+    dec_step_ms = dec_ms / args.steps
+    dec_bytes = N_LAYER * decode_bytes(CTX)
+    dec_gbs = dec_bytes / (dec_step_ms * 1e-3) / 1e9
+    dec_launch_us = dec_ms * 1e3 / (args.steps * N_LAYER)
+    dec_launch_gbs = decode_bytes(CTX) / (dec_launch_us * 1e-6) / 1e9
+
+    log("[bench] prefill warmup 1")
+    prefill_step()
+    hip_rt.sync()
+    log(f"[bench] prefill timed {args.prefill_steps} steps")
+    pre_ms, pre_wall = timed(prefill_step, args.prefill_steps)
+    pre_step_ms = pre_ms / args.prefill_steps
+    pre_flops = N_LAYER * sum(prefill_flops(c * CHUNK, CHUNK) for c in range(PROMPT // CHUNK))
+    pre_tflops = pre_flops / (pre_step_ms * 1e-3) / 1e12
+    pre_launches = N_LAYER * (PROMPT // CHUNK)
+    pre_launch_us = pre_ms * 1e3 / (args.prefill_steps * pre_launches)
+    pre_launch_tflops = (pre_flops / pre_launches) / (pre_launch_us * 1e-6) / 1e12
+
+    traffic = None
+    tp = Path(args.traffic)
+    if tp.exists():
+        try:
+            traffic = json.loads(tp.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, AttributeError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ~{args.cpu_seconds:.0f} s")
+        cpu = cpu_baseline(kv, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "qwen3-4b attention decode, 32768 cached keys, 36 layers (one token per step)",
+                   "n_head": N_HEAD, "n_kv": N_KV, "head_dim": HD, "layers": N_LAYER, "context": CTX,
+                   "kv_dtype": "bf16", "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(dec_launch_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_launch_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "decode_kernel<128,4,bf16>", "avg_launch_us": round(dec_launch_us, 3),
+                     "bytes_per_launch": decode_bytes(CTX)},
+        "prefill": {"metric": "prefill-attn TFLOP/s", "value": round(pre_tflops, 1), "unit": "TFLOP/s",
+                    "ms_per_step": round(pre_step_ms, 3), "steps": args.prefill_steps,
+                    "workload": f"qwen3-4b prefill of {PROMPT} tokens in {CHUNK}-token chunks, 36 layers",
+                    "roofline": {"bound": "mfma", "achieved": round(pre_launch_tflops, 1),
+                                 "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                                 "kernel": "prefill_kernel<128,4,2> (fp16 MFMA, fp32 accumulate)",
+                                 "avg_launch_us": round(pre_launch_us, 3)}},
+        "cpu_baseline": cpu,
+        "device": {"cu": n_cu, "clock_mhz": clock_mhz},
+        "wall_ms": {"decode": round(dec_wall, 2), "prefill": round(pre_wall, 2)},
+    }
+    print(json.dumps(line), flush=True)
+    kv.close()
+    for p in (q_dec, o_dec, q_pre, o_pre):
+        hip_rt.free(p)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -17,19 +17,23 @@
 //            one V row and reads that key's weights for all heads of the
 //            group from LDS, so each V element is loaded once for the group.
 // The four wavefront partials merge in LDS; the work-group's partial
-// (o, m, l per head) goes to global scratch; the last work-group of a KV head
-// to arrive (an atomic counter, reset by that work-group) merges all splits
-// in split order and writes o / l (0 when l == 0, reference nn_ops.cpp:492).
-// The merge order is fixed, so results do not depend on arrival order.
+// (o, m, l per head) goes to global scratch, and a second small kernel merges
+// the splits of each KV head in split order and writes o / l (0 when l == 0,
+// reference nn_ops.cpp:492). The order is fixed, so results are the same run
+// to run. (A single-kernel "last work-group merges" scheme needs a device-
+// scope release fence in every work-group, which on this multi-XCD part
+// writes back and invalidates the XCD's L2 each time: measured 5x slower.)
 #include "device_common.h"
 #include "kernels.h"
+
+#include <cstdlib>
+#include <type_traits>
 
 namespace nnchip
 {
 	namespace
 	{
-		constexpr int kWaves = 4;
-		constexpr int kThreads = 64 * kWaves;
+		constexpr int kMergeThreads = 256;
 
 		template <int HD, bool BF16>
 		struct decode_shape
@@ -41,7 +45,6 @@ namespace nnchip
 			static constexpr int LPK = HD / VEC; // lanes per key in the V layout
 			static constexpr int KPL = 64 / LPK; // keys per V load
 			static constexpr int NV = CH / KPL; // V loads per chunk
-			static constexpr int WGK = kWaves * CH; // keys per work-group iteration
 			static_assert(NT >= 1 && KK >= 1 && LPK <= 64 && NV >= 1, "unsupported decode shape");
 		};
 
@@ -54,9 +57,60 @@ namespace nnchip
 			return r >= rows ? r - rows : r;
 		}
 
-		template <int HD, int G, bool BF16>
-		__global__ __launch_bounds__(kThreads) void decode_kernel(const decode_params p)
+		// Orders one wavefront's LDS writes before its own later reads of
+		// other lanes' values (LDS executes a wavefront's operations in order;
+		// this keeps the compiler from moving them).
+		__device__ __forceinline__ void wave_sync()
 		{
+			__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+			__builtin_amdgcn_wave_barrier();
+			__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+		}
+
+		// The work-group's result from its wavefronts' partials in s_wpart
+		// (o[head_dim], m, l per head, per wavefront), merged in wavefront
+		// order: a partial for the split merge, or, with a single split, o / l.
+		template <int HD, int G, int W>
+		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[G][HD + 2],
+		                                                size_t slot, int split, float* out)
+		{
+			constexpr int PW = HD + 2, kWaves = W, kThreads = 64 * W;
+			const int kvh = blockIdx.y;
+			const bool single = p.n_split == 1;
+			float* gpart = p.part + (slot * p.n_split + split) * G * PW;
+			for (int idx = threadIdx.x; idx < G * PW; idx += kThreads)
+			{
+				const int h = idx / PW, d = idx % PW;
+				float m = -INFINITY;
+#pragma unroll
+				for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_wpart[w][h][HD]);
+				const float m_use = m == -INFINITY ? 0.0f : m;
+				if (d == HD)
+				{
+					if (!single) gpart[idx] = m;
+					continue;
+				}
+				float r = 0.0f;
+#pragma unroll
+				for (int w = 0; w < kWaves; ++w)
+					r = fmaf(s_wpart[w][h][d], fast_exp2(s_wpart[w][h][HD] - m_use), r);
+				if (!single)
+					gpart[idx] = r;
+				else if (d < HD)
+				{
+					float l = 0.0f;
+#pragma unroll
+					for (int w = 0; w < kWaves; ++w)
+						l = fmaf(s_wpart[w][h][HD + 1], fast_exp2(s_wpart[w][h][HD] - m_use), l);
+					out[static_cast<size_t>(kvh * G + h) * HD + d] = l > 0.0f ? r / l : 0.0f;
+				}
+			}
+		}
+
+		template <int HD, int G, bool BF16, int W>
+		__global__ __launch_bounds__(64 * W) void decode_kernel(const decode_params p)
+		{
+			constexpr int kWaves = W, kThreads = 64 * W;
 			using S = decode_shape<HD, BF16>;
 			constexpr int CH = S::CH, NT = S::NT, KK = S::KK, VEC = S::VEC, LPK = S::LPK, KPL = S::KPL, NV = S::NV;
 			constexpr int PW = HD + 2;
@@ -64,12 +118,9 @@ namespace nnchip
 			__shared__ float s_p[kWaves][CH][16]; // weights: [wave][key][head]
 			__shared__ float s_alpha[kWaves][16];
 			__shared__ float s_wpart[kWaves][G][PW];
-			__shared__ float s_w[256 * G]; // final merge: per (split, head) weight
-			__shared__ float s_l[G];
-			__shared__ int s_last;
 
 			const int lane = threadIdx.x & 63;
-			const int wave = threadIdx.x >> 6;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
 			const int col = lane & 15; // head within the group (MFMA N column)
 			const int grp = lane >> 4; // lane group (MFMA K slice / D row quad)
 			const int kvh = blockIdx.y;
@@ -88,6 +139,76 @@ namespace nnchip
 			float* out = p.out + static_cast<size_t>(tok) * p.n_head * HD;
 			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh; // (token, KV head)
 
+			float m_run = -INFINITY; // per column (head), log2 units
+			float l_run = 0.0f; // this lane's share of the column's sum
+			float o[G][VEC];
+#pragma unroll
+			for (int h = 0; h < G; ++h)
+#pragma unroll
+				for (int e = 0; e < VEC; ++e) o[h][e] = 0.0f;
+
+			// This wavefront's chunks: CH keys each, every kWaves-th chunk of the
+			// split that meets [s0, s1]. Software-pipelined: the V rows of chunk
+			// j load during its scores, the K rows of chunk j + 1 during its P.V.
+			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
+			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
+			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
+
+			uint4 kreg[NT][KK][BF16 ? 1 : 2];
+			uint4 vreg[NV];
+			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
+			{
+				cbase = sbase + c * CH;
+				clo = max(s0, cbase);
+				chi = min(s1, cbase + CH - 1);
+				rb = clo % p.rows;
+			};
+			auto load_k = [&](int cbase, int clo, int chi, int rb) __attribute__((always_inline))
+			{
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+				{
+					const int k = min(max(cbase + 16 * t + col, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					if constexpr (BF16)
+					{
+						const uint16_t* kp = static_cast<const uint16_t*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
+#pragma unroll
+						for (int kk = 0; kk < KK; ++kk) kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
+					}
+					else
+					{
+						const float* kp = static_cast<const float*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
+#pragma unroll
+						for (int kk = 0; kk < KK; ++kk)
+						{
+							kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
+							kreg[t][kk][1] = *reinterpret_cast<const uint4*>(kp + 32 * kk + 4);
+						}
+					}
+				}
+			};
+			auto load_v = [&](int cbase, int clo, int chi, int rb) __attribute__((always_inline))
+			{
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+				{
+					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					const char* vp = static_cast<const char*>(p.V) +
+					                 (row * p.kv_dim + head_off + VEC * (lane % LPK)) * (BF16 ? 2 : 4);
+					vreg[j] = *reinterpret_cast<const uint4*>(vp);
+				}
+			};
+
+			if (c_wave <= c_last)
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(c_wave, cbase, clo, chi, rb);
+				load_k(cbase, clo, chi, rb);
+			}
+
+			// (The first K rows are in flight while Q is prepared.)
 			// Q^T as the MFMA B operand: column col = head kvh*G + col, rows
 			// 32*kk + 8*grp + j of head_dim; scaled into log2 units, split.
 			bf16x8 qhi[KK], qlo[KK];
@@ -113,167 +234,122 @@ namespace nnchip
 				split_bf16x8(x, qhi[kk], qlo[kk]);
 			}
 
-			float m_run = -INFINITY; // per column (head), log2 units
-			float l_run = 0.0f; // this lane's share of the column's sum
-			float o[G][VEC];
-#pragma unroll
-			for (int h = 0; h < G; ++h)
-#pragma unroll
-				for (int e = 0; e < VEC; ++e) o[h][e] = 0.0f;
-
-			const int n_it = p.split_keys / S::WGK;
-			for (int it = 0; it < n_it; ++it)
+			for (; c_wave <= c_last; c_wave += kWaves)
 			{
-				const int wg_base = sbase + it * S::WGK;
-				if (wg_base > s1 || wg_base + S::WGK - 1 < s0) continue; // uniform over the work-group
-				const int cbase = wg_base + wave * CH;
-				const int clo = max(s0, cbase), chi = min(s1, cbase + CH - 1);
-				const bool active = clo <= chi; // uniform over the wave
-				const int rb = active ? clo % p.rows : 0;
+				int cbase, clo, chi, rb;
+				chunk_bounds(c_wave, cbase, clo, chi, rb);
+				load_v(cbase, clo, chi, rb);
 
-				uint4 kreg[NT][KK][BF16 ? 1 : 2];
-				uint4 vreg[NV];
-				if (active)
-				{
+				// Scores of the chunk's keys.
+				f32x4 acc[NT];
 #pragma unroll
-					for (int t = 0; t < NT; ++t)
+				for (int t = 0; t < NT; ++t)
+				{
+					acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk)
 					{
-						const int k = min(max(cbase + 16 * t + col, clo), chi);
-						const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
 						if constexpr (BF16)
 						{
-							const uint16_t* kp = static_cast<const uint16_t*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
-#pragma unroll
-							for (int kk = 0; kk < KK; ++kk) kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
+							const bf16x8 a = as_bf16x8(kreg[t][kk][0]);
+							acc[t] = mfma16x16x32(a, qhi[kk], acc[t]);
+							acc[t] = mfma16x16x32(a, qlo[kk], acc[t]);
 						}
 						else
 						{
-							const float* kp = static_cast<const float*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
+							float x[8];
+							const float* f0 = reinterpret_cast<const float*>(&kreg[t][kk][0]);
+							const float* f1 = reinterpret_cast<const float*>(&kreg[t][kk][1]);
 #pragma unroll
-							for (int kk = 0; kk < KK; ++kk)
+							for (int j = 0; j < 4; ++j)
 							{
-								kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
-								kreg[t][kk][1] = *reinterpret_cast<const uint4*>(kp + 32 * kk + 4);
+								x[j] = f0[j];
+								x[4 + j] = f1[j];
 							}
+							bf16x8 khi, klo;
+							split_bf16x8(x, khi, klo);
+							acc[t] = mfma16x16x32(khi, qhi[kk], acc[t]);
+							acc[t] = mfma16x16x32(khi, qlo[kk], acc[t]);
+							acc[t] = mfma16x16x32(klo, qhi[kk], acc[t]);
 						}
 					}
-#pragma unroll
-					for (int j = 0; j < NV; ++j)
-					{
-						const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
-						const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
-						const char* vp = static_cast<const char*>(p.V) +
-						                 (row * p.kv_dim + head_off + VEC * (lane % LPK)) * (BF16 ? 2 : 4);
-						vreg[j] = *reinterpret_cast<const uint4*>(vp);
-					}
-
-					// Scores of the chunk's keys.
-					f32x4 acc[NT];
-#pragma unroll
-					for (int t = 0; t < NT; ++t)
-					{
-						acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-						for (int kk = 0; kk < KK; ++kk)
-						{
-							if constexpr (BF16)
-							{
-								const bf16x8 a = as_bf16x8(kreg[t][kk][0]);
-								acc[t] = mfma16x16x32(a, qhi[kk], acc[t]);
-								acc[t] = mfma16x16x32(a, qlo[kk], acc[t]);
-							}
-							else
-							{
-								float x[8];
-								const float* f0 = reinterpret_cast<const float*>(&kreg[t][kk][0]);
-								const float* f1 = reinterpret_cast<const float*>(&kreg[t][kk][1]);
-#pragma unroll
-								for (int j = 0; j < 4; ++j)
-								{
-									x[j] = f0[j];
-									x[4 + j] = f1[j];
-								}
-								bf16x8 khi, klo;
-								split_bf16x8(x, khi, klo);
-								acc[t] = mfma16x16x32(khi, qhi[kk], acc[t]);
-								acc[t] = mfma16x16x32(khi, qlo[kk], acc[t]);
-								acc[t] = mfma16x16x32(klo, qhi[kk], acc[t]);
-							}
-						}
-					}
-
-					// Chunk max per head, masked keys at -inf.
-					float m_loc = -INFINITY;
-#pragma unroll
-					for (int t = 0; t < NT; ++t)
-#pragma unroll
-						for (int i = 0; i < 4; ++i)
-						{
-							const int k = cbase + 16 * t + 4 * grp + i;
-							const float s = (k >= clo && k <= chi) ? acc[t][i] : -INFINITY;
-							acc[t][i] = s;
-							m_loc = fmaxf(m_loc, s);
-						}
-					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
-					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
-					const float m_new = fmaxf(m_run, m_loc);
-					const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-					const float alpha = fast_exp2(m_run - m_use);
-					m_run = m_new;
-					float lsum = 0.0f;
-#pragma unroll
-					for (int t = 0; t < NT; ++t)
-#pragma unroll
-						for (int i = 0; i < 4; ++i)
-						{
-							const float w = fast_exp2(acc[t][i] - m_use);
-							lsum += w;
-							s_p[wave][16 * t + 4 * grp + i][col] = w;
-						}
-					l_run = l_run * alpha + lsum;
-					if (lane < 16) s_alpha[wave][lane] = alpha;
 				}
-				__syncthreads();
-				if (active)
+				if (c_wave + kWaves <= c_last)
 				{
+					int nb, nlo, nhi, nrb;
+					chunk_bounds(c_wave + kWaves, nb, nlo, nhi, nrb);
+					load_k(nb, nlo, nhi, nrb);
+				}
+
+				// Chunk max per head, masked keys at -inf.
+				float m_loc = -INFINITY;
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int i = 0; i < 4; ++i)
+					{
+						const int k = cbase + 16 * t + 4 * grp + i;
+						const float sc = (k >= clo && k <= chi) ? acc[t][i] : -INFINITY;
+						acc[t][i] = sc;
+						m_loc = fmaxf(m_loc, sc);
+					}
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
+				const float m_new = fmaxf(m_run, m_loc);
+				const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+				const float alpha = fast_exp2(m_run - m_use);
+				m_run = m_new;
+				float lsum = 0.0f;
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int i = 0; i < 4; ++i)
+					{
+						const float w = fast_exp2(acc[t][i] - m_use);
+						lsum += w;
+						s_p[wave][16 * t + 4 * grp + i][col] = w;
+					}
+				l_run = l_run * alpha + lsum;
+				if (lane < 16) s_alpha[wave][lane] = alpha;
+				wave_sync();
+
+#pragma unroll
+				for (int h = 0; h < G; ++h)
+				{
+					const float a = s_alpha[wave][h];
+#pragma unroll
+					for (int e = 0; e < VEC; ++e) o[h][e] *= a;
+				}
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+				{
+					const int kl = j * KPL + lane / LPK;
+					float w[G];
+#pragma unroll
+					for (int h = 0; h < G; ++h) w[h] = s_p[wave][kl][h];
+					float v[VEC];
+					if constexpr (BF16)
+					{
+						const uint32_t* d = reinterpret_cast<const uint32_t*>(&vreg[j]);
+#pragma unroll
+						for (int u = 0; u < 4; ++u)
+						{
+							v[2 * u] = bf16_lo(d[u]);
+							v[2 * u + 1] = bf16_hi(d[u]);
+						}
+					}
+					else
+					{
+						const float* f = reinterpret_cast<const float*>(&vreg[j]);
+#pragma unroll
+						for (int u = 0; u < 4; ++u) v[u] = f[u];
+					}
 #pragma unroll
 					for (int h = 0; h < G; ++h)
-					{
-						const float a = s_alpha[wave][h];
 #pragma unroll
-						for (int e = 0; e < VEC; ++e) o[h][e] *= a;
-					}
-#pragma unroll
-					for (int j = 0; j < NV; ++j)
-					{
-						const int kl = j * KPL + lane / LPK;
-						float w[G];
-#pragma unroll
-						for (int h = 0; h < G; ++h) w[h] = s_p[wave][kl][h];
-						float v[VEC];
-						if constexpr (BF16)
-						{
-							const uint32_t* d = reinterpret_cast<const uint32_t*>(&vreg[j]);
-#pragma unroll
-							for (int u = 0; u < 4; ++u)
-							{
-								v[2 * u] = bf16_lo(d[u]);
-								v[2 * u + 1] = bf16_hi(d[u]);
-							}
-						}
-						else
-						{
-							const float* f = reinterpret_cast<const float*>(&vreg[j]);
-#pragma unroll
-							for (int u = 0; u < 4; ++u) v[u] = f[u];
-						}
-#pragma unroll
-						for (int h = 0; h < G; ++h)
-#pragma unroll
-							for (int e = 0; e < VEC; ++e) o[h][e] = fmaf(w[h], v[e], o[h][e]);
-					}
+						for (int e = 0; e < VEC; ++e) o[h][e] = fmaf(w[h], v[e], o[h][e]);
 				}
-				__syncthreads();
+				wave_sync(); // the weights are read before the next chunk overwrites them
 			}
 
 			// Wave partial: sum the key slots of o, the lane groups of l.
@@ -299,106 +375,442 @@ namespace nnchip
 			}
 			__syncthreads();
 
-			// Work-group partial, waves merged in order.
-			float* gpart = p.part + (slot * p.n_split + split) * G * PW;
-			for (int idx = threadIdx.x; idx < G * PW; idx += kThreads)
+			write_wg_result<HD, G, W>(p, s_wpart, slot, split, out);
+		}
+
+		// Chunk sizes of the BF16 kernel: CH keys per wavefront chunk, so that a
+		// chunk's K and V rows are 64 VGPRs each.
+		template <int HD>
+		struct bf16_shape
+		{
+			static constexpr int CH = HD == 256 ? 32 : 64;
+			static constexpr int NT = CH / 16; // 16-key MFMA tiles
+			static constexpr int NC = CH / 32; // 32-key P.V MFMA steps
+			static constexpr int KK = HD / 32;
+			static constexpr int DB = HD / 16; // 16-row d blocks of O^T
+			static constexpr int LPK = HD / 8; // lanes per V row
+			static constexpr int KPL = 64 / LPK; // V rows per load
+			static constexpr int NV = CH / KPL; // V loads per chunk
+			// LDS pitch of a V row, in bf16: 8 dwords past a multiple of 64 banks,
+			// so the four rows one 16-lane group reads with ds_read_b64_tr_b16 sit
+			// in disjoint banks (measured: a pitch of head_dim + 8 conflicts).
+			static constexpr int VPITCH = HD <= 128 ? 144 : 272;
+			static_assert(NC >= 1 && NV >= 1, "unsupported decode shape");
+		};
+
+		// Two bf16 halves of one row of O^T's A operand: lane (g, c) of the
+		// ds_read_b64_tr_b16 gives V[key0 + 4g + k][d0 + c], k = 0..3, when lane
+		// c of each 16-lane group points at V[key0 + 4g + c / 4][d0 + 4 (c % 4)]
+		// (the transpose works within 16-lane groups: result element k of lane
+		// c comes from lane 4k + c / 4, element c % 4).
+		__device__ __forceinline__ u32x2 vt_read(const uint16_t* row_ptr)
+		{
+			typedef short s16x4 __attribute__((ext_vector_type(4)));
+			typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+			const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(row_ptr));
+			return __builtin_bit_cast(u32x2, v);
+		}
+
+		// BF16 K/V: both products on MFMA.
+		//   S^T = K . Q^T     as in decode_kernel (Q split into bf16 hi + lo).
+		//   O^T += V^T . P^T  v_mfma_f32_16x16x32_bf16. P^T comes straight from
+		//                     the registers that hold S^T: two 16-key tiles give
+		//                     a lane the 8 weights it supplies as B operand, keys
+		//                     32c + 16h + 4g + k in k-slot 8g + 4h + k. V rows go
+		//                     to a per-wavefront LDS tile as loaded, and the A
+		//                     operand (V^T) is read back with ds_read_b64_tr_b16
+		//                     in that same key order. P is split into bf16 hi + lo,
+		//                     so both products are near-fp32 against the exact
+		//                     bf16 K and V. O^T's columns are the heads, so the
+		//                     online-softmax rescale stays in the lane.
+		// Loads run one chunk ahead: a chunk's K registers are reissued as soon
+		// as its scores are done, its V registers as soon as they are in LDS.
+		template <int HD, int G, int W>
+		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_kernel(
+			const decode_params p)
+		{
+			using S = bf16_shape<HD>;
+			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
+			              NV = S::NV, VPITCH = S::VPITCH;
+			constexpr int PW = HD + 2, kWaves = W;
+
+			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
+			__shared__ float s_wpart[W][G][PW];
+
+			const int lane = threadIdx.x & 63;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
+			const int col = lane & 15;
+			const int grp = lane >> 4;
+			const int kvh = blockIdx.y;
+			const int split = blockIdx.x;
+			const int tok = blockIdx.z;
+			const int n_kv = gridDim.y;
+
+			int first, last;
+			attn_span(p.causal, p.window, p.pos0 + tok, p.n_seq, first, last);
+			const int sbase = p.split_base + split * p.split_keys;
+			const int s0 = max(first, sbase);
+			const int s1 = min(last, sbase + p.split_keys - 1);
+			const size_t head_off = static_cast<size_t>(kvh) * HD;
+			const float* q = p.q + static_cast<size_t>(tok) * p.n_head * HD;
+			float* out = p.out + static_cast<size_t>(tok) * p.n_head * HD;
+			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh;
+			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
+			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
+			uint16_t* vt = s_v[wave];
+
+			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
+			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
+			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
+			const bool has_chunk = c_wave <= c_last; // uniform over the wavefront
+			const int n_wchunks = has_chunk ? (c_last - c_wave) / kWaves + 1 : 0;
+			const int c_wlast = c_wave + (n_wchunks - 1) * kWaves;
+
+			u32x4 kA[NT][KK], kB[NT][KK]; // two chunks in flight: A holds even, B odd chunks
+			u32x4 vA[NV], vB[NV];
+			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
 			{
-				const int h = idx / PW, d = idx % PW;
-				float m = -INFINITY;
+				cbase = sbase + c * CH;
+				clo = max(s0, cbase);
+				chi = min(s1, cbase + CH - 1);
+				rb = clo % p.rows;
+			};
+			// Loads are never under a branch (a conditional load makes the
+			// compiler wait for it, or move the buffer out of registers, where
+			// the paths join): a chunk index past the wavefront's last chunk is
+			// clamped to it, which re-reads rows that are still in L2.
+			auto load_k = [&](int c, u32x4 (&kreg)[NT][KK]) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
 #pragma unroll
-				for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_wpart[w][h][HD]);
-				const float m_use = m == -INFINITY ? 0.0f : m;
-				float r;
-				if (d == HD)
-					r = m;
+				for (int t = 0; t < NT; ++t)
+				{
+					const int k = min(max(cbase + 16 * t + col, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					const uint16_t* kp = Kg + row * p.kv_dim + 8 * grp;
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk) kreg[t][kk] = *reinterpret_cast<const u32x4*>(kp + 32 * kk);
+				}
+			};
+			// Load j: key j * KPL + lane / LPK, elements 8 * (lane % LPK) .. + 8.
+			auto load_v = [&](int c, u32x4 (&vreg)[NV]) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+				{
+					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					vreg[j] = *reinterpret_cast<const u32x4*>(Vg + row * p.kv_dim + 8 * (lane % LPK));
+				}
+			};
+
+			if (has_chunk)
+			{
+				load_k(c_wave, kA);
+				load_v(c_wave, vA);
+				load_k(c_wave + kWaves, kB);
+				load_v(c_wave + kWaves, vB);
+			}
+
+			// (The first K and V rows are in flight while Q is prepared.) Q^T as
+			// the B operand, scaled into log2 units and split into bf16 hi + lo.
+			bf16x8 qhi[KK], qlo[KK];
+#pragma unroll
+			for (int kk = 0; kk < KK; ++kk)
+			{
+				float x[8];
+				if (col < G)
+				{
+					const float* qp = q + static_cast<size_t>(kvh * G + col) * HD + 32 * kk + 8 * grp;
+					const float4 a = *reinterpret_cast<const float4*>(qp);
+					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
+					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+					x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+					for (int j = 0; j < 8; ++j) x[j] *= p.qscale;
+				}
 				else
 				{
-					r = 0.0f;
 #pragma unroll
-					for (int w = 0; w < kWaves; ++w)
+					for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+				}
+				split_bf16x8(x, qhi[kk], qlo[kk]);
+			}
+
+			float m_run = -INFINITY, l_run = 0.0f;
+			f32x4 acc_o[DB];
+#pragma unroll
+			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+			// One chunk from buffers (kreg, vreg); the chunk two ahead is loaded
+			// into them as soon as they are consumed. A chunk past the
+			// wavefront's last one has no valid key (clo > chi) and adds nothing.
+			auto chunk = [&](int cw, u32x4 (&kreg)[NT][KK], u32x4 (&vreg)[NV]) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(cw, cbase, clo, chi, rb);
+
+				f32x4 sc[NT];
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+				{
+					sc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk)
 					{
-						const float f = fast_exp2(s_wpart[w][h][HD] - m_use);
-						r = fmaf(s_wpart[w][h][d], f, r);
+						const bf16x8 a = as_bf16x8(kreg[t][kk]);
+						sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
+						sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
 					}
 				}
-				gpart[idx] = r;
+				load_k(cw + 2 * kWaves, kreg);
+
+				// This chunk's V rows into the wavefront's LDS tile, then the next
+				// chunk's V loads into the freed registers.
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
+				load_v(cw + 2 * kWaves, vreg);
+
+				// Online softmax per head (column).
+				float m_loc = -INFINITY;
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int i = 0; i < 4; ++i)
+					{
+						const int k = cbase + 16 * t + 4 * grp + i;
+						const float v = (k >= clo && k <= chi) ? sc[t][i] : -INFINITY;
+						sc[t][i] = v;
+						m_loc = fmaxf(m_loc, v);
+					}
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
+				const float m_new = fmaxf(m_run, m_loc);
+				const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+				const float alpha = fast_exp2(m_run - m_use);
+				m_run = m_new;
+				float lsum = 0.0f;
+				bf16x8 phi[NC], plo[NC];
+#pragma unroll
+				for (int c = 0; c < NC; ++c)
+				{
+					float w[8];
+#pragma unroll
+					for (int i = 0; i < 4; ++i)
+					{
+						w[i] = fast_exp2(sc[2 * c][i] - m_use);
+						w[4 + i] = fast_exp2(sc[2 * c + 1][i] - m_use);
+					}
+#pragma unroll
+					for (int i = 0; i < 8; ++i) lsum += w[i];
+					split_bf16x8(w, phi[c], plo[c]);
+				}
+				l_run = l_run * alpha + lsum;
+#pragma unroll
+				for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
+
+				wave_sync();
+#pragma unroll
+				for (int c = 0; c < NC; ++c)
+#pragma unroll
+					for (int db = 0; db < DB; ++db)
+					{
+						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
+						const u32x2 lo = vt_read(r0);
+						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
+						const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+						acc_o[db] = mfma16x16x32(a, phi[c], acc_o[db]);
+						acc_o[db] = mfma16x16x32(a, plo[c], acc_o[db]);
+					}
+				wave_sync(); // V is read before the next chunk overwrites it
+			};
+			for (int i = 0; i < n_wchunks; i += 2, c_wave += 2 * kWaves)
+			{
+				chunk(c_wave, kA, vA);
+				chunk(c_wave + kWaves, kB, vB);
 			}
 
-			// The last work-group of this KV head merges every split.
-			__threadfence();
-			__syncthreads();
-			if (threadIdx.x == 0)
+			// Wavefront partial: each (head, d) of O^T has one owner lane.
+			l_run += __shfl_xor(l_run, 16);
+			l_run += __shfl_xor(l_run, 32);
+			if (col < G)
 			{
-				const unsigned prev = atomicAdd(p.count + slot, 1u);
-				s_last = prev == static_cast<unsigned>(p.n_split - 1);
+#pragma unroll
+				for (int db = 0; db < DB; ++db)
+#pragma unroll
+					for (int i = 0; i < 4; ++i) s_wpart[wave][col][16 * db + 4 * grp + i] = acc_o[db][i];
+				if (grp == 0)
+				{
+					s_wpart[wave][col][HD] = m_run;
+					s_wpart[wave][col][HD + 1] = l_run;
+				}
 			}
 			__syncthreads();
-			if (!s_last) return;
-			__threadfence();
+			write_wg_result<HD, G, W>(p, s_wpart, slot, split, out);
+		}
 
-			const float* kpart = p.part + slot * p.n_split * G * PW;
-			for (int idx = threadIdx.x; idx < p.n_split * G; idx += kThreads)
-				s_w[idx] = kpart[static_cast<size_t>(idx) * PW + HD];
-			__syncthreads();
-			if (threadIdx.x < G)
+		// Merges the n_split partials of one (token, query head) in a fixed
+		// order and writes o / l (0 when l == 0, reference nn_ops.cpp:492).
+		// Grid: (n_kv * G, n_tok). Each thread issues all of its loads before
+		// using them: one (m, l) pair per split, then one float4 of o for every
+		// J-th split of its quad.
+		template <int HD, int G>
+		__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const decode_params p)
+		{
+			constexpr int kThreads = kMergeThreads;
+			constexpr int PW = HD + 2;
+			constexpr int QN = HD / 4; // output quads of one head
+			constexpr int J = kThreads / QN; // threads per quad
+			constexpr int MAXS = 256; // splits
+			__shared__ float s_f[MAXS];
+			__shared__ float s_red[kThreads / 64];
+			__shared__ float4 s_acc[kThreads];
+
+			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
+			const int n_kv = gridDim.x / G;
+			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh;
+			const float* hp = p.part + (slot * p.n_split * G + h) * PW; // split s at hp + s * G * PW
+			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+			const int q = threadIdx.x % QN, j = threadIdx.x / QN;
+
+			// One round of loads: this thread's (m, l) and the first 8 of its o quads.
+			auto load_batch = [&](int s0, float4* v) __attribute__((always_inline))
 			{
-				const int h = threadIdx.x;
-				float m = -INFINITY;
-				for (int s = 0; s < p.n_split; ++s) m = fmaxf(m, s_w[s * G + h]);
-				const float m_use = m == -INFINITY ? 0.0f : m;
-				float l = 0.0f;
-				for (int s = 0; s < p.n_split; ++s)
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
 				{
-					const float f = fast_exp2(s_w[s * G + h] - m_use);
-					l = fmaf(kpart[(static_cast<size_t>(s) * G + h) * PW + HD + 1], f, l);
-					s_w[s * G + h] = f;
+					const int sp = s0 + u * J;
+					v[u] = sp < p.n_split ? *reinterpret_cast<const float4*>(hp + static_cast<size_t>(sp) * G * PW + 4 * q)
+					                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 				}
-				s_l[h] = l;
-			}
-			__syncthreads();
-			for (int idx = threadIdx.x; idx < G * HD / 4; idx += kThreads)
+			};
+			float4 v[8];
+			load_batch(j, v);
+			float m = -INFINITY, l = 0.0f;
+			if (threadIdx.x < p.n_split)
 			{
-				const int h = idx / (HD / 4), d = 4 * (idx % (HD / 4));
-				float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-				for (int s = 0; s < p.n_split; ++s)
-				{
-					const float f = s_w[s * G + h];
-					const float4 v = *reinterpret_cast<const float4*>(kpart + (static_cast<size_t>(s) * G + h) * PW + d);
-					acc.x = fmaf(v.x, f, acc.x);
-					acc.y = fmaf(v.y, f, acc.y);
-					acc.z = fmaf(v.z, f, acc.z);
-					acc.w = fmaf(v.w, f, acc.w);
-				}
-				const float l = s_l[h];
-				const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-				float* op = out + static_cast<size_t>(kvh * G + h) * HD + d;
-				*reinterpret_cast<float4*>(op) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+				const float* sp = hp + static_cast<size_t>(threadIdx.x) * G * PW;
+				m = sp[HD];
+				l = sp[HD + 1];
 			}
-			if (threadIdx.x == 0) p.count[slot] = 0u;
+			float mx = m;
+#pragma unroll
+			for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+			if (lane == 0) s_red[wave] = mx;
+			__syncthreads();
+			mx = s_red[0];
+#pragma unroll
+			for (int w = 1; w < kThreads / 64; ++w) mx = fmaxf(mx, s_red[w]);
+			const float m_use = mx == -INFINITY ? 0.0f : mx;
+			const float f = threadIdx.x < p.n_split ? fast_exp2(m - m_use) : 0.0f;
+			s_f[threadIdx.x] = f;
+			float lw = l * f;
+#pragma unroll
+			for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off);
+			__syncthreads();
+			if (lane == 0) s_red[wave] = lw;
+			__syncthreads();
+			float L = s_red[0];
+#pragma unroll
+			for (int w = 1; w < kThreads / 64; ++w) L += s_red[w];
+
+			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+			for (int s0 = j;; s0 += 8 * J)
+			{
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
+				{
+					const int sp = s0 + u * J;
+					const float fw = sp < p.n_split ? s_f[sp] : 0.0f;
+					acc.x = fmaf(v[u].x, fw, acc.x);
+					acc.y = fmaf(v[u].y, fw, acc.y);
+					acc.z = fmaf(v[u].z, fw, acc.z);
+					acc.w = fmaf(v[u].w, fw, acc.w);
+				}
+				if (s0 + 8 * J >= p.n_split) break;
+				load_batch(s0 + 8 * J, v);
+			}
+			s_acc[threadIdx.x] = acc;
+			__syncthreads();
+			if (threadIdx.x < QN)
+			{
+				float4 r = s_acc[threadIdx.x];
+#pragma unroll
+				for (int jj = 1; jj < J; ++jj)
+				{
+					const float4 w4 = s_acc[jj * QN + threadIdx.x];
+					r.x += w4.x;
+					r.y += w4.y;
+					r.z += w4.z;
+					r.w += w4.w;
+				}
+				const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+				float* op = p.out + static_cast<size_t>(tok) * p.n_head * HD + static_cast<size_t>(kvh * G + h) * HD + 4 * threadIdx.x;
+				*reinterpret_cast<float4*>(op) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+			}
+		}
+
+		// NNC_HIP_DECODE_KERNEL=valu runs BF16 caches through the VALU P.V
+		// kernel instead of the MFMA one (for comparison).
+		bool decode_valu_pv()
+		{
+			static const bool v = []
+			{
+				const char* e = std::getenv("NNC_HIP_DECODE_KERNEL");
+				return e && e[0] == 'v';
+			}();
+			return v;
+		}
+
+		template <int HD, int G, bool BF16>
+		void launch_g(const decode_params& p, int n_kv, int n_tok, int waves, hipStream_t stream)
+		{
+			const dim3 grid(p.n_split, n_kv, n_tok);
+			if (BF16 && !decode_valu_pv())
+				decode_bf16_kernel<HD, G, 4><<<grid, 256, 0, stream>>>(p);
+			else if (waves == 8)
+				decode_kernel<HD, G, BF16, 8><<<grid, 512, 0, stream>>>(p);
+			else
+				decode_kernel<HD, G, BF16, 4><<<grid, 256, 0, stream>>>(p);
+			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(n_kv * G, n_tok), kMergeThreads, 0, stream>>>(p);
 		}
 
 		template <int HD, bool BF16>
-		bool launch_hd(const decode_params& p, int n_kv, int n_tok, int group, hipStream_t stream)
+		bool launch_hd(const decode_params& p, int n_kv, int n_tok, int group, int waves, hipStream_t stream)
 		{
-			const dim3 grid(p.n_split, n_kv, n_tok), block(kThreads);
 			switch (group)
 			{
-			case 1: decode_kernel<HD, 1, BF16><<<grid, block, 0, stream>>>(p); return true;
-			case 2: decode_kernel<HD, 2, BF16><<<grid, block, 0, stream>>>(p); return true;
-			case 4: decode_kernel<HD, 4, BF16><<<grid, block, 0, stream>>>(p); return true;
-			case 8: decode_kernel<HD, 8, BF16><<<grid, block, 0, stream>>>(p); return true;
+			case 1: launch_g<HD, 1, BF16>(p, n_kv, n_tok, waves, stream); return true;
+			case 2: launch_g<HD, 2, BF16>(p, n_kv, n_tok, waves, stream); return true;
+			case 4: launch_g<HD, 4, BF16>(p, n_kv, n_tok, waves, stream); return true;
+			case 8: launch_g<HD, 8, BF16>(p, n_kv, n_tok, waves, stream); return true;
 			default: return false;
 			}
 		}
+
+	}
+
+	int decode_waves()
+	{
+		static const int w = []
+		{
+			const char* e = std::getenv("NNC_HIP_DECODE_WAVES"); // 4 or 8, for tuning
+			return (e && std::atoi(e) == 8) ? 8 : 4;
+		}();
+		return w;
 	}
 
 	int decode_wg_keys(int head_dim, bool bf16)
 	{
 		switch (head_dim)
 		{
-		case 64: return bf16 ? decode_shape<64, true>::WGK : decode_shape<64, false>::WGK;
-		case 128: return bf16 ? decode_shape<128, true>::WGK : decode_shape<128, false>::WGK;
-		case 256: return bf16 ? decode_shape<256, true>::WGK : decode_shape<256, false>::WGK;
+		case 64: return (bf16 && !decode_valu_pv()) ? bf16_shape<64>::CH * 4 : (bf16 ? decode_shape<64, true>::CH : decode_shape<64, false>::CH) * decode_waves();
+		case 128: return (bf16 && !decode_valu_pv()) ? bf16_shape<128>::CH * 4 : (bf16 ? decode_shape<128, true>::CH : decode_shape<128, false>::CH) * decode_waves();
+		case 256: return (bf16 && !decode_valu_pv()) ? bf16_shape<256>::CH * 4 : (bf16 ? decode_shape<256, true>::CH : decode_shape<256, false>::CH) * decode_waves();
 		default: return 0;
 		}
 	}
@@ -406,17 +818,18 @@ namespace nnchip
 	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
 	                   hipStream_t stream)
 	{
+		const int w = decode_waves();
 		switch (head_dim)
 		{
 		case 64:
-			return bf16 ? launch_hd<64, true>(p, n_kv, n_tok, group, stream)
-			            : launch_hd<64, false>(p, n_kv, n_tok, group, stream);
+			return bf16 ? launch_hd<64, true>(p, n_kv, n_tok, group, w, stream)
+			            : launch_hd<64, false>(p, n_kv, n_tok, group, w, stream);
 		case 128:
-			return bf16 ? launch_hd<128, true>(p, n_kv, n_tok, group, stream)
-			            : launch_hd<128, false>(p, n_kv, n_tok, group, stream);
+			return bf16 ? launch_hd<128, true>(p, n_kv, n_tok, group, w, stream)
+			            : launch_hd<128, false>(p, n_kv, n_tok, group, w, stream);
 		case 256:
-			return bf16 ? launch_hd<256, true>(p, n_kv, n_tok, group, stream)
-			            : launch_hd<256, false>(p, n_kv, n_tok, group, stream);
+			return bf16 ? launch_hd<256, true>(p, n_kv, n_tok, group, w, stream)
+			            : launch_hd<256, false>(p, n_kv, n_tok, group, w, stream);
 		default: return false;
 		}
 	}

@@ -2,6 +2,12 @@
 // batch path, reference src/libnnc/model.cpp:1750-1757 and the chunked
 // prefill of a long prompt), BF16 K/V.
 //
+// Precision: the MFMAs run in fp16 with fp32 accumulation. BF16 K/V convert
+// to fp16 exactly (8 significant bits fit in 11) for magnitudes up to 65504,
+// beyond which they saturate; Q (scaled) and the softmax weights P in [0, 1]
+// round to fp16, 8x finer than bf16, which keeps the worst case of a
+// first 512-token chunk at Qwen3-4B shape near 1e-3 of nnc's fp32 result.
+//
 // Rows of the problem are (token, query head) pairs of one KV head, token
 // major, so the heads of a GQA group sit in adjacent rows and share every
 // K/V tile a work-group stages. Grid: n_kv * n_qtiles work-groups of 4
@@ -10,7 +16,7 @@
 // last, staging K ([key][d]) and V^T ([d][key], keys permuted to match the
 // register layout of P) in LDS, with the next tile's global loads in flight
 // during the current tile's math:
-//   S^T = K . Q^T      v_mfma_f32_16x16x32_bf16, keys on M, rows on N, so each
+//   S^T = K . Q^T      v_mfma_f32_16x16x32_f16, keys on M, rows on N, so each
 //                      lane ends up owning one row's scores: the row max and
 //                      sum need only two cross-lane steps;
 //   online softmax     in fp32 and log2 units (Q is pre-scaled by
@@ -24,31 +30,35 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <cstdio>
+#include <cstdlib>
+
 namespace nnchip
 {
 	namespace
 	{
-		constexpr int kThreads = 256;
 		constexpr int kBK = 64; // keys per tile
 
-		template <int HD, int G, int NQ>
-		__global__ __launch_bounds__(kThreads) void prefill_kernel(const prefill_params p)
+		// W wavefronts per work-group, each owning 16 * NQ rows.
+		template <int HD, int G, int NQ, int W>
+		__global__ __launch_bounds__(64 * W) void prefill_kernel(const prefill_params p)
 		{
+			constexpr int kThreads = 64 * W;
 			constexpr int KK = HD / 32; // k-steps of the QK MFMA
 			constexpr int DB = HD / 16; // 16-wide d blocks of O^T
-			constexpr int KPAD = HD + 8; // LDS row pitch of K, in bf16
-			constexpr int VPAD = kBK + 8; // LDS row pitch of V^T, in bf16
-			constexpr int ROWS = 64 * NQ; // rows per work-group
+			constexpr int KPAD = HD + 8; // LDS row pitch of K, in fp16
+			constexpr int VPAD = kBK + 8; // LDS row pitch of V^T, in fp16
+			constexpr int ROWS = 16 * NQ * W; // rows per work-group
 			constexpr int KCH = kBK * HD / 8 / kThreads; // 16-byte K chunks per thread per tile
 			constexpr int VUNITS = (kBK / 4) * (HD / 8); // (4 keys x 8 d) units of V per tile
 			constexpr int VUN = (VUNITS + kThreads - 1) / kThreads; // per thread
 			static_assert(KCH >= 1 && KCH * kThreads == kBK * HD / 8, "K tile must split evenly over the work-group");
 
-			__shared__ __attribute__((aligned(16))) uint16_t s_k[kBK * KPAD];
-			__shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * VPAD];
+			__shared__ __attribute__((aligned(16))) uint16_t s_k[kBK * KPAD]; // fp16 bits
+			__shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * VPAD]; // fp16 bits
 
 			const int lane = threadIdx.x & 63;
-			const int wave = threadIdx.x >> 6;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
 			const int col = lane & 15;
 			const int grp = lane >> 4;
 
@@ -96,8 +106,8 @@ namespace nnchip
 			}
 			const bool wave_rows = wrow0 < n_rows;
 
-			// Q^T as the B operand, pre-scaled into log2 units, bf16.
-			bf16x8 qb[NQ][KK];
+			// Q^T as the B operand, pre-scaled into log2 units, fp16.
+			f16x8 qb[NQ][KK];
 #pragma unroll
 			for (int nb = 0; nb < NQ; ++nb)
 			{
@@ -113,12 +123,12 @@ namespace nnchip
 						const float4 a = *reinterpret_cast<const float4*>(qp + 32 * kk + 8 * grp);
 						const float4 b = *reinterpret_cast<const float4*>(qp + 32 * kk + 8 * grp + 4);
 						const float s = p.qscale;
-						w.x = pack_bf16x2(a.x * s, a.y * s);
-						w.y = pack_bf16x2(a.z * s, a.w * s);
-						w.z = pack_bf16x2(b.x * s, b.y * s);
-						w.w = pack_bf16x2(b.z * s, b.w * s);
+						w.x = pack_f16x2(a.x * s, a.y * s);
+						w.y = pack_f16x2(a.z * s, a.w * s);
+						w.z = pack_f16x2(b.x * s, b.y * s);
+						w.w = pack_f16x2(b.z * s, b.w * s);
 					}
-					qb[nb][kk] = as_bf16x8(w);
+					qb[nb][kk] = as_f16x8(w);
 				}
 			}
 
@@ -141,13 +151,13 @@ namespace nnchip
 
 			uint4 kreg[KCH];
 			uint4 vreg[VUN][4];
-			auto load_tile = [&](int kb)
+			auto load_tile = [&](int kb) __attribute__((always_inline))
 			{
 				// [lo, hi] is never longer than the buffer (checked on the host), so
 				// the offset from lo wraps a ring at most once.
 				const int lo = max(kb, kmin), hi = min(kb + kBK - 1, kmax);
 				const int rb = lo % p.rows;
-				auto row_of = [&](int k) -> size_t
+				auto row_of = [&](int k) __attribute__((always_inline)) -> size_t
 				{
 					const int kc = min(max(k, lo), hi);
 					int r = rb + (kc - lo);
@@ -172,14 +182,20 @@ namespace nnchip
 						vreg[u][j] = *reinterpret_cast<const uint4*>(Vg + row_of(kb + 4 * quad + j) * p.kv_dim + 8 * dg);
 				}
 			};
-			auto store_tile = [&]()
+			auto store_tile = [&]() __attribute__((always_inline))
 			{
 #pragma unroll
 				for (int u = 0; u < KCH; ++u)
 				{
 					const int c = threadIdx.x + kThreads * u;
 					const int key = c / (HD / 8), d8 = c % (HD / 8);
-					*reinterpret_cast<uint4*>(s_k + key * KPAD + 8 * d8) = kreg[u];
+					const uint4 b = kreg[u];
+					uint4 h;
+					h.x = pack_f16x2_rtz(bf16_lo(b.x), bf16_hi(b.x));
+					h.y = pack_f16x2_rtz(bf16_lo(b.y), bf16_hi(b.y));
+					h.z = pack_f16x2_rtz(bf16_lo(b.z), bf16_hi(b.z));
+					h.w = pack_f16x2_rtz(bf16_lo(b.w), bf16_hi(b.w));
+					*reinterpret_cast<uint4*>(s_k + key * KPAD + 8 * d8) = h;
 				}
 #pragma unroll
 				for (int u = 0; u < VUN; ++u)
@@ -198,10 +214,10 @@ namespace nnchip
 					for (int e = 0; e < 4; ++e)
 					{
 						uint2 lo, hi;
-						lo.x = (w0[e] & 0xffffu) | (w1[e] << 16);
-						lo.y = (w2[e] & 0xffffu) | (w3[e] << 16);
-						hi.x = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-						hi.y = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
+						lo.x = pack_f16x2_rtz(bf16_lo(w0[e]), bf16_lo(w1[e]));
+						lo.y = pack_f16x2_rtz(bf16_lo(w2[e]), bf16_lo(w3[e]));
+						hi.x = pack_f16x2_rtz(bf16_hi(w0[e]), bf16_hi(w1[e]));
+						hi.y = pack_f16x2_rtz(bf16_hi(w2[e]), bf16_hi(w3[e]));
 						*reinterpret_cast<uint2*>(s_vt + (8 * dg + 2 * e) * VPAD + pos) = lo;
 						*reinterpret_cast<uint2*>(s_vt + (8 * dg + 2 * e + 1) * VPAD + pos) = hi;
 					}
@@ -230,7 +246,7 @@ namespace nnchip
 #pragma unroll
 					for (int mb = 0; mb < 4; ++mb)
 					{
-						const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(s_k + (16 * mb + col) * KPAD + 32 * kk + 8 * grp));
+						const f16x8 a = as_f16x8(*reinterpret_cast<const uint4*>(s_k + (16 * mb + col) * KPAD + 32 * kk + 8 * grp));
 #pragma unroll
 						for (int nb = 0; nb < NQ; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][kk], s[mb][nb]);
 					}
@@ -249,7 +265,7 @@ namespace nnchip
 						}
 				}
 
-				bf16x8 pb[2][NQ];
+				f16x8 pb[2][NQ];
 #pragma unroll
 				for (int nb = 0; nb < NQ; ++nb)
 				{
@@ -281,11 +297,11 @@ namespace nnchip
 					for (int c = 0; c < 2; ++c)
 					{
 						uint4 w;
-						w.x = pack_bf16x2(pw[2 * c][0], pw[2 * c][1]);
-						w.y = pack_bf16x2(pw[2 * c][2], pw[2 * c][3]);
-						w.z = pack_bf16x2(pw[2 * c + 1][0], pw[2 * c + 1][1]);
-						w.w = pack_bf16x2(pw[2 * c + 1][2], pw[2 * c + 1][3]);
-						pb[c][nb] = as_bf16x8(w);
+						w.x = pack_f16x2(pw[2 * c][0], pw[2 * c][1]);
+						w.y = pack_f16x2(pw[2 * c][2], pw[2 * c][3]);
+						w.z = pack_f16x2(pw[2 * c + 1][0], pw[2 * c + 1][1]);
+						w.w = pack_f16x2(pw[2 * c + 1][2], pw[2 * c + 1][3]);
+						pb[c][nb] = as_f16x8(w);
 					}
 				}
 
@@ -294,7 +310,7 @@ namespace nnchip
 #pragma unroll
 					for (int db = 0; db < DB; ++db)
 					{
-						const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(s_vt + (16 * db + col) * VPAD + 32 * c + 8 * grp));
+						const f16x8 a = as_f16x8(*reinterpret_cast<const uint4*>(s_vt + (16 * db + col) * VPAD + 32 * c + 8 * grp));
 #pragma unroll
 						for (int nb = 0; nb < NQ; ++nb) acc_o[db][nb] = mfma16x16x32(a, pb[c][nb], acc_o[db][nb]);
 					}
@@ -320,35 +336,53 @@ namespace nnchip
 			}
 		}
 
-		template <int HD, int NQ>
+		template <int HD, int NQ, int W>
 		bool launch_g(const prefill_params& p, int group, hipStream_t stream)
 		{
-			const dim3 grid(p.n_qtiles * p.n_kv), block(kThreads);
+			const dim3 grid(p.n_qtiles * p.n_kv), block(64 * W);
 			switch (group)
 			{
-			case 1: prefill_kernel<HD, 1, NQ><<<grid, block, 0, stream>>>(p); return true;
-			case 2: prefill_kernel<HD, 2, NQ><<<grid, block, 0, stream>>>(p); return true;
-			case 4: prefill_kernel<HD, 4, NQ><<<grid, block, 0, stream>>>(p); return true;
-			case 8: prefill_kernel<HD, 8, NQ><<<grid, block, 0, stream>>>(p); return true;
+			case 1: prefill_kernel<HD, 1, NQ, W><<<grid, block, 0, stream>>>(p); return true;
+			case 2: prefill_kernel<HD, 2, NQ, W><<<grid, block, 0, stream>>>(p); return true;
+			case 4: prefill_kernel<HD, 4, NQ, W><<<grid, block, 0, stream>>>(p); return true;
+			case 8: prefill_kernel<HD, 8, NQ, W><<<grid, block, 0, stream>>>(p); return true;
 			default: return false;
+			}
+		}
+
+		// Tile shape (wavefronts per work-group, 16-row blocks per wavefront):
+		// NNC_HIP_PREFILL_TILE="W,NQ" overrides the default, for tuning.
+		void tile_shape(int head_dim, int& w, int& nq)
+		{
+			w = 4;
+			nq = head_dim == 256 ? 1 : 2;
+			if (const char* e = std::getenv("NNC_HIP_PREFILL_TILE"))
+			{
+				int a = 0, b = 0;
+				if (std::sscanf(e, "%d,%d", &a, &b) == 2 && (a == 2 || a == 4) && (b == 1 || b == 2)) w = a, nq = b;
 			}
 		}
 	}
 
-	int prefill_tile_rows(int head_dim, int group)
-	{
-		(void)group;
-		return head_dim == 256 ? 64 : 128;
-	}
-
-	bool launch_prefill(const prefill_params& p, int head_dim, int group, bool bf16, hipStream_t stream)
+	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream)
 	{
 		if (!bf16) return false;
-		switch (head_dim)
+		int w, nq;
+		tile_shape(head_dim, w, nq);
+		const int rows = 16 * nq * w;
+		p.n_qtiles = (p.n_tok * group + rows - 1) / rows;
+		switch (head_dim * 100 + w * 10 + nq)
 		{
-		case 64: return launch_g<64, 2>(p, group, stream);
-		case 128: return launch_g<128, 2>(p, group, stream);
-		case 256: return launch_g<256, 1>(p, group, stream);
+		case 6421: return launch_g<64, 1, 2>(p, group, stream);
+		case 6422: return launch_g<64, 2, 2>(p, group, stream);
+		case 6441: return launch_g<64, 1, 4>(p, group, stream);
+		case 6442: return launch_g<64, 2, 4>(p, group, stream);
+		case 12821: return launch_g<128, 1, 2>(p, group, stream);
+		case 12822: return launch_g<128, 2, 2>(p, group, stream);
+		case 12841: return launch_g<128, 1, 4>(p, group, stream);
+		case 12842: return launch_g<128, 2, 4>(p, group, stream);
+		case 25621: return launch_g<256, 1, 2>(p, group, stream);
+		case 25641: return launch_g<256, 1, 4>(p, group, stream);
 		default: return false;
 		}
 	}

@@ -12,13 +12,43 @@ namespace nnchip
 	//   A: lane l holds A[l % 16][8 * (l / 16) + j], j = 0..7   (M x K = 16 x 32)
 	//   B: lane l holds B[8 * (l / 16) + j][l % 16]              (K x N = 32 x 16)
 	//   D: lane l holds D[4 * (l / 16) + i][l % 16], i = 0..3    (M x N = 16 x 16)
+	// v_mfma_f32_16x16x32_f16 has the same operand layout.
 	typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-	typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+	typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+	typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 	typedef float f32x4 __attribute__((ext_vector_type(4)));
+	// 16 bytes as a native vector: register buffers of this type stay in
+	// registers (arrays of HIP's uint4 struct can end up in scratch or LDS).
+	typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+	typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 	__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c)
 	{
 		return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+	}
+
+	__device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c)
+	{
+		return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+	}
+
+	__device__ __forceinline__ f16x8 as_f16x8(const uint4& v) { return __builtin_bit_cast(f16x8, v); }
+	__device__ __forceinline__ f16x8 as_f16x8(const u32x4& v) { return __builtin_bit_cast(f16x8, v); }
+
+	// Two fp32 -> packed fp16, rounded to nearest even.
+	__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi)
+	{
+		const f16x2 h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+		return __builtin_bit_cast(uint32_t, h);
+	}
+
+	// Two bf16 values (as fp32) -> packed fp16 with round-toward-zero: exact
+	// for magnitudes in fp16's normal range (a bf16 significand has 8 bits,
+	// fp16's 11); larger magnitudes saturate at +-65504 instead of becoming
+	// infinities, and magnitudes below 2^-14 keep 2^-24 absolute precision.
+	__device__ __forceinline__ uint32_t pack_f16x2_rtz(float lo, float hi)
+	{
+		return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 	}
 
 	// nnc's BF16 contract (reference runtime.h:97-113): widen by a 16-bit
@@ -41,6 +71,7 @@ namespace nnchip
 	}
 
 	__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
+	__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
 	// Splits 8 fp32 values into bf16 hi + lo parts with x ~= hi + lo to about
 	// 16 significant bits, so two bf16 MFMAs give a near-fp32 product against

@@ -17,7 +17,6 @@ namespace nnchip
 		const void* K; // [rows][kv_dim], BF16 bits or F32
 		const void* V;
 		float* part; // [n_tok][n_kv][n_split][group][head_dim + 2]: o, then m (log2 units), then l
-		unsigned* count; // [n_tok][n_kv] arrival counters, zero between launches
 		int rows, kv_dim, n_head;
 		int pos0, n_seq, window, causal; // token t sits at pos0 + t
 		int split_base; // first key of split 0, a multiple of split_keys
@@ -30,8 +29,9 @@ namespace nnchip
 	// element type; split_keys must be a multiple of it.
 	int decode_wg_keys(int head_dim, bool bf16);
 
-	// Launches the decode kernel over an (n_split, n_kv, n_tok) grid; returns
-	// false when (head_dim, group, bf16) has no instantiation.
+	// Launches the decode kernel over an (n_split, n_kv, n_tok) grid, then
+	// (n_split > 1) the split merge over (n_kv, n_tok); returns false when
+	// (head_dim, group, bf16) has no instantiation.
 	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
 	                   hipStream_t stream);
 
@@ -45,14 +45,11 @@ namespace nnchip
 		int rows, kv_dim, n_head, n_kv;
 		int n_tok, pos0, n_seq, window;
 		int causal;
-		int n_qtiles; // query tiles per KV head
+		int n_qtiles; // query tiles per KV head (set by launch_prefill)
 		float qscale; // scale * log2(e)
 	};
 
-	// Query rows ((token, head) pairs of one KV head) per prefill work-group.
-	int prefill_tile_rows(int head_dim, int group);
-
-	bool launch_prefill(const prefill_params& p, int head_dim, int group, bool bf16, hipStream_t stream);
+	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream);
 
 	// F32 rows -> the cache's element type, row (pos0 + t) % rows.
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,

@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -84,7 +85,6 @@ struct nnc_hip_kv
 	std::vector<kv_buffer> bufs;
 	uint64_t bytes = 0;
 	dev_scratch part; // decode partials
-	dev_scratch count; // decode arrival counters (kept zero between launches)
 	dev_scratch q; // staging of host q / out / append rows
 	dev_scratch out;
 	dev_scratch rows_k;
@@ -102,15 +102,14 @@ namespace
 			if (b.k) (void)hipFree(b.k);
 			if (b.v) (void)hipFree(b.v);
 		}
-		for (dev_scratch* s : {&kv->part, &kv->count, &kv->q, &kv->out, &kv->rows_k, &kv->rows_v})
+		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
 		delete kv;
 	}
 
-	// Makes s at least `bytes` long. A new allocation is zeroed on the stream
-	// (the decode counters rely on it); the old one is freed after the stream
-	// has drained.
+	// Makes s at least `bytes` long; the old allocation is freed after the
+	// stream has drained.
 	nnc_status reserve(nnc_hip_kv* kv, dev_scratch& s, size_t bytes, const char* what)
 	{
 		if (s.bytes >= bytes) return NNC_OK;
@@ -121,7 +120,6 @@ namespace
 		const size_t n = (std::max<size_t>(bytes, 256) + 255) & ~static_cast<size_t>(255);
 		NNC_HIP_TRY(hipMalloc(&s.ptr, n), what);
 		s.bytes = n;
-		NNC_HIP_TRY(hipMemsetAsync(s.ptr, 0, n, kv->stream), what);
 		return NNC_OK;
 	}
 
@@ -188,6 +186,8 @@ namespace
 		const long long pairs = static_cast<long long>(n_tok) * n_kv;
 		const long long want = std::max<long long>(1, 2LL * kv->n_cu / std::max<long long>(pairs, 1));
 		long long sk = (span + want - 1) / want;
+		if (const char* e = std::getenv("NNC_HIP_DECODE_SPLIT")) // keys per work-group, for tuning
+			if (std::atoll(e) > 0) sk = std::atoll(e);
 		sk = std::max<long long>(wgk, (sk + wgk - 1) / wgk * wgk);
 		while ((kmax / sk) - (kmin / sk) + 1 > kMaxSplits) sk += wgk;
 		const int split_keys = static_cast<int>(sk);
@@ -196,8 +196,6 @@ namespace
 
 		const size_t part_floats = static_cast<size_t>(pairs) * n_split * group * (head_dim + 2);
 		if (nnc_status s = reserve(kv, kv->part, part_floats * sizeof(float), "decode scratch")) return s;
-		if (nnc_status s = reserve(kv, kv->count, static_cast<size_t>(pairs) * sizeof(unsigned), "decode counters"))
-			return s;
 
 		nnchip::decode_params p{};
 		p.q = q;
@@ -205,7 +203,6 @@ namespace
 		p.K = b.k;
 		p.V = b.v;
 		p.part = static_cast<float*>(kv->part.ptr);
-		p.count = static_cast<unsigned*>(kv->count.ptr);
 		p.rows = b.rows;
 		p.kv_dim = b.kv_dim;
 		p.n_head = n_head;
@@ -258,8 +255,6 @@ namespace
 			p.n_seq = n_seq;
 			p.window = window;
 			p.causal = causal ? 1 : 0;
-			const int tile = nnchip::prefill_tile_rows(head_dim, group);
-			p.n_qtiles = (n_tok * group + tile - 1) / tile;
 			p.qscale = scale * 1.4426950408889634f;
 			if (!nnchip::launch_prefill(p, head_dim, group, bf16, kv->stream))
 				return fail(NNC_ERR_UNSUPPORTED_MODEL, "no prefill kernel for head_dim %d, group %d", head_dim, group);
