@@ -2,10 +2,10 @@
 // attention core, reference src/libnnc/model.cpp:1731-1749, whose unit of
 // work is a (KV head, 256-key block) pair).
 //
-// Grid: (n_split, n_kv). A work-group of 4 wavefronts owns one KV head and
-// one absolute-aligned range of split_keys keys of the query's span; each
-// wavefront streams chunks of CH keys (CH * head_dim * 2 bytes of K and the
-// same of V per chunk, all loads issued before any use):
+// Grid: (n_split, n_kv, n_tok). A work-group of 4 wavefronts owns one KV head
+// and one absolute-aligned range of split_keys keys of the query's span; each
+// wavefront streams chunks of CH keys, the next chunk's K and V loads in
+// flight while the current one is computed:
 //   scores   S^T[key][head] = K . Q^T on MFMA (v_mfma_f32_16x16x32_bf16): the
 //            16 keys of a tile are the M rows, loaded straight from HBM in
 //            the A-operand layout (16 contiguous bytes per lane); the group's
@@ -13,16 +13,21 @@
 //            halves, so the product against the exact bf16 K is near-fp32;
 //   softmax  per head (column): the chunk max over keys, exp2 of the
 //            log2-scaled scores, a running (m, l) with the usual rescale;
-//   P.V      on the VALU in fp32: each lane owns 8 consecutive elements of
-//            one V row and reads that key's weights for all heads of the
-//            group from LDS, so each V element is loaded once for the group.
+//   P.V      BF16 caches (decode_bf16_kernel): O^T = V^T . P^T on MFMA. The
+//            chunk's V rows go to the wavefront's LDS tile and come back
+//            transposed (ds_read_b64_tr_b16) as the A operand; P^T, split into
+//            bf16 hi + lo, is the B operand straight from the score registers
+//            (the key order inside a 32-key step is permuted to match).
+//            F32 caches (decode_kernel): on the VALU in fp32, each lane owning
+//            consecutive elements of one V row and reading the key's weights
+//            for all heads of the group from LDS.
 // The four wavefront partials merge in LDS; the work-group's partial
 // (o, m, l per head) goes to global scratch, and a second small kernel merges
 // the splits of each KV head in split order and writes o / l (0 when l == 0,
 // reference nn_ops.cpp:492). The order is fixed, so results are the same run
-// to run. (A single-kernel "last work-group merges" scheme needs a device-
-// scope release fence in every work-group, which on this multi-XCD part
-// writes back and invalidates the XCD's L2 each time: measured 5x slower.)
+// to run. (A single-kernel "last work-group merges" scheme needs an
+// agent-scope release in every work-group, which on this multi-XCD part
+// writes back the XCD's L2: measured 1.7x slower at 32k keys.)
 #include "device_common.h"
 #include "kernels.h"
 
@@ -104,6 +109,105 @@ namespace nnchip
 						l = fmaf(s_wpart[w][h][HD + 1], fast_exp2(s_wpart[w][h][HD] - m_use), l);
 					out[static_cast<size_t>(kvh * G + h) * HD + d] = l > 0.0f ? r / l : 0.0f;
 				}
+			}
+		}
+
+		// Merges the n_split partials of one (token, query head) in a fixed
+		// order and writes o / l (0 when l == 0, reference nn_ops.cpp:492),
+		// with kMergeThreads threads. Each thread issues all of its loads
+		// before using them: one (m, l) pair per split, then one float4 of o
+		// for every J-th split of its quad.
+		template <int HD, int G>
+		__device__ __forceinline__ void merge_splits(const decode_params& p, size_t slot, int tok, int kvh, int h)
+		{
+			constexpr int kThreads = kMergeThreads;
+			constexpr int PW = HD + 2;
+			constexpr int QN = HD / 4; // output quads of one head
+			constexpr int J = kThreads / QN; // threads per quad
+			constexpr int MAXS = 256; // splits
+			__shared__ float s_f[MAXS];
+			__shared__ float s_red[kThreads / 64];
+			__shared__ float4 s_acc[kThreads];
+
+			const float* hp = p.part + (slot * p.n_split * G + h) * PW; // split s at hp + s * G * PW
+			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+			const int q = threadIdx.x % QN, j = threadIdx.x / QN;
+
+			// One round of loads: this thread's (m, l) and the first 8 of its o quads.
+			auto load_batch = [&](int s0, float4* v) __attribute__((always_inline))
+			{
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
+				{
+					const int sp = s0 + u * J;
+					v[u] = sp < p.n_split ? *reinterpret_cast<const float4*>(hp + static_cast<size_t>(sp) * G * PW + 4 * q)
+					                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				}
+			};
+			float4 v[8];
+			load_batch(j, v);
+			float m = -INFINITY, l = 0.0f;
+			if (threadIdx.x < p.n_split)
+			{
+				const float* sp = hp + static_cast<size_t>(threadIdx.x) * G * PW;
+				m = sp[HD];
+				l = sp[HD + 1];
+			}
+			float mx = m;
+#pragma unroll
+			for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+			__syncthreads(); // s_red / s_f / s_acc are free (a previous call may still read them)
+			if (lane == 0) s_red[wave] = mx;
+			__syncthreads();
+			mx = s_red[0];
+#pragma unroll
+			for (int w = 1; w < kThreads / 64; ++w) mx = fmaxf(mx, s_red[w]);
+			const float m_use = mx == -INFINITY ? 0.0f : mx;
+			const float f = threadIdx.x < p.n_split ? fast_exp2(m - m_use) : 0.0f;
+			s_f[threadIdx.x] = f;
+			float lw = l * f;
+#pragma unroll
+			for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off);
+			__syncthreads();
+			if (lane == 0) s_red[wave] = lw;
+			__syncthreads();
+			float L = s_red[0];
+#pragma unroll
+			for (int w = 1; w < kThreads / 64; ++w) L += s_red[w];
+
+			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+			for (int s0 = j;; s0 += 8 * J)
+			{
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
+				{
+					const int sp = s0 + u * J;
+					const float fw = sp < p.n_split ? s_f[sp] : 0.0f;
+					acc.x = fmaf(v[u].x, fw, acc.x);
+					acc.y = fmaf(v[u].y, fw, acc.y);
+					acc.z = fmaf(v[u].z, fw, acc.z);
+					acc.w = fmaf(v[u].w, fw, acc.w);
+				}
+				if (s0 + 8 * J >= p.n_split) break;
+				load_batch(s0 + 8 * J, v);
+			}
+			s_acc[threadIdx.x] = acc;
+			__syncthreads();
+			if (threadIdx.x < QN)
+			{
+				float4 r = s_acc[threadIdx.x];
+#pragma unroll
+				for (int jj = 1; jj < J; ++jj)
+				{
+					const float4 w4 = s_acc[jj * QN + threadIdx.x];
+					r.x += w4.x;
+					r.y += w4.y;
+					r.z += w4.z;
+					r.w += w4.w;
+				}
+				const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+				float* op = p.out + static_cast<size_t>(tok) * p.n_head * HD + static_cast<size_t>(kvh * G + h) * HD + 4 * threadIdx.x;
+				*reinterpret_cast<float4*>(op) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
 			}
 		}
 
@@ -466,8 +570,8 @@ namespace nnchip
 			const int n_wchunks = has_chunk ? (c_last - c_wave) / kWaves + 1 : 0;
 			const int c_wlast = c_wave + (n_wchunks - 1) * kWaves;
 
-			u32x4 kA[NT][KK], kB[NT][KK]; // two chunks in flight: A holds even, B odd chunks
-			u32x4 vA[NV], vB[NV];
+			u32x4 kreg[NT][KK]; // the chunk in flight
+			u32x4 vreg[NV];
 			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
 			{
 				cbase = sbase + c * CH;
@@ -479,7 +583,7 @@ namespace nnchip
 			// compiler wait for it, or move the buffer out of registers, where
 			// the paths join): a chunk index past the wavefront's last chunk is
 			// clamped to it, which re-reads rows that are still in L2.
-			auto load_k = [&](int c, u32x4 (&kreg)[NT][KK]) __attribute__((always_inline))
+			auto load_k = [&](int c) __attribute__((always_inline))
 			{
 				int cbase, clo, chi, rb;
 				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
@@ -494,7 +598,7 @@ namespace nnchip
 				}
 			};
 			// Load j: key j * KPL + lane / LPK, elements 8 * (lane % LPK) .. + 8.
-			auto load_v = [&](int c, u32x4 (&vreg)[NV]) __attribute__((always_inline))
+			auto load_v = [&](int c) __attribute__((always_inline))
 			{
 				int cbase, clo, chi, rb;
 				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
@@ -509,10 +613,8 @@ namespace nnchip
 
 			if (has_chunk)
 			{
-				load_k(c_wave, kA);
-				load_v(c_wave, vA);
-				load_k(c_wave + kWaves, kB);
-				load_v(c_wave + kWaves, vB);
+				load_k(c_wave);
+				load_v(c_wave);
 			}
 
 			// (The first K and V rows are in flight while Q is prepared.) Q^T as
@@ -545,10 +647,9 @@ namespace nnchip
 #pragma unroll
 			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-			// One chunk from buffers (kreg, vreg); the chunk two ahead is loaded
-			// into them as soon as they are consumed. A chunk past the
-			// wavefront's last one has no valid key (clo > chi) and adds nothing.
-			auto chunk = [&](int cw, u32x4 (&kreg)[NT][KK], u32x4 (&vreg)[NV]) __attribute__((always_inline))
+			// One chunk from (kreg, vreg); the wavefront's next chunk is loaded
+			// into them as soon as they are consumed.
+			auto chunk = [&](int cw) __attribute__((always_inline))
 			{
 				int cbase, clo, chi, rb;
 				chunk_bounds(cw, cbase, clo, chi, rb);
@@ -566,14 +667,14 @@ namespace nnchip
 						sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
 					}
 				}
-				load_k(cw + 2 * kWaves, kreg);
+				load_k(cw + kWaves);
 
 				// This chunk's V rows into the wavefront's LDS tile, then the next
 				// chunk's V loads into the freed registers.
 #pragma unroll
 				for (int j = 0; j < NV; ++j)
 					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
-				load_v(cw + 2 * kWaves, vreg);
+				load_v(cw + kWaves);
 
 				// Online softmax per head (column).
 				float m_loc = -INFINITY;
@@ -628,11 +729,7 @@ namespace nnchip
 					}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			for (int i = 0; i < n_wchunks; i += 2, c_wave += 2 * kWaves)
-			{
-				chunk(c_wave, kA, vA);
-				chunk(c_wave + kWaves, kB, vB);
-			}
+			for (int i = 0; i < n_wchunks; ++i, c_wave += kWaves) chunk(c_wave);
 
 			// Wavefront partial: each (head, d) of O^T has one owner lane.
 			l_run += __shfl_xor(l_run, 16);
@@ -653,105 +750,13 @@ namespace nnchip
 			write_wg_result<HD, G, W>(p, s_wpart, slot, split, out);
 		}
 
-		// Merges the n_split partials of one (token, query head) in a fixed
-		// order and writes o / l (0 when l == 0, reference nn_ops.cpp:492).
-		// Grid: (n_kv * G, n_tok). Each thread issues all of its loads before
-		// using them: one (m, l) pair per split, then one float4 of o for every
-		// J-th split of its quad.
+		// Grid: (n_kv * G, n_tok); one (token, query head) per work-group.
 		template <int HD, int G>
 		__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const decode_params p)
 		{
-			constexpr int kThreads = kMergeThreads;
-			constexpr int PW = HD + 2;
-			constexpr int QN = HD / 4; // output quads of one head
-			constexpr int J = kThreads / QN; // threads per quad
-			constexpr int MAXS = 256; // splits
-			__shared__ float s_f[MAXS];
-			__shared__ float s_red[kThreads / 64];
-			__shared__ float4 s_acc[kThreads];
-
 			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
 			const int n_kv = gridDim.x / G;
-			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh;
-			const float* hp = p.part + (slot * p.n_split * G + h) * PW; // split s at hp + s * G * PW
-			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-			const int q = threadIdx.x % QN, j = threadIdx.x / QN;
-
-			// One round of loads: this thread's (m, l) and the first 8 of its o quads.
-			auto load_batch = [&](int s0, float4* v) __attribute__((always_inline))
-			{
-#pragma unroll
-				for (int u = 0; u < 8; ++u)
-				{
-					const int sp = s0 + u * J;
-					v[u] = sp < p.n_split ? *reinterpret_cast<const float4*>(hp + static_cast<size_t>(sp) * G * PW + 4 * q)
-					                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-				}
-			};
-			float4 v[8];
-			load_batch(j, v);
-			float m = -INFINITY, l = 0.0f;
-			if (threadIdx.x < p.n_split)
-			{
-				const float* sp = hp + static_cast<size_t>(threadIdx.x) * G * PW;
-				m = sp[HD];
-				l = sp[HD + 1];
-			}
-			float mx = m;
-#pragma unroll
-			for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-			if (lane == 0) s_red[wave] = mx;
-			__syncthreads();
-			mx = s_red[0];
-#pragma unroll
-			for (int w = 1; w < kThreads / 64; ++w) mx = fmaxf(mx, s_red[w]);
-			const float m_use = mx == -INFINITY ? 0.0f : mx;
-			const float f = threadIdx.x < p.n_split ? fast_exp2(m - m_use) : 0.0f;
-			s_f[threadIdx.x] = f;
-			float lw = l * f;
-#pragma unroll
-			for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off);
-			__syncthreads();
-			if (lane == 0) s_red[wave] = lw;
-			__syncthreads();
-			float L = s_red[0];
-#pragma unroll
-			for (int w = 1; w < kThreads / 64; ++w) L += s_red[w];
-
-			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-			for (int s0 = j;; s0 += 8 * J)
-			{
-#pragma unroll
-				for (int u = 0; u < 8; ++u)
-				{
-					const int sp = s0 + u * J;
-					const float fw = sp < p.n_split ? s_f[sp] : 0.0f;
-					acc.x = fmaf(v[u].x, fw, acc.x);
-					acc.y = fmaf(v[u].y, fw, acc.y);
-					acc.z = fmaf(v[u].z, fw, acc.z);
-					acc.w = fmaf(v[u].w, fw, acc.w);
-				}
-				if (s0 + 8 * J >= p.n_split) break;
-				load_batch(s0 + 8 * J, v);
-			}
-			s_acc[threadIdx.x] = acc;
-			__syncthreads();
-			if (threadIdx.x < QN)
-			{
-				float4 r = s_acc[threadIdx.x];
-#pragma unroll
-				for (int jj = 1; jj < J; ++jj)
-				{
-					const float4 w4 = s_acc[jj * QN + threadIdx.x];
-					r.x += w4.x;
-					r.y += w4.y;
-					r.z += w4.z;
-					r.w += w4.w;
-				}
-				const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-				float* op = p.out + static_cast<size_t>(tok) * p.n_head * HD + static_cast<size_t>(kvh * G + h) * HD + 4 * threadIdx.x;
-				*reinterpret_cast<float4*>(op) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
-			}
+			merge_splits<HD, G>(p, static_cast<size_t>(tok) * n_kv + kvh, tok, kvh, h);
 		}
 
 		// NNC_HIP_DECODE_KERNEL=valu runs BF16 caches through the VALU P.V

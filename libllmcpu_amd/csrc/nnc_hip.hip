@@ -166,7 +166,7 @@ namespace
 		return NNC_OK;
 	}
 
-	// Split size: about two work-groups per CU over all (token, KV head)
+	// Split size: about one work-group per CU over all (token, KV head)
 	// pairs, a multiple of what one work-group iteration consumes, and at
 	// most kMaxSplits splits.
 	nnc_status decode_chunk(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, int32_t n_tok, int32_t pos0,
@@ -184,7 +184,7 @@ namespace
 		const int wgk = nnchip::decode_wg_keys(head_dim, bf16);
 		const int span = kmax - kmin + 1;
 		const long long pairs = static_cast<long long>(n_tok) * n_kv;
-		const long long want = std::max<long long>(1, 2LL * kv->n_cu / std::max<long long>(pairs, 1));
+		const long long want = std::max<long long>(1, 1LL * kv->n_cu / std::max<long long>(pairs, 1));
 		long long sk = (span + want - 1) / want;
 		if (const char* e = std::getenv("NNC_HIP_DECODE_SPLIT")) // keys per work-group, for tuning
 			if (std::atoll(e) > 0) sk = std::atoll(e);
