@@ -93,6 +93,42 @@ def cpu_baseline(kv, target_s: float) -> dict:
                       f"(nproc {nproc}; the reference's kernels and worker pool)"}
 
 
+def pmc_summary(fetch_csv: str, write_csv: str) -> dict:
+    """HBM bytes per decode call from two `rocprofv3 --pmc` runs of
+    `bench.py --only decode --calibrate` (FETCH_SIZE, then WRITE_SIZE, both
+    in KiB per dispatch). The copy of CALIBRATE_MIB MiB that such a run
+    starts with reads and writes exactly that many bytes, which converts each
+    counter to bytes."""
+    import csv
+
+    def per_kernel(path):
+        acc = {}
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            key = ("copy" if "copy" in name.lower() else "merge" if "decode_merge" in name
+                   else "decode" if "decode" in name else None)
+            if key:
+                acc.setdefault(key, []).append(float(r["Counter_Value"]))
+        return {k: float(np.median(v)) for k, v in acc.items()}
+
+    f, w = per_kernel(fetch_csv), per_kernel(write_csv)
+    copy_bytes = CALIBRATE_MIB << 20
+    f_scale = copy_bytes / (f["copy"] * 1024)
+    w_scale = copy_bytes / (w["copy"] * 1024)
+    fetch = (f["decode"] + f.get("merge", 0.0)) * 1024 * f_scale
+    write = (w["decode"] + w.get("merge", 0.0)) * 1024 * w_scale
+    return {"hbm_bytes_per_launch": int(round(fetch + write)), "fetch_bytes": int(round(fetch)),
+            "write_bytes": int(round(write)), "algorithmic_bytes": decode_bytes(CTX),
+            "fetch_kib_per_dispatch": {k: round(v, 1) for k, v in f.items()},
+            "write_kib_per_dispatch": {k: round(v, 1) for k, v in w.items()},
+            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+            "calibration": f"torch copy_ of {CALIBRATE_MIB} MiB (reads and writes {copy_bytes} bytes)",
+            "launch": "one attend call: decode_bf16_kernel + decode_merge_kernel"}
+
+
+CALIBRATE_MIB = 1024
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,7 +141,14 @@ def main() -> int:
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
                     help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
+    ap.add_argument("--calibrate", action="store_true",
+                    help=f"start with a {CALIBRATE_MIB} MiB copy kernel (counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
               "multi-GPU path; see DESIGN.md for how the op would shard)", file=sys.stderr)
@@ -148,6 +191,16 @@ def main() -> int:
         nh.fill_normal(q_pre + li * PROMPT * N_HEAD * HD * 4, PROMPT * N_HEAD * HD, (1234 + 3000 + li) * 256 + 3, HD,
                        False, stream)
     kv.sync()
+    if args.calibrate:
+        # A plain copy kernel of known size (torch's elementwise copy).
+        import torch
+
+        a = torch.ones(CALIBRATE_MIB << 18, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
 
     def decode_step():
         for li in range(N_LAYER):
@@ -237,8 +290,8 @@ def main() -> int:
                    "kv_dtype": "bf16", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dec_launch_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_launch_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_kernel<128,4,bf16>", "avg_launch_us": round(dec_launch_us, 3),
-                     "bytes_per_launch": decode_bytes(CTX)},
+                     "kernel": "decode_bf16_kernel<128,4,4> + decode_merge_kernel<128,4> (one attend call)",
+                     "avg_launch_us": round(dec_launch_us, 3), "bytes_per_launch": decode_bytes(CTX)},
         "prefill": {"metric": "prefill-attn TFLOP/s", "value": round(pre_tflops, 1), "unit": "TFLOP/s",
                     "ms_per_step": round(pre_step_ms, 3), "steps": args.prefill_steps,
                     "workload": f"qwen3-4b prefill of {PROMPT} tokens in {CHUNK}-token chunks, 36 layers",
