@@ -62,16 +62,6 @@ namespace nnchip
 			return r >= rows ? r - rows : r;
 		}
 
-		// Orders one wavefront's LDS writes before its own later reads of
-		// other lanes' values (LDS executes a wavefront's operations in order;
-		// this keeps the compiler from moving them).
-		__device__ __forceinline__ void wave_sync()
-		{
-			__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-			__builtin_amdgcn_wave_barrier();
-			__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-		}
-
 		// The work-group's result from its wavefronts' partials in s_wpart
 		// (o[head_dim], m, l per head, per wavefront), merged in wavefront
 		// order: a partial for the split merge, or, with a single split, o / l.

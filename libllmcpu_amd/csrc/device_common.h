@@ -73,24 +73,40 @@ namespace nnchip
 	__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 	__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+	// Two fp32 -> packed bf16, rounded to nearest even (v_cvt_pk_bf16_f32).
+	__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi)
+	{
+		typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+		const bf16x2 h = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+		return __builtin_bit_cast(uint32_t, h);
+	}
+
 	// Splits 8 fp32 values into bf16 hi + lo parts with x ~= hi + lo to about
 	// 16 significant bits, so two bf16 MFMAs give a near-fp32 product against
 	// an exact bf16 operand.
 	__device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo)
 	{
-		uint4 h, l;
-		uint32_t* hp = reinterpret_cast<uint32_t*>(&h);
-		uint32_t* lp = reinterpret_cast<uint32_t*>(&l);
+		u32x4 h, l;
 #pragma unroll
 		for (int j = 0; j < 4; ++j)
 		{
 			const float a = x[2 * j], b = x[2 * j + 1];
-			const uint32_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
-			hp[j] = ha | (hb << 16);
-			lp[j] = pack_bf16x2(a - bf16_bits_to_f32(ha), b - bf16_bits_to_f32(hb));
+			const uint32_t hw = cvt_pk_bf16(a, b);
+			h[j] = hw;
+			l[j] = cvt_pk_bf16(a - bf16_lo(hw), b - bf16_hi(hw));
 		}
 		hi = as_bf16x8(h);
 		lo = as_bf16x8(l);
+	}
+
+	// Orders one wavefront's LDS writes before its own later reads of other
+	// lanes' values (LDS executes a wavefront's operations in order; this
+	// keeps the compiler from moving them).
+	__device__ __forceinline__ void wave_sync()
+	{
+		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+		__builtin_amdgcn_wave_barrier();
+		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 	}
 
 	__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
