@@ -52,30 +52,32 @@ namespace nnchip
 		// the other's MFMAs, and cap a wavefront at 256 registers.
 		constexpr int kWpe = 2;
 
-		// Per head_dim: 16-row blocks per work-group (NB), wavefronts per SIMD
-		// (WPE), and whether Q's lo half waits in LDS instead of registers.
+		// Per head_dim, within a wavefront's 256 registers: 16-row blocks per
+		// work-group (NB), whether Q's hi half also waits in LDS (the lo half
+		// always does), and whether the next step's K is loaded a step ahead
+		// into registers (else at the start of its step).
 		template <int HD>
 		struct prefill_cfg;
 		template <>
 		struct prefill_cfg<64>
 		{
 			static constexpr int NB = 2, WPE = 2;
-			static constexpr bool QLO_LDS = true;
+			static constexpr bool QHI_LDS = false, K_AHEAD = true;
 		};
 		template <>
 		struct prefill_cfg<128>
 		{
 			static constexpr int NB = 2, WPE = 2;
-			static constexpr bool QLO_LDS = true;
+			static constexpr bool QHI_LDS = false, K_AHEAD = false; // measured: loading K a step ahead (with Q hi in LDS) is no faster
 		};
 		template <>
 		struct prefill_cfg<256>
 		{
 			static constexpr int NB = 1, WPE = 2;
-			static constexpr bool QLO_LDS = true;
+			static constexpr bool QHI_LDS = false, K_AHEAD = false;
 		};
 
-		template <int HD, int NB, bool QLDS>
+		template <int HD, int NB, bool QHI_LDS>
 		struct prefill_shape
 		{
 			static constexpr int KK = HD / 32; // k-steps of the QK MFMA
@@ -85,9 +87,9 @@ namespace nnchip
 			static constexpr int KPL = 64 / LPK; // V rows per load
 			static constexpr int NV = kWK / KPL; // V loads per step
 			static constexpr int OPITCH = HD + 4; // floats per row in the final merge
-			static constexpr int QPITCH = HD + 8; // bf16 per row of Q's lo half
+			static constexpr int QPITCH = HD + 8; // bf16 per row of Q's halves in LDS
 			static constexpr int kVBytes = kWaves * kWK * HD * 2; // per-wavefront V tiles, bf16
-			static constexpr int kQBytes = QLDS ? ROWS * QPITCH * 2 : 0;
+			static constexpr int kQBytes = (QHI_LDS ? 2 : 1) * ROWS * QPITCH * 2; // lo rows, then hi rows
 			static constexpr int kOBytes = kWaves * ROWS * OPITCH * 4;
 			static constexpr int kLds = kVBytes + kQBytes > kOBytes ? kVBytes + kQBytes : kOBytes;
 			static_assert(NV >= 1 && KPL * NV == kWK, "unsupported prefill shape");
@@ -151,8 +153,8 @@ namespace nnchip
 		{
 			static_assert(prefill_cfg<HD>::WPE == kWpe, "one occupancy for every head_dim");
 			constexpr int NB = prefill_cfg<HD>::NB;
-			constexpr bool QLDS = prefill_cfg<HD>::QLO_LDS;
-			using S = prefill_shape<HD, NB, QLDS>;
+			constexpr bool QHI_LDS = prefill_cfg<HD>::QHI_LDS, K_AHEAD = prefill_cfg<HD>::K_AHEAD;
+			using S = prefill_shape<HD, NB, QHI_LDS>;
 			constexpr int KK = S::KK, DB = S::DB, ROWS = S::ROWS, LPK = S::LPK, KPL = S::KPL, NV = S::NV,
 			              OPITCH = S::OPITCH, QPITCH = S::QPITCH;
 
@@ -204,12 +206,14 @@ namespace nnchip
 			}
 
 			// Q^T as the B operand, pre-scaled into log2 units, bf16 hi + lo. The
-			// hi half stays in registers; the lo half too, or, where registers
-			// are the limit, in LDS at the address the same lane reads it back
-			// from.
-			bf16x8 qhi[NB][KK];
-			bf16x8 qlo_r[QLDS ? 1 : NB][KK];
-			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes);
+			// lo half (and, where registers are short, the hi half) waits in LDS
+			// at the address the same lane reads it back from.
+			bf16x8 qhi[QHI_LDS ? 1 : NB][KK];
+			uint16_t* s_q = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes);
+			auto q_lds = [&](int half, int nb, int kk) __attribute__((always_inline)) -> bf16x8*
+			{
+				return reinterpret_cast<bf16x8*>(s_q + (half * ROWS + 16 * nb + col) * QPITCH + 32 * kk + 8 * grp);
+			};
 #pragma unroll
 			for (int nb = 0; nb < NB; ++nb)
 			{
@@ -235,12 +239,13 @@ namespace nnchip
 #pragma unroll
 						for (int j = 0; j < 8; ++j) x[j] = 0.0f;
 					}
-					bf16x8 lo;
-					split_bf16x8(x, qhi[nb][kk], lo);
-					if constexpr (QLDS)
-						*reinterpret_cast<bf16x8*>(s_qlo + (16 * nb + col) * QPITCH + 32 * kk + 8 * grp) = lo;
+					bf16x8 hi, lo;
+					split_bf16x8(x, hi, lo);
+					*q_lds(0, nb, kk) = lo;
+					if constexpr (QHI_LDS)
+						*q_lds(1, nb, kk) = hi;
 					else
-						qlo_r[QLDS ? 0 : nb][kk] = lo;
+						qhi[QHI_LDS ? 0 : nb][kk] = hi;
 				}
 			}
 
@@ -375,7 +380,7 @@ namespace nnchip
 			// scores: S^T - m_off for both 16-key blocks, then the next K loads.
 			auto scores = [&](int i, f32x4 (&sc)[2][NB]) __attribute__((always_inline))
 			{
-				load_k(i);
+				if constexpr (!K_AHEAD) load_k(i);
 #pragma unroll
 				for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -386,16 +391,13 @@ namespace nnchip
 						for (int kk = 0; kk < KK; ++kk)
 						{
 							const bf16x8 a = as_bf16x8(kreg[mb][kk]);
-							bf16x8 qlo;
-							if constexpr (QLDS)
-								qlo = *reinterpret_cast<const bf16x8*>(s_qlo + (16 * nb + col) * QPITCH + 32 * kk + 8 * grp);
-							else
-								qlo = qlo_r[QLDS ? 0 : nb][kk];
-							acc = mfma16x16x32(a, qhi[nb][kk], acc);
-							acc = mfma16x16x32(a, qlo, acc);
+							const bf16x8 qh = QHI_LDS ? *q_lds(1, nb, kk) : qhi[QHI_LDS ? 0 : nb][kk];
+							acc = mfma16x16x32(a, qh, acc);
+							acc = mfma16x16x32(a, *q_lds(0, nb, kk), acc);
 						}
 						sc[mb][nb] = acc;
 					}
+				if constexpr (K_AHEAD) load_k(i + 1); // past the last step: nothing in range, zeros
 			};
 			// Masks keys outside a row's span (only on steps that cross an edge)
 			// and returns each row's maximum; true when some row's offset has to
@@ -488,7 +490,11 @@ namespace nnchip
 				load_v(i + 1); // past the last step: nothing in range, zeros
 			};
 
-			if (n_steps > 0) load_v(0);
+			if (n_steps > 0)
+			{
+				if constexpr (K_AHEAD) load_k(0);
+				load_v(0);
+			}
 			// The inner loop runs the steps that need no rescale; a step whose
 			// scores outgrow a row's offset leaves it, is rescaled and finished
 			// outside, so the O accumulators are only touched by MFMAs in the
