@@ -298,7 +298,7 @@ def main() -> int:
                     "roofline": {"bound": "mfma", "achieved": round(pre_launch_tflops, 1),
                                  "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                                 "kernel": "prefill_kernel<128,4,2> (fp16 MFMA, fp32 accumulate)",
+                                 "kernel": "prefill_kernel<128,4> (bf16 hi+lo QK, fp16 PV MFMA, fp32 accumulate)",
                                  "avg_launch_us": round(pre_launch_us, 3)}},
         "cpu_baseline": cpu,
         "device": {"cu": n_cu, "clock_mhz": clock_mhz},

@@ -124,7 +124,8 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
  * NNC_ERR_CONTEXT_FULL: a key the batch needs lies outside what the buffer
  * can hold (a full buffer with pos0 + n_tok > rows, or a ring too small for
  * the window plus the batch).
- * NNC_ERR_UNSUPPORTED_MODEL: a head_dim or group outside the supported set. */
+ * NNC_ERR_UNSUPPORTED_MODEL: a head_dim or group outside the supported set,
+ * or a BF16 batch (n_tok > 1) over a buffer of 2 GiB or more. */
 nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
                           int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
                           int32_t head_dim, float scale);

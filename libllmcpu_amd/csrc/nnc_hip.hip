@@ -298,6 +298,10 @@ namespace
 			            group);
 		if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
 			return fail(NNC_ERR_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
+		// The BF16 batch kernel addresses a buffer with 32-bit byte offsets.
+		if (n_tok > 1 && kv->bf16 && static_cast<uint64_t>(b.rows) * b.kv_dim * 2 > 0x7fffffffu)
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "a %d x %d BF16 buffer is too large for the batch kernel (2 GiB)",
+			            b.rows, b.kv_dim);
 		// Every key the batch reads must still be in the buffer: the newest
 		// position written is n_seq - 1, and the buffer keeps the last `rows`.
 		int first0, last0;
