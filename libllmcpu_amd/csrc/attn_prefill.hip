@@ -54,30 +54,30 @@ namespace nnchip
 
 		// Per head_dim, within a wavefront's 256 registers: 16-row blocks per
 		// work-group (NB), whether Q's hi half also waits in LDS (the lo half
-		// always does), and whether the next step's K is loaded a step ahead
-		// into registers (else at the start of its step).
+		// always does), and whether K streams into LDS a step ahead (else into
+		// registers at the start of its step).
 		template <int HD>
 		struct prefill_cfg;
 		template <>
 		struct prefill_cfg<64>
 		{
 			static constexpr int NB = 2, WPE = 2;
-			static constexpr bool QHI_LDS = false, K_AHEAD = true;
+			static constexpr bool QHI_LDS = false, K_LDS = true;
 		};
 		template <>
 		struct prefill_cfg<128>
 		{
 			static constexpr int NB = 2, WPE = 2;
-			static constexpr bool QHI_LDS = false, K_AHEAD = false; // measured: loading K a step ahead (with Q hi in LDS) is no faster
+			static constexpr bool QHI_LDS = false, K_LDS = true;
 		};
 		template <>
 		struct prefill_cfg<256>
 		{
 			static constexpr int NB = 1, WPE = 2;
-			static constexpr bool QHI_LDS = false, K_AHEAD = false;
+			static constexpr bool QHI_LDS = false, K_LDS = false; // LDS-bound: two work-groups per CU must fit
 		};
 
-		template <int HD, int NB, bool QHI_LDS>
+		template <int HD, int NB, bool QHI_LDS, bool K_LDS>
 		struct prefill_shape
 		{
 			static constexpr int KK = HD / 32; // k-steps of the QK MFMA
@@ -91,7 +91,9 @@ namespace nnchip
 			static constexpr int kVBytes = kWaves * kWK * HD * 2; // per-wavefront V tiles, bf16
 			static constexpr int kQBytes = (QHI_LDS ? 2 : 1) * ROWS * QPITCH * 2; // lo rows, then hi rows
 			static constexpr int kOBytes = kWaves * ROWS * OPITCH * 4;
-			static constexpr int kLds = kVBytes + kQBytes > kOBytes ? kVBytes + kQBytes : kOBytes;
+			static constexpr int kKBytes = K_LDS ? kWaves * kWK * HD * 2 : 0; // per-wavefront K tiles, bf16
+			static constexpr int kLoop = kVBytes + kKBytes + kQBytes;
+			static constexpr int kLds = kLoop > kOBytes ? kLoop : kOBytes;
 			static_assert(NV >= 1 && KPL * NV == kWK, "unsupported prefill shape");
 		};
 
@@ -121,6 +123,14 @@ namespace nnchip
 		{
 			typedef __attribute__((address_space(3))) void* lds_ptr;
 			__builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)lds, 16, voffset, 0, 0, 0);
+		}
+
+		// 16-byte slot swizzle of row `row` of a K tile: the A-operand reads of
+		// 16 consecutive rows at one slot land in distinct banks.
+		template <int HD>
+		__device__ __forceinline__ int kswz(int row)
+		{
+			return HD == 64 ? (row >> 1) & 7 : row & 15;
 		}
 
 		// Eight bf16 (one 16-byte load) -> eight fp16, exact up to 65504.
@@ -153,8 +163,8 @@ namespace nnchip
 		{
 			static_assert(prefill_cfg<HD>::WPE == kWpe, "one occupancy for every head_dim");
 			constexpr int NB = prefill_cfg<HD>::NB;
-			constexpr bool QHI_LDS = prefill_cfg<HD>::QHI_LDS, K_AHEAD = prefill_cfg<HD>::K_AHEAD;
-			using S = prefill_shape<HD, NB, QHI_LDS>;
+			constexpr bool QHI_LDS = prefill_cfg<HD>::QHI_LDS, K_LDS = prefill_cfg<HD>::K_LDS;
+			using S = prefill_shape<HD, NB, QHI_LDS, K_LDS>;
 			constexpr int KK = S::KK, DB = S::DB, ROWS = S::ROWS, LPK = S::LPK, KPL = S::KPL, NV = S::NV,
 			              OPITCH = S::OPITCH, QPITCH = S::QPITCH;
 
@@ -209,7 +219,7 @@ namespace nnchip
 			// lo half (and, where registers are short, the hi half) waits in LDS
 			// at the address the same lane reads it back from.
 			bf16x8 qhi[QHI_LDS ? 1 : NB][KK];
-			uint16_t* s_q = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes);
+			uint16_t* s_q = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes + S::kKBytes);
 			auto q_lds = [&](int half, int nb, int kk) __attribute__((always_inline)) -> bf16x8*
 			{
 				return reinterpret_cast<bf16x8*>(s_q + (half * ROWS + 16 * nb + col) * QPITCH + 32 * kk + 8 * grp);
@@ -310,14 +320,46 @@ namespace nnchip
 				return ok ? static_cast<uint32_t>(row) * row_bytes + col_bytes : 0x80000000u;
 			};
 
-			// K as the A operand, into registers: lane (grp, col) reads key col of
-			// a 16-key block, elements 32 kk + 8 grp .. + 8.
+			const int v_row = lane / LPK; // a lane's tile row within one 16-byte-per-lane load
+
+			// K as the A operand: lane (grp, col) takes key col of a 16-key block,
+			// elements 32 kk + 8 grp .. + 8 (16-byte slot 4 kk + grp of the row).
+			// K_LDS: the wavefront's 32 rows stream into its LDS tile like V's
+			// (slot s of row r at s ^ kswz(r)), a step ahead of their use;
+			// otherwise they load into registers at the start of the step.
+			uint16_t* kt = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes) + wave * kWK * HD;
 			uint32_t k_off[2];
 #pragma unroll
 			for (int mb = 0; mb < 2; ++mb) k_off[mb] = static_cast<uint32_t>(16 * mb + col) * row_bytes + 16u * grp;
-			u32x4 kreg[2][KK];
+			uint32_t k_col[NV];
+#pragma unroll
+			for (int j = 0; j < NV; ++j) k_col[j] = 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(j * KPL + v_row));
+			u32x4 kreg[K_LDS ? 1 : 2][KK];
+			auto load_k_lds = [&](int i) __attribute__((always_inline))
+			{
+				int r;
+				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase, r);
+				if (!straddles(r))
+				{
+#pragma unroll
+					for (int j = 0; j < NV; ++j)
+						load_lds16(rk, kt + j * KPL * HD, static_cast<uint32_t>(j * KPL + v_row) * row_bytes + k_col[j]);
+				}
+				else
+				{
+					const __amdgpu_buffer_rsrc_t ring = rsrc(kbase, 0, end_ring);
+#pragma unroll
+					for (int j = 0; j < NV; ++j)
+						load_lds16(ring, kt + j * KPL * HD, ring_off(r, j * KPL + v_row, k_col[j]));
+				}
+			};
 			auto load_k = [&](int i) __attribute__((always_inline))
 			{
+				if constexpr (K_LDS)
+				{
+					load_k_lds(i);
+					return;
+				}
 				int r;
 				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase, r);
 				if (!straddles(r))
@@ -326,7 +368,7 @@ namespace nnchip
 					for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
 						for (int kk = 0; kk < KK; ++kk)
-							kreg[mb][kk] =
+							kreg[K_LDS ? 0 : mb][kk] =
 								__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off[mb] + 64u * kk, 0, 0));
 				}
 				else
@@ -338,7 +380,7 @@ namespace nnchip
 						const uint32_t off = ring_off(r, 16 * mb + col, 16u * grp);
 #pragma unroll
 						for (int kk = 0; kk < KK; ++kk)
-							kreg[mb][kk] =
+							kreg[K_LDS ? 0 : mb][kk] =
 								__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ring, off + 64u * kk, 0, 0));
 					}
 				}
@@ -350,7 +392,6 @@ namespace nnchip
 			// which holds the row's segment (l % LPK) ^ vswz(row). The swizzle
 			// keeps the transposing reads of 4 (8) rows in distinct banks.
 			uint16_t* vt = reinterpret_cast<uint16_t*>(s_raw) + wave * kWK * HD;
-			const int v_row = lane / LPK;
 			uint32_t v_col[NV];
 #pragma unroll
 			for (int j = 0; j < NV; ++j) v_col[j] = 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(j * KPL + v_row));
@@ -380,7 +421,7 @@ namespace nnchip
 			// scores: S^T - m_off for both 16-key blocks, then the next K loads.
 			auto scores = [&](int i, f32x4 (&sc)[2][NB]) __attribute__((always_inline))
 			{
-				if constexpr (!K_AHEAD) load_k(i);
+				if constexpr (!K_LDS) load_k(i);
 #pragma unroll
 				for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -390,14 +431,21 @@ namespace nnchip
 #pragma unroll
 						for (int kk = 0; kk < KK; ++kk)
 						{
-							const bf16x8 a = as_bf16x8(kreg[mb][kk]);
+							bf16x8 a;
+							if constexpr (K_LDS)
+							{
+								const int row = 16 * mb + col, slot = 4 * kk + grp;
+								a = *reinterpret_cast<const bf16x8*>(kt + row * HD + 8 * (slot ^ kswz<HD>(row)));
+							}
+							else
+								a = as_bf16x8(kreg[K_LDS ? 0 : mb][kk]);
 							const bf16x8 qh = QHI_LDS ? *q_lds(1, nb, kk) : qhi[QHI_LDS ? 0 : nb][kk];
 							acc = mfma16x16x32(a, qh, acc);
 							acc = mfma16x16x32(a, *q_lds(0, nb, kk), acc);
 						}
 						sc[mb][nb] = acc;
 					}
-				if constexpr (K_AHEAD) load_k(i + 1); // past the last step: nothing in range, zeros
+				if constexpr (K_LDS) load_k(i + 1); // past the last step: nothing in range, zeros
 			};
 			// Masks keys outside a row's span (only on steps that cross an edge)
 			// and returns each row's maximum; true when some row's offset has to
@@ -492,7 +540,7 @@ namespace nnchip
 
 			if (n_steps > 0)
 			{
-				if constexpr (K_AHEAD) load_k(0);
+				if constexpr (K_LDS) load_k(0);
 				load_v(0);
 			}
 			// The inner loop runs the steps that need no rescale; a step whose
