@@ -5,9 +5,10 @@
 // Rows of the problem are (token, query head) pairs of one KV head, token
 // major, so the heads of a GQA group sit in adjacent rows and share every key
 // the work-group reads. Grid: n_kv * n_qtiles work-groups of 4 wavefronts; a
-// work-group owns ROWS = 16 * NB rows and walks its key range in steps of
-// 128 keys, wavefront w taking keys 32w .. 32w + 31 of each step for all of
-// the work-group's rows. Each wavefront therefore reads a disjoint quarter of
+// work-group owns 32 rows and walks its key range in steps of 128 keys,
+// wavefront w taking keys 32w .. 32w + 31 of each step for all 32 rows, so
+// every product is one 32 x 32 tile (v_mfma_f32_32x32x16, which one
+// wavefront keeps near the matrix peak). Each wavefront therefore reads a disjoint quarter of
 // the keys, keeps its own online softmax, and the four partial results merge
 // once, in LDS, at the end.
 //
@@ -54,33 +55,21 @@ namespace nnchip
 		constexpr float kLazy = 8.0f; // max growth of a row's scores over its offset, log2 units
 		constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3: raw 32-bit data
 
-		// Per head_dim: 16-row blocks per work-group (NB) and wavefronts per
-		// SIMD (WPE; two let one wavefront's VALU work overlap the other's
-		// MFMAs and cap a wavefront at 256 registers).
-		template <int HD>
-		struct prefill_cfg;
-		template <>
-		struct prefill_cfg<64>
-		{
-			static constexpr int NB = 2, WPE = 2;
-		};
-		template <>
-		struct prefill_cfg<128>
-		{
-			static constexpr int NB = 2, WPE = 2;
-		};
-		template <>
-		struct prefill_cfg<256>
-		{
-			static constexpr int NB = 2, WPE = 1;
-		};
+		constexpr int kRows = 32; // rows per work-group: one 32-wide N tile
 
-		template <int HD, int NB>
+		// Wavefronts per SIMD: two where a wavefront fits in 256 registers, so
+		// one wavefront's VALU work and loads overlap the other's MFMAs.
+		template <int HD>
+		constexpr int prefill_wpe()
+		{
+			return HD == 256 ? 1 : 2;
+		}
+
+		template <int HD>
 		struct prefill_shape
 		{
-			static constexpr int KK = HD / 32; // k-steps of the QK MFMA
-			static constexpr int DB = HD / 16; // 16-row d blocks of O^T
-			static constexpr int ROWS = 16 * NB; // rows per work-group
+			static constexpr int KT = HD / 16; // QK MFMAs per Q half (16 elements of d each)
+			static constexpr int DBK = HD / 32; // 32-row d blocks of O^T
 			static constexpr int LPK = HD / 8; // lanes per tile row (16 bytes each)
 			static constexpr int KPL = 64 / LPK; // tile rows per DMA
 			static constexpr int NV = kWK / KPL; // DMAs per tile per step
@@ -89,8 +78,8 @@ namespace nnchip
 			static constexpr int kTile = kWK * HD * 2; // bytes of one wavefront's K (or V) tile
 			static constexpr int kVBytes = kWaves * kTile;
 			static constexpr int kKBytes = kWaves * kTile;
-			static constexpr int kQBytes = ROWS * QPITCH * 2;
-			static constexpr int kOBytes = kWaves * ROWS * OPITCH * 4;
+			static constexpr int kQBytes = kRows * QPITCH * 2;
+			static constexpr int kOBytes = kWaves * kRows * OPITCH * 4;
 			static constexpr int kLoop = kVBytes + kKBytes + kQBytes;
 			static constexpr int kLds = kLoop > kOBytes ? kLoop : kOBytes;
 			static_assert(NV >= 1 && KPL * NV == kWK, "unsupported prefill shape");
@@ -153,23 +142,22 @@ namespace nnchip
 
 		template <int HD, int G>
 		__global__ __launch_bounds__(64 * kWaves)
-			__attribute__((amdgpu_waves_per_eu(prefill_cfg<HD>::WPE, prefill_cfg<HD>::WPE))) void prefill_kernel(
+			__attribute__((amdgpu_waves_per_eu(prefill_wpe<HD>(), prefill_wpe<HD>()))) void prefill_kernel(
 				const prefill_params p)
 		{
-			constexpr int NB = prefill_cfg<HD>::NB;
-			using S = prefill_shape<HD, NB>;
-			constexpr int KK = S::KK, DB = S::DB, ROWS = S::ROWS, LPK = S::LPK, KPL = S::KPL, NV = S::NV,
-			              OPITCH = S::OPITCH, QPITCH = S::QPITCH;
+			using S = prefill_shape<HD>;
+			constexpr int KT = S::KT, DBK = S::DBK, LPK = S::LPK, KPL = S::KPL, NV = S::NV, OPITCH = S::OPITCH,
+			              QPITCH = S::QPITCH;
 
 			// K and V tiles and Q's lo half during the key loop, then the merge buffer.
 			__shared__ __attribute__((aligned(16))) unsigned char s_raw[S::kLds];
-			__shared__ float s_m[kWaves][ROWS];
-			__shared__ float s_l[kWaves][ROWS];
+			__shared__ float s_m[kWaves][kRows];
+			__shared__ float s_l[kWaves][kRows];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps step control scalar
-			const int col = lane & 15;
-			const int grp = lane >> 4;
+			const int r32 = lane & 31; // this lane's row of the tile (and key, as an A-operand row)
+			const int h = lane >> 5; // which half of an MFMA's k range this lane holds
 
 			// Work-groups of one KV head run on one XCD (blockIdx.x % 8 picks
 			// the XCD), so its K/V rows are shared through that XCD's L2; within
@@ -181,7 +169,7 @@ namespace nnchip
 			const int qt = p.n_qtiles - 1 - bid % p.n_qtiles;
 
 			const int n_rows = p.n_tok * G;
-			const int row0 = qt * ROWS;
+			const int row0 = qt * kRows;
 			const size_t q_stride = static_cast<size_t>(p.n_head) * HD;
 
 			// The work-group's key range [kmin, kmax], and [first_hi, last_lo],
@@ -189,24 +177,14 @@ namespace nnchip
 			// position).
 			int kmin, kmax, first_hi, last_lo;
 			{
-				const int t0 = row0 / G, t1 = min(p.n_tok - 1, (row0 + ROWS - 1) / G);
+				const int t0 = row0 / G, t1 = min(p.n_tok - 1, (row0 + kRows - 1) / G);
 				attn_span(p.causal, p.window, p.pos0 + t0, p.n_seq, kmin, last_lo);
 				attn_span(p.causal, p.window, p.pos0 + t1, p.n_seq, first_hi, kmax);
 			}
-			// Each lane's rows (one per 16-row block): their spans.
-			int rfirst[NB], rlast[NB];
-#pragma unroll
-			for (int nb = 0; nb < NB; ++nb)
-			{
-				const int r = row0 + 16 * nb + col;
-				if (r < n_rows)
-					attn_span(p.causal, p.window, p.pos0 + r / G, p.n_seq, rfirst[nb], rlast[nb]);
-				else
-				{
-					rfirst[nb] = 1;
-					rlast[nb] = 0; // no key
-				}
-			}
+			// This lane's row and its span.
+			const int my_row = row0 + r32;
+			int rfirst = 1, rlast = 0; // no key
+			if (my_row < n_rows) attn_span(p.causal, p.window, p.pos0 + my_row / G, p.n_seq, rfirst, rlast);
 
 			// The key range as contiguous segments of rows: keys kmin .. from row
 			// rb0 up to the buffer's end, then (a ring that wraps) the rest from
@@ -268,30 +246,28 @@ namespace nnchip
 			// The first step's tiles go out before Q is read, so the latencies overlap.
 			if (n_steps > 0) load_tiles(0);
 
-			// Q^T as the B operand, pre-scaled into log2 units, bf16 hi + lo: the
-			// hi half in registers, the lo half in LDS at the address the same
-			// lane reads it back from.
-			bf16x8 qhi[NB][KK];
+			// Q^T as the B operand (lane l: row l % 32, elements 16 t + 8 h .. + 8),
+			// pre-scaled into log2 units, bf16 hi + lo: the hi half in registers,
+			// the lo half in LDS at the address the same lane reads it back from.
+			bf16x8 qhi[KT];
 			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes + S::kKBytes);
-			auto q_lo = [&](int nb, int kk) __attribute__((always_inline)) -> bf16x8*
+			auto q_lo = [&](int t) __attribute__((always_inline)) -> bf16x8*
 			{
-				return reinterpret_cast<bf16x8*>(s_qlo + (16 * nb + col) * QPITCH + 32 * kk + 8 * grp);
+				return reinterpret_cast<bf16x8*>(s_qlo + r32 * QPITCH + 16 * t + 8 * h);
 			};
-#pragma unroll
-			for (int nb = 0; nb < NB; ++nb)
 			{
-				const int r = row0 + 16 * nb + col;
-				const bool ok = r < n_rows;
-				const float* qp =
-					p.q + (ok ? static_cast<size_t>(r / G) * q_stride + static_cast<size_t>(kvh * G + r % G) * HD : 0);
+				const bool ok = my_row < n_rows;
+				const float* qp = p.q + (ok ? static_cast<size_t>(my_row / G) * q_stride +
+				                                  static_cast<size_t>(kvh * G + my_row % G) * HD
+				                            : 0);
 #pragma unroll
-				for (int kk = 0; kk < KK; ++kk)
+				for (int t = 0; t < KT; ++t)
 				{
 					float x[8];
 					if (ok)
 					{
-						const float4 a = *reinterpret_cast<const float4*>(qp + 32 * kk + 8 * grp);
-						const float4 b = *reinterpret_cast<const float4*>(qp + 32 * kk + 8 * grp + 4);
+						const float4 a = *reinterpret_cast<const float4*>(qp + 16 * t + 8 * h);
+						const float4 b = *reinterpret_cast<const float4*>(qp + 16 * t + 8 * h + 4);
 						x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
 						x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 #pragma unroll
@@ -303,178 +279,152 @@ namespace nnchip
 						for (int j = 0; j < 8; ++j) x[j] = 0.0f;
 					}
 					bf16x8 lo;
-					split_bf16x8(x, qhi[nb][kk], lo);
-					*q_lo(nb, kk) = lo;
+					split_bf16x8(x, qhi[t], lo);
+					*q_lo(t) = lo;
 				}
 			}
 
-			f32x4 acc_o[DB][NB];
-			f32x4 acc_l[NB];
-			float m_off[NB]; // each row's score offset (-inf until it has seen a key)
-			f32x4 c_init[NB]; // S^T's accumulator start: -m_off, or 0 before the first key
+			f32x16 acc_o[DBK]; // O^T: lane l holds d = 32 b + 8 (i / 4) + 4 h + i % 4 of row l % 32
+			float l_acc = 0.0f; // this lane's half of its row's sum of weights
+			float m_off = -INFINITY; // the row's score offset (-inf until it has seen a key)
+			f32x16 c_init; // S^T's accumulator start: -m_off, or 0 before the first key
 #pragma unroll
-			for (int nb = 0; nb < NB; ++nb)
-			{
+			for (int b = 0; b < DBK; ++b)
 #pragma unroll
-				for (int db = 0; db < DB; ++db) acc_o[db][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-				acc_l[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-				m_off[nb] = -INFINITY;
-				c_init[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-			}
-			// fp16 1.0 in every element: the A operand that sums P over keys.
-			const f16x8 ones = as_f16x8(u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u});
-			// V^T read position of this lane (keys 16h + 4g + c / 4 + 0..3 across
-			// the transpose, elements 16 db + 4 (c % 4) .. + 4).
-			const int trow = 4 * grp + (col >> 2);
+				for (int e = 0; e < 16; ++e) acc_o[b][e] = 0.0f;
+#pragma unroll
+			for (int e = 0; e < 16; ++e) c_init[e] = 0.0f;
+			// V^T read position of this lane: a 16-lane group q covers elements
+			// 32 b + 16 (q & 1) .. + 16 of four tile rows 16 c + 4 h (+ 8).
+			const int tq = (lane >> 4) & 1, ti = lane & 15;
 
 			for (int i = 0; i < n_steps; ++i)
 			{
 				int seg_last;
 				const int kw0 = step_key(i, seg_last);
 
-				// S^T - m for both 16-key blocks, while V^T converts to fp16.
-				f32x4 sc[2][NB];
-				f16x8 vta[DB];
+				// S^T - m (32 keys x 32 rows), while V^T converts to fp16: keys
+				// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
+				f32x16 sc = c_init;
 #pragma unroll
-				for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-					for (int mb = 0; mb < 2; ++mb)
-					{
-						f32x4 acc = c_init[nb];
-#pragma unroll
-						for (int kk = 0; kk < KK; ++kk)
-						{
-							const int row = 16 * mb + col, slot = 4 * kk + grp;
-							const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + row * HD + 8 * (slot ^ kswz<HD>(row)));
-							acc = mfma16x16x32(a, qhi[nb][kk], acc);
-							acc = mfma16x16x32(a, *q_lo(nb, kk), acc);
-						}
-						sc[mb][nb] = acc;
-					}
-#pragma unroll
-				for (int db = 0; db < DB; ++db)
+				for (int t = 0; t < KT; ++t)
 				{
-					const int seg = 2 * db + ((col & 3) >> 1), half = 4 * (col & 1);
-					const u32x2 lo = tr_read(vt + trow * HD + 8 * (seg ^ vswz<HD>(trow)) + half);
-					const u32x2 hi = tr_read(vt + (trow + 16) * HD + 8 * (seg ^ vswz<HD>(trow + 16)) + half);
-					vta[db] = as_f16x8(bf16x8_to_f16x8(u32x4{lo.x, lo.y, hi.x, hi.y}));
+					const int slot = 2 * t + h;
+					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + r32 * HD + 8 * (slot ^ kswz<HD>(r32)));
+					sc = mfma32x32x16(a, qhi[t], sc);
+					sc = mfma32x32x16(a, *q_lo(t), sc);
 				}
+				f16x8 vta[2][DBK];
+#pragma unroll
+				for (int c = 0; c < 2; ++c)
+#pragma unroll
+					for (int b = 0; b < DBK; ++b)
+					{
+						const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), half = 4 * (ti & 1);
+						const int ra = 16 * c + 4 * h + (ti >> 2), rb = ra + 8;
+						const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + half);
+						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + half);
+						vta[c][b] = as_f16x8(bf16x8_to_f16x8(u32x4{lo.x, lo.y, hi.x, hi.y}));
+					}
 				// Both tiles are read: the next step's rows. A DMA's LDS write is
 				// not ordered after earlier LDS reads still in flight, so those
 				// complete first.
 				lds_reads_done();
 				if (i + 1 < n_steps) load_tiles(i + 1);
 
-				// Mask keys outside a row's span or past the segment (only on steps
-				// that cross an edge).
+				// Mask keys outside the row's span or past the segment (only on
+				// steps that cross an edge).
 				if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
 				{
+					const int hi_key = min(rlast, seg_last);
 #pragma unroll
-					for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-						for (int e = 0; e < 4; ++e)
-						{
-							const int k = kw0 + 16 * mb + 4 * grp + e;
-#pragma unroll
-							for (int nb = 0; nb < NB; ++nb)
-								if (k < rfirst[nb] || k > min(rlast[nb], seg_last)) sc[mb][nb][e] = -INFINITY;
-						}
+					for (int e = 0; e < 16; ++e)
+					{
+						const int k = kw0 + 8 * (e / 4) + 4 * h + (e % 4);
+						if (k < rfirst || k > hi_key) sc[e] = -INFINITY;
+					}
 				}
 
-				// Raise a row's offset when its scores outgrow it by more than
+				// Raise the row's offset when its scores outgrow it by more than
 				// kLazy (or on its first visible key): rare, and O's rescale with it.
-				bool grow = false;
-				float mx[NB];
+				float mx = sc[0];
 #pragma unroll
-				for (int nb = 0; nb < NB; ++nb)
-				{
-					float m = fmaxf(fmaxf(fmaxf(sc[0][nb][0], sc[0][nb][1]), fmaxf(sc[0][nb][2], sc[0][nb][3])),
-					                fmaxf(fmaxf(sc[1][nb][0], sc[1][nb][1]), fmaxf(sc[1][nb][2], sc[1][nb][3])));
-					m = fmaxf(m, __shfl_xor(m, 16));
-					m = fmaxf(m, __shfl_xor(m, 32));
-					mx[nb] = m;
-					grow |= m > kLazy || (m_off[nb] == -INFINITY && m != -INFINITY);
-				}
+				for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+				mx = max_with_other_half(mx);
+				const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
 				if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
 				{
+					const bool fresh = m_off == -INFINITY;
+					const float d = grow ? mx : 0.0f;
+					const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
+					if (grow) m_off = (fresh ? 0.0f : m_off) + d;
+					const float ci = m_off == -INFINITY ? 0.0f : -m_off;
 #pragma unroll
-					for (int nb = 0; nb < NB; ++nb)
-					{
-						const bool fresh = m_off[nb] == -INFINITY;
-						const bool g = mx[nb] > kLazy || (fresh && mx[nb] != -INFINITY);
-						const float d = g ? mx[nb] : 0.0f;
-						const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
-						if (g) m_off[nb] = (fresh ? 0.0f : m_off[nb]) + d;
-						const float ci = m_off[nb] == -INFINITY ? 0.0f : -m_off[nb];
-						c_init[nb] = f32x4{ci, ci, ci, ci};
+					for (int e = 0; e < 16; ++e) c_init[e] = ci;
 #pragma unroll
-						for (int db = 0; db < DB; ++db) acc_o[db][nb] *= alpha;
-						acc_l[nb] *= alpha;
-#pragma unroll
-						for (int mb = 0; mb < 2; ++mb) sc[mb][nb] -= d;
-					}
+					for (int b = 0; b < DBK; ++b) acc_o[b] *= alpha;
+					l_acc *= alpha;
+					sc -= d;
 				}
 
-				// P^T (keys 16h + 4g + e in slot 8g + 4h + e) as the B operand,
-				// one 16-row block at a time.
+				// P^T as the B operand, per 16-key half c (k-slot j holds key
+				// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row sums
+				// from the same fp16 weights.
+				const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
-				for (int nb = 0; nb < NB; ++nb)
+				for (int c = 0; c < 2; ++c)
 				{
-					float w[8];
+					u32x4 pw;
 #pragma unroll
-					for (int e = 0; e < 4; ++e)
+					for (int q = 0; q < 4; ++q)
 					{
-						w[e] = fast_exp2(sc[0][nb][e]);
-						w[4 + e] = fast_exp2(sc[1][nb][e]);
+						// (a scalar copy: clang's bit_cast of a vector element
+						// reads element 0 whatever the index)
+						const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
+						pw[q] = w2;
+						l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
 					}
-					const f16x8 pb = as_f16x8(u32x4{pack_f16x2(w[0], w[1]), pack_f16x2(w[2], w[3]),
-					                                pack_f16x2(w[4], w[5]), pack_f16x2(w[6], w[7])});
+					const f16x8 pb = as_f16x8(pw);
 #pragma unroll
-					for (int db = 0; db < DB; ++db) acc_o[db][nb] = mfma16x16x32(vta[db], pb, acc_o[db][nb]);
-					acc_l[nb] = mfma16x16x32(ones, pb, acc_l[nb]);
+					for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(vta[c][b], pb, acc_o[b]);
 				}
 			}
 
 			// Merge the wavefronts: o = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M),
 			// 0 when no key was seen (reference nn_ops.cpp:492).
-			if (grp == 0)
+			const float l_row = add_with_other_half(l_acc);
+			if (h == 0)
 			{
-#pragma unroll
-				for (int nb = 0; nb < NB; ++nb)
-				{
-					s_m[wave][16 * nb + col] = m_off[nb];
-					s_l[wave][16 * nb + col] = acc_l[nb][0];
-				}
+				s_m[wave][r32] = m_off;
+				s_l[wave][r32] = l_row;
 			}
 			__syncthreads(); // every tile is read (no DMA is left: the last step issues none); s_raw becomes the merge buffer
 			float* s_o = reinterpret_cast<float*>(s_raw);
-#pragma unroll
-			for (int nb = 0; nb < NB; ++nb)
 			{
-				const int r = 16 * nb + col;
-				float M = s_m[0][r];
+				float M = s_m[0][r32];
 #pragma unroll
-				for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][r]);
+				for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][r32]);
 				float L = 0.0f, f_own = 0.0f;
 #pragma unroll
 				for (int w = 0; w < kWaves; ++w)
 				{
-					const float f = s_m[w][r] == -INFINITY ? 0.0f : fast_exp2(s_m[w][r] - M);
-					L = fmaf(s_l[w][r], f, L);
+					const float f = s_m[w][r32] == -INFINITY ? 0.0f : fast_exp2(s_m[w][r32] - M);
+					L = fmaf(s_l[w][r32], f, L);
 					if (w == wave) f_own = f;
 				}
 				const float sc_own = L > 0.0f ? f_own / L : 0.0f;
-				float* orow = s_o + (wave * ROWS + r) * OPITCH + 4 * grp;
+				float* orow = s_o + (wave * kRows + r32) * OPITCH + 4 * h;
 #pragma unroll
-				for (int db = 0; db < DB; ++db)
-				{
-					const f32x4 v = acc_o[db][nb] * sc_own;
-					*reinterpret_cast<float4*>(orow + 16 * db) = make_float4(v[0], v[1], v[2], v[3]);
-				}
+				for (int b = 0; b < DBK; ++b)
+#pragma unroll
+					for (int g = 0; g < 4; ++g)
+						*reinterpret_cast<float4*>(orow + 32 * b + 8 * g) =
+							make_float4(acc_o[b][4 * g] * sc_own, acc_o[b][4 * g + 1] * sc_own, acc_o[b][4 * g + 2] * sc_own,
+							            acc_o[b][4 * g + 3] * sc_own);
 			}
 			__syncthreads();
 			constexpr int Q4 = HD / 4; // float4s per row
-			for (int idx = threadIdx.x; idx < ROWS * Q4; idx += 64 * kWaves)
+			for (int idx = threadIdx.x; idx < kRows * Q4; idx += 64 * kWaves)
 			{
 				const int r = idx / Q4, d4 = idx % Q4;
 				const int gr = row0 + r;
@@ -483,7 +433,7 @@ namespace nnchip
 #pragma unroll
 				for (int w = 1; w < kWaves; ++w)
 				{
-					const float4 v = *reinterpret_cast<const float4*>(s_o + (w * ROWS + r) * OPITCH + 4 * d4);
+					const float4 v = *reinterpret_cast<const float4*>(s_o + (w * kRows + r) * OPITCH + 4 * d4);
 					acc.x += v.x;
 					acc.y += v.y;
 					acc.z += v.z;
@@ -512,10 +462,7 @@ namespace nnchip
 	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream)
 	{
 		if (!bf16) return false;
-		const int rows = 16 * (head_dim == 64    ? prefill_cfg<64>::NB
-		                       : head_dim == 128 ? prefill_cfg<128>::NB
-		                                         : prefill_cfg<256>::NB);
-		p.n_qtiles = (p.n_tok * group + rows - 1) / rows;
+		p.n_qtiles = (p.n_tok * group + kRows - 1) / kRows;
 		switch (head_dim)
 		{
 		case 64: return launch_hd<64>(p, group, stream);

@@ -32,6 +32,39 @@ namespace nnchip
 		return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 	}
 
+	// v_mfma_f32_32x32x16_{bf16,f16}: 8 elements of A and of B per lane, 16
+	// fp32 accumulators per lane (measured on gfx950: one wavefront keeps these
+	// at ~97% of the matrix peak, where 16x16x32 needs two):
+	//   A: lane l holds A[l % 32][8 * (l / 32) + j], j = 0..7   (M x K = 32 x 16)
+	//   B: lane l holds B[8 * (l / 32) + j][l % 32]              (K x N = 16 x 32)
+	//   D: lane l holds D[8 * (i / 4) + 4 * (l / 32) + i % 4][l % 32], i = 0..15
+	typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+	__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c)
+	{
+		return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+	}
+
+	__device__ __forceinline__ f32x16 mfma32x32x16(const f16x8& a, const f16x8& b, const f32x16& c)
+	{
+		return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+	}
+
+	// max(x[l], x[l ^ 32]) on every lane, without LDS: v_permlane32_swap
+	// exchanges one half-wavefront of its two operands, so the two results
+	// hold each lane's value and its partner's (in either order).
+	__device__ __forceinline__ float max_with_other_half(float x)
+	{
+		const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+		return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+	}
+
+	__device__ __forceinline__ float add_with_other_half(float x)
+	{
+		const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+		return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+	}
+
 	__device__ __forceinline__ f16x8 as_f16x8(const uint4& v) { return __builtin_bit_cast(f16x8, v); }
 	__device__ __forceinline__ f16x8 as_f16x8(const u32x4& v) { return __builtin_bit_cast(f16x8, v); }
 
