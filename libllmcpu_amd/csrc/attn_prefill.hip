@@ -8,34 +8,35 @@
 // work-group owns 32 rows and walks its key range in steps of 128 keys,
 // wavefront w taking keys 32w .. 32w + 31 of each step for all 32 rows, so
 // every product is one 32 x 32 tile (v_mfma_f32_32x32x16, which one
-// wavefront keeps near the matrix peak). Each wavefront therefore reads a disjoint quarter of
-// the keys, keeps its own online softmax, and the four partial results merge
-// once, in LDS, at the end.
+// wavefront keeps near the matrix peak). Each wavefront therefore reads a
+// disjoint quarter of the keys, keeps its own online softmax, and the four
+// partial results merge once, in LDS, at the end.
 //
-// Per step, a wavefront's 32 K rows and 32 V rows arrive in its own LDS tiles
-// by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled in
-// 16-byte slots so the reads below are conflict-free), issued during the
-// previous step:
-//   S^T = K . Q^T      v_mfma_f32_16x16x32_bf16, K rows as the A operand and
-//                      Q^T as B, split into bf16 hi + lo so the product
-//                      against the exact bf16 K is near-fp32. The
-//                      accumulator starts at -m (the row's running offset),
-//                      so the scores come out already shifted. Meanwhile the
-//                      VALU reads V^T back transposed (ds_read_b64_tr_b16)
-//                      and converts it to fp16 (exact up to 65504; larger
-//                      magnitudes saturate there); then both tiles are free
-//                      and the next step's loads go out;
-//   softmax            in fp32 and log2 units (Q is pre-scaled by
-//                      scale * log2 e). The offset m is raised only when a
-//                      row's scores exceed it by more than 8, so weights stay
-//                      in (0, 256] and the O rescale is rare;
-//   O^T += V^T . P^T   v_mfma_f32_16x16x32_f16 with P (fp16, rounded to
+// The work-group first stages its Q rows through LDS (each thread loads one
+// eighth of a row once, pre-scaled into log2 units and split into bf16 hi +
+// lo); every wavefront keeps the hi half of its B operand in registers and
+// reads the lo half from LDS. Per step, a wavefront's 32 K rows and 32 V rows
+// arrive in its own LDS tiles by LDS-DMA (buffer_load ... lds, 16 bytes per
+// lane, rows XOR-swizzled in 16-byte slots so the reads below are
+// conflict-free), issued during the previous step:
+//   S^T = K . Q^T      v_mfma_f32_32x32x16_bf16, K rows as the A operand and
+//                      Q^T as B, hi and lo, so the product against the exact
+//                      bf16 K is near-fp32. The accumulator starts at -m (the
+//                      row's running offset), so the scores come out already
+//                      shifted. Meanwhile the VALU reads V^T back transposed
+//                      (ds_read_b64_tr_b16) and converts it to fp16 (exact up
+//                      to 65504; larger magnitudes saturate there); then both
+//                      tiles are free and the next step's loads go out;
+//   softmax            in fp32 and log2 units. The offset m is raised only
+//                      when a row's scores exceed it by more than 8, so
+//                      weights stay in (0, 256] and the O rescale is rare; the
+//                      two halves of a row's 32 scores meet through
+//                      v_permlane32_swap;
+//   O^T += V^T . P^T   v_mfma_f32_32x32x16_f16 with P (fp16, rounded to
 //                      nearest) as the B operand straight from the score
-//                      registers (key order permuted to match), one 16-row
-//                      block at a time so the next block's exp overlaps the
-//                      MFMAs. The row sums l come from the same rounded P
-//                      through one more MFMA against a block of ones, so
-//                      numerator and denominator see identical weights.
+//                      registers (key order permuted to match). The row sums
+//                      l come from the same rounded P through v_dot2_f32_f16,
+//                      so numerator and denominator see identical weights.
 // K/V are read through buffer descriptors whose range check returns zeros
 // for rows past the key range without touching memory; a range that wraps a
 // ring buffer is walked as two contiguous segments. Masking is applied only
@@ -49,40 +50,37 @@ namespace nnchip
 {
 	namespace
 	{
-		constexpr int kWaves = 4; // wavefronts per work-group
-		constexpr int kWK = 32; // keys per wavefront per step
+		constexpr int kWaves = 4; // wavefronts per work-group (key quarters of a step)
+		constexpr int kWK = 32; // keys per wavefront per step (one MFMA tile)
 		constexpr int kStep = kWaves * kWK; // keys per work-group step
+		constexpr int kRows = 32; // rows per work-group
 		constexpr float kLazy = 8.0f; // max growth of a row's scores over its offset, log2 units
 		constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3: raw 32-bit data
 
-		constexpr int kRows = 32; // rows per work-group: one 32-wide N tile
-
-		// Wavefronts per SIMD: two where a wavefront fits in 256 registers, so
-		// one wavefront's VALU work and loads overlap the other's MFMAs.
-		template <int HD>
-		constexpr int prefill_wpe()
-		{
-			return HD == 256 ? 1 : 2;
-		}
-
+		// LDS: the wavefronts' K and V tiles, Q's lo half, Q's hi half (staged
+		// once, then the merge's row statistics); the merge buffer reuses the
+		// tiles and the lo half. At head_dim 128 this is 80 KiB, so two
+		// work-groups (two wavefronts per SIMD) share a CU.
 		template <int HD>
 		struct prefill_shape
 		{
+			static constexpr int WPE = HD == 256 ? 1 : 2; // wavefronts per SIMD
 			static constexpr int KT = HD / 16; // QK MFMAs per Q half (16 elements of d each)
 			static constexpr int DBK = HD / 32; // 32-row d blocks of O^T
 			static constexpr int LPK = HD / 8; // lanes per tile row (16 bytes each)
 			static constexpr int KPL = 64 / LPK; // tile rows per DMA
 			static constexpr int NV = kWK / KPL; // DMAs per tile per step
 			static constexpr int OPITCH = HD + 4; // floats per row in the final merge
-			static constexpr int QPITCH = HD + 8; // bf16 per row of Q's lo half in LDS
-			static constexpr int kTile = kWK * HD * 2; // bytes of one wavefront's K (or V) tile
-			static constexpr int kVBytes = kWaves * kTile;
-			static constexpr int kKBytes = kWaves * kTile;
-			static constexpr int kQBytes = kRows * QPITCH * 2;
+			static constexpr int kTile = kWK * HD * 2; // bytes of one K (or V) tile
+			static constexpr int kTiles = kWaves * 2 * kTile;
+			static constexpr int kQ = kRows * HD * 2; // bytes of one bf16 half of Q
+			static constexpr int kQlo = kTiles; // offsets
+			static constexpr int kQhi = kTiles + kQ;
+			static constexpr int kLds = kTiles + 2 * kQ;
 			static constexpr int kOBytes = kWaves * kRows * OPITCH * 4;
-			static constexpr int kLoop = kVBytes + kKBytes + kQBytes;
-			static constexpr int kLds = kLoop > kOBytes ? kLoop : kOBytes;
 			static_assert(NV >= 1 && KPL * NV == kWK, "unsupported prefill shape");
+			static_assert(kOBytes <= kQhi && 2 * kWaves * kRows * 4 <= kQ, "merge buffer layout");
+			static_assert(kLds <= 160 * 1024, "prefill LDS budget");
 		};
 
 		// Two 16-bit halves of one row of O^T's A operand: lane (g, c) of the
@@ -96,13 +94,14 @@ namespace nnchip
 			return __builtin_bit_cast(u32x2, v);
 		}
 
-		// 16-byte slot swizzle of row `row` of a V tile (an even XOR, so a
-		// 32-byte pair stays together): the transposing reads of four (and
-		// eight) consecutive rows at one element offset land in distinct banks.
+		// 16-byte slot swizzle of row `row` of a V tile, in whole 64-byte
+		// groups: a half-wavefront's transposing reads cover one 64-byte
+		// segment of each of four consecutive rows, which land in distinct
+		// banks.
 		template <int HD>
 		__device__ __forceinline__ int vswz(int row)
 		{
-			return HD == 64 ? 2 * ((row >> 1) & 3) : 2 * (row & 7);
+			return HD == 64 ? 4 * ((row >> 1) & 1) : 4 * (row & 3);
 		}
 
 		// 16-byte slot swizzle of row `row` of a K tile: the A-operand reads of
@@ -133,6 +132,19 @@ namespace nnchip
 			__builtin_amdgcn_sched_barrier(0);
 		}
 
+		// Waits until this wavefront's LDS-DMA loads have landed (s_waitcnt
+		// vmcnt(0); expcnt and lgkmcnt at their maximum, i.e. not waited on:
+		// gfx9 encoding vmcnt[3:0] = 0, expcnt[6:4] = 7, lgkmcnt[11:8] = 0xf,
+		// vmcnt[15:14] = 0). The compiler's own tracking of LDS-DMA writes
+		// does not reliably order later LDS reads of the same tile after them,
+		// so every step waits explicitly. Nothing is scheduled across it.
+		__device__ __forceinline__ void dma_done()
+		{
+			__builtin_amdgcn_sched_barrier(0);
+			__builtin_amdgcn_s_waitcnt(0x0F70);
+			__builtin_amdgcn_sched_barrier(0);
+		}
+
 		// Eight bf16 -> eight fp16, exact up to 65504.
 		__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& b)
 		{
@@ -142,17 +154,13 @@ namespace nnchip
 
 		template <int HD, int G>
 		__global__ __launch_bounds__(64 * kWaves)
-			__attribute__((amdgpu_waves_per_eu(prefill_wpe<HD>(), prefill_wpe<HD>()))) void prefill_kernel(
+			__attribute__((amdgpu_waves_per_eu(prefill_shape<HD>::WPE, prefill_shape<HD>::WPE))) void prefill_kernel(
 				const prefill_params p)
 		{
 			using S = prefill_shape<HD>;
-			constexpr int KT = S::KT, DBK = S::DBK, LPK = S::LPK, KPL = S::KPL, NV = S::NV, OPITCH = S::OPITCH,
-			              QPITCH = S::QPITCH;
+			constexpr int KT = S::KT, DBK = S::DBK, LPK = S::LPK, KPL = S::KPL, NV = S::NV, OPITCH = S::OPITCH;
 
-			// K and V tiles and Q's lo half during the key loop, then the merge buffer.
 			__shared__ __attribute__((aligned(16))) unsigned char s_raw[S::kLds];
-			__shared__ float s_m[kWaves][kRows];
-			__shared__ float s_l[kWaves][kRows];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps step control scalar
@@ -160,13 +168,16 @@ namespace nnchip
 			const int h = lane >> 5; // which half of an MFMA's k range this lane holds
 
 			// Work-groups of one KV head run on one XCD (blockIdx.x % 8 picks
-			// the XCD), so its K/V rows are shared through that XCD's L2; within
-			// a head, the query tiles with the most keys start first.
+			// the XCD), so its K/V rows are shared through that XCD's L2. Within
+			// a head the first half of the work-groups take the query tiles with
+			// the most keys, heaviest first, and the second half the lightest
+			// first, so the two that share a CU carry about equal work.
 			int bid = blockIdx.x;
 			const int n_wg = gridDim.x;
 			if ((n_wg & 7) == 0) bid = (bid & 7) * (n_wg >> 3) + (bid >> 3);
 			const int kvh = bid / p.n_qtiles;
-			const int qt = p.n_qtiles - 1 - bid % p.n_qtiles;
+			const int j = bid % p.n_qtiles, half = (p.n_qtiles + 1) / 2;
+			const int qt = j < half ? p.n_qtiles - 1 - j : j - half;
 
 			const int n_rows = p.n_tok * G;
 			const int row0 = qt * kRows;
@@ -228,61 +239,71 @@ namespace nnchip
 			// bytes at l * 16, i.e. row j KPL + l / LPK, slot l % LPK, which holds
 			// the row's 16-byte segment (l % LPK) ^ swizzle(row).
 			const int t_row = lane / LPK;
-			uint16_t* vt = reinterpret_cast<uint16_t*>(s_raw) + wave * kWK * HD;
-			uint16_t* kt = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes) + wave * kWK * HD;
+			uint16_t* kt = reinterpret_cast<uint16_t*>(s_raw) + wave * 2 * kWK * HD;
+			uint16_t* vt = kt + kWK * HD;
 			auto load_tiles = [&](int i) __attribute__((always_inline))
 			{
 				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
 				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
 #pragma unroll
-				for (int j = 0; j < NV; ++j)
+				for (int jj = 0; jj < NV; ++jj)
 				{
-					const int row = j * KPL + t_row;
+					const int row = jj * KPL + t_row;
 					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					load_lds16(rk, kt + j * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
-					load_lds16(rv, vt + j * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
+					load_lds16(rk, kt + jj * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
+					load_lds16(rv, vt + jj * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
 				}
 			};
 			// The first step's tiles go out before Q is read, so the latencies overlap.
 			if (n_steps > 0) load_tiles(0);
 
-			// Q^T as the B operand (lane l: row l % 32, elements 16 t + 8 h .. + 8),
-			// pre-scaled into log2 units, bf16 hi + lo: the hi half in registers,
-			// the lo half in LDS at the address the same lane reads it back from.
-			bf16x8 qhi[KT];
-			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kVBytes + S::kKBytes);
-			auto q_lo = [&](int t) __attribute__((always_inline)) -> bf16x8*
+			// Q, pre-scaled into log2 units, as bf16 hi + lo in LDS, in the K
+			// tiles' layout (row r, 16-byte slot s at s ^ kswz(r)): thread t
+			// converts the eighth t % 8 of row t / 8.
+			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kQlo);
+			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + S::kQhi);
 			{
-				return reinterpret_cast<bf16x8*>(s_qlo + r32 * QPITCH + 16 * t + 8 * h);
-			};
-			{
-				const bool ok = my_row < n_rows;
-				const float* qp = p.q + (ok ? static_cast<size_t>(my_row / G) * q_stride +
-				                                  static_cast<size_t>(kvh * G + my_row % G) * HD
+				constexpr int E = HD / 8; // elements per thread
+				const int r = threadIdx.x >> 3, seg = threadIdx.x & 7;
+				const int grow = row0 + r;
+				const bool ok = grow < n_rows;
+				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
+				                                  static_cast<size_t>(kvh * G + grow % G) * HD + seg * E
 				                            : 0);
 #pragma unroll
-				for (int t = 0; t < KT; ++t)
+				for (int c = 0; c < E / 8; ++c)
 				{
 					float x[8];
 					if (ok)
 					{
-						const float4 a = *reinterpret_cast<const float4*>(qp + 16 * t + 8 * h);
-						const float4 b = *reinterpret_cast<const float4*>(qp + 16 * t + 8 * h + 4);
+						const float4 a = *reinterpret_cast<const float4*>(qp + 8 * c);
+						const float4 b = *reinterpret_cast<const float4*>(qp + 8 * c + 4);
 						x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
 						x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 #pragma unroll
-						for (int j = 0; j < 8; ++j) x[j] *= p.qscale;
+						for (int e = 0; e < 8; ++e) x[e] *= p.qscale;
 					}
 					else
 					{
 #pragma unroll
-						for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+						for (int e = 0; e < 8; ++e) x[e] = 0.0f;
 					}
-					bf16x8 lo;
-					split_bf16x8(x, qhi[t], lo);
-					*q_lo(t) = lo;
+					bf16x8 hi, lo;
+					split_bf16x8(x, hi, lo);
+					const int off = r * HD + 8 * ((seg * (E / 8) + c) ^ kswz<HD>(r));
+					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
+					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
 				}
 			}
+			__syncthreads();
+			// Q^T as the B operand: lane l holds row l % 32, elements 16 t + 8 h .. + 8.
+			auto q_slot = [&](int t) __attribute__((always_inline)) -> int
+			{
+				return r32 * HD + 8 * ((2 * t + h) ^ kswz<HD>(r32));
+			};
+			bf16x8 qhi[KT];
+#pragma unroll
+			for (int t = 0; t < KT; ++t) qhi[t] = *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t));
 
 			f32x16 acc_o[DBK]; // O^T: lane l holds d = 32 b + 8 (i / 4) + 4 h + i % 4 of row l % 32
 			float l_acc = 0.0f; // this lane's half of its row's sum of weights
@@ -297,11 +318,13 @@ namespace nnchip
 			// V^T read position of this lane: a 16-lane group q covers elements
 			// 32 b + 16 (q & 1) .. + 16 of four tile rows 16 c + 4 h (+ 8).
 			const int tq = (lane >> 4) & 1, ti = lane & 15;
+			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
 			for (int i = 0; i < n_steps; ++i)
 			{
 				int seg_last;
 				const int kw0 = step_key(i, seg_last);
+				dma_done(); // this step's tiles have landed
 
 				// S^T - m (32 keys x 32 rows), while V^T converts to fp16: keys
 				// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
@@ -309,10 +332,9 @@ namespace nnchip
 #pragma unroll
 				for (int t = 0; t < KT; ++t)
 				{
-					const int slot = 2 * t + h;
-					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + r32 * HD + 8 * (slot ^ kswz<HD>(r32)));
+					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
 					sc = mfma32x32x16(a, qhi[t], sc);
-					sc = mfma32x32x16(a, *q_lo(t), sc);
+					sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
 				}
 				f16x8 vta[2][DBK];
 #pragma unroll
@@ -320,10 +342,10 @@ namespace nnchip
 #pragma unroll
 					for (int b = 0; b < DBK; ++b)
 					{
-						const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), half = 4 * (ti & 1);
+						const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), hf = 4 * (ti & 1);
 						const int ra = 16 * c + 4 * h + (ti >> 2), rb = ra + 8;
-						const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + half);
-						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + half);
+						const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + hf);
+						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + hf);
 						vta[c][b] = as_f16x8(bf16x8_to_f16x8(u32x4{lo.x, lo.y, hi.x, hi.y}));
 					}
 				// Both tiles are read: the next step's rows. A DMA's LDS write is
@@ -370,7 +392,6 @@ namespace nnchip
 				// P^T as the B operand, per 16-key half c (k-slot j holds key
 				// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row sums
 				// from the same fp16 weights.
-				const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
 				for (int c = 0; c < 2; ++c)
 				{
@@ -391,25 +412,33 @@ namespace nnchip
 			}
 
 			// Merge the wavefronts: o = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M),
-			// 0 when no key was seen (reference nn_ops.cpp:492).
+			// 0 when no key was seen (reference nn_ops.cpp:492). The row
+			// statistics take the place of Q's hi half, the partial results that
+			// of the tiles.
+			float* s_m = reinterpret_cast<float*>(s_raw + S::kQhi); // [kWaves][kRows]
+			float* s_l = s_m + kWaves * kRows;
 			const float l_row = add_with_other_half(l_acc);
+			// Every wavefront has left the key loop: the tiles are read (no DMA
+			// is left: the last step issues none) and so is Q's hi half.
+			__syncthreads();
 			if (h == 0)
 			{
-				s_m[wave][r32] = m_off;
-				s_l[wave][r32] = l_row;
+				s_m[wave * kRows + r32] = m_off;
+				s_l[wave * kRows + r32] = l_row;
 			}
-			__syncthreads(); // every tile is read (no DMA is left: the last step issues none); s_raw becomes the merge buffer
+			__syncthreads();
 			float* s_o = reinterpret_cast<float*>(s_raw);
 			{
-				float M = s_m[0][r32];
+				float M = s_m[r32];
 #pragma unroll
-				for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][r32]);
+				for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w * kRows + r32]);
 				float L = 0.0f, f_own = 0.0f;
 #pragma unroll
 				for (int w = 0; w < kWaves; ++w)
 				{
-					const float f = s_m[w][r32] == -INFINITY ? 0.0f : fast_exp2(s_m[w][r32] - M);
-					L = fmaf(s_l[w][r32], f, L);
+					const float mw = s_m[w * kRows + r32];
+					const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+					L = fmaf(s_l[w * kRows + r32], f, L);
 					if (w == wave) f_own = f;
 				}
 				const float sc_own = L > 0.0f ? f_own / L : 0.0f;
