@@ -14,8 +14,8 @@
 //
 // The work-group first stages its Q rows through LDS (each thread loads one
 // eighth of a row once, pre-scaled into log2 units and split into bf16 hi +
-// lo); every wavefront keeps the hi half of its B operand in registers and
-// reads the lo half from LDS. Per step, a wavefront's 32 K rows and 32 V rows
+// lo); every wavefront then keeps both halves of its B operand in registers
+// (at head_dim 256 it reads them from LDS). Per step, a wavefront's 32 K rows and 32 V rows
 // arrive in its own LDS tiles by LDS-DMA (buffer_load ... lds, 16 bytes per
 // lane, rows XOR-swizzled in 16-byte slots so the reads below are
 // conflict-free), issued during the previous step:
@@ -65,6 +65,9 @@ namespace nnchip
 		struct prefill_shape
 		{
 			static constexpr int WPE = HD == 256 ? 1 : 2; // wavefronts per SIMD
+			// Q's B operand (hi and lo halves) held in registers; at head_dim 256
+			// it would not fit beside the accumulators, and is read from LDS.
+			static constexpr bool QREG = HD != 256;
 			static constexpr int KT = HD / 16; // QK MFMAs per Q half (16 elements of d each)
 			static constexpr int DBK = HD / 32; // 32-row d blocks of O^T
 			static constexpr int LPK = HD / 8; // lanes per tile row (16 bytes each)
@@ -301,9 +304,16 @@ namespace nnchip
 			{
 				return r32 * HD + 8 * ((2 * t + h) ^ kswz<HD>(r32));
 			};
-			bf16x8 qhi[KT];
+			bf16x8 qhi[S::QREG ? KT : 1], qlo[S::QREG ? KT : 1];
+			if constexpr (S::QREG)
+			{
 #pragma unroll
-			for (int t = 0; t < KT; ++t) qhi[t] = *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t));
+				for (int t = 0; t < KT; ++t)
+				{
+					qhi[t] = *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t));
+					qlo[t] = *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t));
+				}
+			}
 
 			f32x16 acc_o[DBK]; // O^T: lane l holds d = 32 b + 8 (i / 4) + 4 h + i % 4 of row l % 32
 			float l_acc = 0.0f; // this lane's half of its row's sum of weights
@@ -333,8 +343,16 @@ namespace nnchip
 				for (int t = 0; t < KT; ++t)
 				{
 					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
-					sc = mfma32x32x16(a, qhi[t], sc);
-					sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
+					if constexpr (S::QREG)
+					{
+						sc = mfma32x32x16(a, qhi[t], sc);
+						sc = mfma32x32x16(a, qlo[t], sc);
+					}
+					else
+					{
+						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
+						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
+					}
 				}
 				f16x8 vta[2][DBK];
 #pragma unroll
