@@ -52,6 +52,31 @@ namespace nnchip
 	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream);
 
 	// F32 rows -> the cache's element type, row (pos0 + t) % rows.
+	constexpr int kPrepMaxPairs = 256; // RoPE pairs per head (head_dim up to 512)
+
+	// The pre-attention step of one batch (reference model.cpp:1616-1691).
+	struct prep_params
+	{
+		float* q; // [n_tok][n_head * head_dim], normalised and rotated in place
+		const float* k; // [n_tok][kv_dim]
+		const float* v; // [n_tok][kv_dim]
+		void* K; // the layer's buffers: [rows][kv_dim], BF16 bits or F32
+		void* V;
+		const float* q_gamma; // head_dim floats, or null: no Q norm
+		const float* k_gamma; // head_dim floats, or null: no K norm
+		const float* freq_factors; // n_rot / 2 floats, or null
+		int n_head, n_kv, head_dim, rows, pos0, bf16;
+		int v_norm; // RMS-normalise V per head, no gamma
+		int n_rot; // rotated lanes per head (even); 0: no RoPE
+		int mode; // 0 NEOX, 1 NORM
+		float eps, pos_scale;
+		float inv[kPrepMaxPairs]; // base^(-2i/n_rot), accumulated in fp32 as the reference does
+	};
+
+	// Launches the pre-attention step over an (n_head + 2 n_kv, n_tok) grid of
+	// head rows; false for a head_dim or n_rot outside the supported range.
+	bool launch_prep(const prep_params& p, int n_tok, hipStream_t stream);
+
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
 	                       int n_tok, bool bf16, hipStream_t stream);
 

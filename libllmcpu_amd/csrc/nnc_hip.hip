@@ -401,6 +401,66 @@ nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos
 	return NNC_OK;
 }
 
+nnc_status nnc_hip_kv_prep_append_device(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, float* q,
+                                         const float* k, const float* v, const nnc_hip_prep* prep)
+{
+	if (nnc_status s = check_kv(kv, buf)) return s;
+	if (!q || !k || !v || !prep) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL q, k, v or parameters");
+	const kv_buffer& b = kv->bufs[buf];
+	if (n_tok <= 0 || pos0 < 0) return fail(NNC_ERR_INVALID_ARGUMENT, "n_tok %d, pos0 %d", n_tok, pos0);
+	if (n_tok > b.rows)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "%d tokens overwrite each other in a buffer of %d rows", n_tok, b.rows);
+	const nnc_hip_prep& pr = *prep;
+	if (pr.n_head <= 0 || pr.n_kv <= 0 || pr.head_dim <= 0)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "n_head %d, n_kv %d, head_dim %d", pr.n_head, pr.n_kv, pr.head_dim);
+	if (static_cast<long long>(pr.n_kv) * pr.head_dim != b.kv_dim)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "n_kv * head_dim = %lld, buffer kv_dim %d",
+		            static_cast<long long>(pr.n_kv) * pr.head_dim, b.kv_dim);
+	if (pr.n_rot < 0 || pr.n_rot % 2 != 0 || pr.n_rot > pr.head_dim)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "n_rot %d (even, at most head_dim %d)", pr.n_rot, pr.head_dim);
+	if (pr.rope_mode != 0 && pr.rope_mode != 1) return fail(NNC_ERR_INVALID_ARGUMENT, "rope_mode %d", pr.rope_mode);
+	if (pr.n_rot > 0 && !(pr.freq_base > 0.0f)) return fail(NNC_ERR_INVALID_ARGUMENT, "freq_base %g", pr.freq_base);
+	if (pr.head_dim > 2 * nnchip::kPrepMaxPairs)
+		return fail(NNC_ERR_UNSUPPORTED_MODEL, "head_dim %d above %d", pr.head_dim, 2 * nnchip::kPrepMaxPairs);
+
+	nnchip::prep_params p{};
+	p.q = q;
+	p.k = k;
+	p.v = v;
+	p.K = b.k;
+	p.V = b.v;
+	p.q_gamma = pr.q_gamma;
+	p.k_gamma = pr.k_gamma;
+	p.freq_factors = pr.freq_factors;
+	p.n_head = pr.n_head;
+	p.n_kv = pr.n_kv;
+	p.head_dim = pr.head_dim;
+	p.rows = b.rows;
+	p.pos0 = pos0;
+	p.bf16 = kv->bf16 ? 1 : 0;
+	p.v_norm = pr.v_norm ? 1 : 0;
+	p.n_rot = pr.n_rot;
+	p.mode = pr.rope_mode;
+	p.eps = pr.rms_eps;
+	p.pos_scale = pr.pos_scale;
+	// The reference's frequency schedule (nn_ops.cpp:1840-1851): the ratio
+	// base^(-2/n_rot) in fp32, multiplied in step by step.
+	if (pr.n_rot > 0)
+	{
+		const float ratio = std::pow(pr.freq_base, -2.0f / static_cast<float>(pr.n_rot));
+		float inv = 1.0f;
+		for (int i = 0; i < pr.n_rot / 2; ++i)
+		{
+			p.inv[i] = inv;
+			inv *= ratio;
+		}
+	}
+	if (!nnchip::launch_prep(p, n_tok, kv->stream))
+		return fail(NNC_ERR_UNSUPPORTED_MODEL, "no pre-attention kernel for head_dim %d", pr.head_dim);
+	NNC_HIP_TRY(hipGetLastError(), "pre-attention step");
+	return NNC_OK;
+}
+
 nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_rows, void* k_out, void* v_out)
 {
 	if (nnc_status s = check_kv(kv, buf)) return s;

@@ -61,6 +61,14 @@ _F = C.c_float
 _B = C.c_bool
 _U64 = C.c_uint64
 
+class NncHipPrep(C.Structure):
+    """struct nnc_hip_prep of include/nnc_hip.h (pointers are device addresses)."""
+
+    _fields_ = [("n_head", _I), ("n_kv", _I), ("head_dim", _I), ("q_gamma", _P), ("k_gamma", _P), ("v_norm", _I),
+                ("rms_eps", _F), ("n_rot", _I), ("freq_base", _F), ("pos_scale", _F), ("rope_mode", _I),
+                ("freq_factors", _P)]
+
+
 # name: (restype, argtypes) for every function include/nnc_hip.h declares.
 SIGNATURES = {
     "nnc_hip_kv_create": (C.c_int, [_I, C.POINTER(_I), C.POINTER(_I), _B, C.POINTER(_P)]),
@@ -69,6 +77,7 @@ SIGNATURES = {
     "nnc_hip_kv_append": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_kv_append_f32": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_kv_append_f32_device": (C.c_int, [_P, _I, _I, _I, _P, _P]),
+    "nnc_hip_kv_prep_append_device": (C.c_int, [_P, _I, _I, _I, _P, _P, _P, C.POINTER(NncHipPrep)]),
     "nnc_hip_kv_read": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_attend": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_device": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
@@ -243,6 +252,44 @@ class KVCache:
             n_seq = pos0 + n_tok
         _check(self._lib.nnc_hip_attend_device(self.handle, buf, q_dev, out_dev, n_tok, pos0, n_seq, window,
                                                bool(causal), n_head, n_kv, head_dim, float(scale)))
+
+    def prep_append_device(self, buf: int, q_dev: int, k_dev: int, v_dev: int, *, pos0: int, n_tok: int,
+                           prep: NncHipPrep) -> None:
+        """Per-head norms, RoPE and the K/V append of a batch whose q/k/v are in
+        device memory (q updated in place); queued on the cache's stream."""
+        _check(self._lib.nnc_hip_kv_prep_append_device(self.handle, buf, pos0, n_tok, q_dev, k_dev, v_dev,
+                                                       C.byref(prep)))
+
+    def prep_append(self, buf: int, q: np.ndarray, k: np.ndarray, v: np.ndarray, *, pos0: int, n_head: int, n_kv: int,
+                    head_dim: int, q_gamma: np.ndarray | None = None, k_gamma: np.ndarray | None = None,
+                    v_norm: bool = False, eps: float = 1e-6, n_rot: int = 0, base: float = 10000.0,
+                    pos_scale: float = 1.0, mode: int = 0, freq_factors: np.ndarray | None = None) -> np.ndarray:
+        """prep_append_device from host arrays (uploaded to scratch device
+        memory, freed afterwards); returns the normalised, rotated q."""
+        from . import hip_rt
+
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        arrays = [q, np.ascontiguousarray(k, dtype=np.float32), np.ascontiguousarray(v, dtype=np.float32)]
+        extras = [q_gamma, k_gamma, freq_factors]
+        ptrs, dev = [], []
+        try:
+            for a in arrays + [None if e is None else np.ascontiguousarray(e, dtype=np.float32) for e in extras]:
+                if a is None:
+                    ptrs.append(None)
+                    continue
+                d = hip_rt.malloc(max(a.nbytes, 4))
+                dev.append(d)
+                hip_rt.to_device(d, a)
+                ptrs.append(d)
+            prep = NncHipPrep(n_head, n_kv, head_dim, ptrs[3], ptrs[4], int(bool(v_norm)), eps, n_rot, base, pos_scale,
+                              mode, ptrs[5])
+            n_tok = q.size // (n_head * head_dim)
+            self.prep_append_device(buf, ptrs[0], ptrs[1], ptrs[2], pos0=pos0, n_tok=n_tok, prep=prep)
+            self.sync()
+            return hip_rt.to_host(np.empty_like(q), ptrs[0])
+        finally:
+            for d in dev:
+                hip_rt.free(d)
 
     def sync(self) -> None:
         _check(self._lib.nnc_hip_kv_sync(self.handle))

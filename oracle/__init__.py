@@ -64,7 +64,10 @@ class _Lib:
         f("attn_span", None, [_I, _I, _I, _I, C.POINTER(_I), C.POINTER(_I)])
         f("bf16_round", None, [_P, _P, _SZ])
         f("rope", None, [_P, _I, _I, _I, _F, _F, _I])
+        f("rope_ff", None, [_P, _I, _I, _I, _F, _F, _I, _P])
         f("rmsnorm_groups", None, [_P, _SZ, _SZ, _F])
+        f("rmsnorm_gamma", None, [_P, _SZ, _SZ, _P, _F])
+        f("rmsnorm_plain", None, [_P, _SZ, _SZ, _F])
 
     def _fn(self, name, res, args):
         fn = getattr(self.lib, self.prefix + name)
@@ -116,6 +119,26 @@ class _Lib:
         self._rmsnorm_groups(_p(x), x.size // dim, dim, eps)
         return x
 
+    def rope_ff(self, x, n_heads, head_dim, n_rot, pos, base, mode, freq_factors=None):
+        """RoPE with per-pair frequency factors (None: none)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        self._rope_ff(_p(x), n_heads, head_dim, n_rot, pos, base, mode, _p(ff))
+        return x
+
+    def rmsnorm_gamma(self, x, dim, gamma=None, eps=1e-6):
+        """Per-group RMSNorm with a learned gamma (None: ones)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        g = np.ones(dim, np.float32) if gamma is None else np.ascontiguousarray(gamma, dtype=np.float32)
+        self._rmsnorm_gamma(_p(x), x.size // dim, dim, _p(g), eps)
+        return x
+
+    def rmsnorm_plain(self, x, dim, eps=1e-6):
+        """Per-group RMSNorm without gamma (the V norm of Gemma 4)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).copy()
+        self._rmsnorm_plain(_p(x), x.size // dim, dim, eps)
+        return x
+
 
 def _layer_call(fn, extra, q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale):
     q = np.ascontiguousarray(q, dtype=np.float32)
@@ -146,6 +169,8 @@ class Oracle(_Lib):
         self._fn("f32_from_bf16", _F, [C.c_uint16])
         self._fn("bf16_from_f32", C.c_uint16, [_F])
         self._fn("ref_fixture_attn_blocks", _I, [_I, _P, _P, _P])
+        self._fn("prep_append", None, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _F, _I, _F, _F, _I, _P, _I, _I, _I, _P,
+                                       _P])
 
     def attend_layer(self, q, K, V, *, kv_bf16, rows, pos0, n_seq=None, window=0, causal=True, n_head, n_kv,
                      head_dim, scale, threads=8):
@@ -158,6 +183,25 @@ class Oracle(_Lib):
         """Double-precision softmax attention per query head over its span."""
         return _layer_call(self._textbook_attend, [], q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head,
                            n_kv, head_dim, scale)
+
+    def prep_append(self, q, k, v, K, V, *, n_head, n_kv, head_dim, pos0, kv_bf16, q_gamma=None, k_gamma=None,
+                    v_norm=False, eps=1e-6, n_rot=0, base=10000.0, pos_scale=1.0, mode=0, freq_factors=None):
+        """Per-head norms, RoPE and the K/V append of one batch (reference
+        model.cpp:1616-1691). q, k, v: [n_tok][heads * head_dim] fp32; K, V: the
+        layer's buffers ([rows][kv_dim], uint16 BF16 bits or fp32), copied and
+        returned with the new rows. Returns (q, K, V)."""
+        q = np.ascontiguousarray(q, dtype=np.float32).copy()
+        k = np.ascontiguousarray(k, dtype=np.float32).copy()
+        v = np.ascontiguousarray(v, dtype=np.float32).copy()
+        K = np.ascontiguousarray(K).copy()
+        V = np.ascontiguousarray(V).copy()
+        n_tok = q.size // (n_head * head_dim)
+        qg = None if q_gamma is None else np.ascontiguousarray(q_gamma, dtype=np.float32)
+        kg = None if k_gamma is None else np.ascontiguousarray(k_gamma, dtype=np.float32)
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        self._prep_append(_p(q), _p(k), _p(v), n_tok, n_head, n_kv, head_dim, _p(qg), _p(kg), int(v_norm), eps, n_rot,
+                          base, pos_scale, mode, _p(ff), pos0, K.shape[0], int(kv_bf16), _p(K), _p(V))
+        return q, K, V
 
     def kv_rows(self, n_ctx, window, n_batch):
         return self._kv_rows(n_ctx, window, n_batch)

@@ -11,8 +11,12 @@
 //   orc_attn_span                          reference src/libnnc/model.cpp:2300-2316
 //   orc_kv_rows / orc_max_rewind           reference src/libnnc/model.cpp:1936-1957
 //   orc_attend_layer                       reference src/libnnc/model.cpp:1229-1317, 1693-1757
-//   orc_rope                               reference src/libnnc/nn_ops.cpp:1830-1873
+//   orc_rope / orc_rope_ff                 reference src/libnnc/nn_ops.cpp:1830-1873
 //   orc_rmsnorm_groups                     reference src/libnnc/nn_ops.cpp:590-632 (gamma = 1)
+//   orc_rmsnorm_gamma                      reference src/libnnc/nn_ops.cpp:590-632
+//   orc_rmsnorm_plain                      reference src/libnnc/nn_ops.cpp:558-588
+//   orc_prep_append                        reference src/libnnc/model.cpp:1616-1691 (per-head
+//                                          Q/K/V norms, RoPE on Q and K, K/V append)
 // and two checkers that are not restatements:
 //   orc_textbook_attend   double-precision softmax attention per query, the
 //                         scalar reference of reference src/appnnc/tests.cpp:2424-2446
@@ -297,9 +301,10 @@ void orc_textbook_attend(const float* q, float* out, const void* K, const void* 
 }
 
 // Rotary embedding of n_heads vectors of head_dim floats at position pos:
-// angle_i = pos * base^(-2i/n_rot), the per-step ratio accumulated in fp32;
-// mode 0 (NEOX) pairs lanes i and i + n_rot/2, mode 1 (NORM) lanes 2i and 2i+1.
-void orc_rope(float* x, int n_heads, int head_dim, int n_rot, float pos, float base, int mode)
+// angle_i = pos * base^(-2i/n_rot) (divided by freq_factors[i] when given),
+// the per-step ratio accumulated in fp32; mode 0 (NEOX) pairs lanes i and
+// i + n_rot/2, mode 1 (NORM) lanes 2i and 2i+1; lanes past n_rot pass through.
+void orc_rope_ff(float* x, int n_heads, int head_dim, int n_rot, float pos, float base, int mode, const float* ff)
 {
 	if (n_rot <= 0) return;
 	const int half = n_rot / 2;
@@ -308,7 +313,8 @@ void orc_rope(float* x, int n_heads, int head_dim, int n_rot, float pos, float b
 	float inv = 1.0f;
 	for (int i = 0; i < half; ++i)
 	{
-		const float th = pos * inv;
+		float th = pos * inv;
+		if (ff) th /= ff[i];
 		c[i] = std::cos(th);
 		s[i] = std::sin(th);
 		inv *= ratio;
@@ -328,6 +334,11 @@ void orc_rope(float* x, int n_heads, int head_dim, int n_rot, float pos, float b
 	}
 }
 
+void orc_rope(float* x, int n_heads, int head_dim, int n_rot, float pos, float base, int mode)
+{
+	orc_rope_ff(x, n_heads, head_dim, n_rot, pos, base, mode, nullptr);
+}
+
 // RMSNorm of n_groups vectors of dim floats, in place, gamma = 1: the sum of
 // squares in double, y = x * (1 / sqrt(mean + eps)).
 void orc_rmsnorm_groups(float* x, size_t n_groups, size_t dim, float eps)
@@ -339,6 +350,73 @@ void orc_rmsnorm_groups(float* x, size_t n_groups, size_t dim, float eps)
 		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
 		const float r = static_cast<float>(1.0 / std::sqrt(s2 / static_cast<double>(dim) + eps));
 		for (size_t i = 0; i < dim; ++i) xg[i] *= r;
+	}
+}
+
+// RMSNorm with a learned gamma (NULL = 1), in place: the sum of squares in
+// double, scale = 1 / sqrt(sum * (1/dim as fp32) + eps), y = x * scale * gamma.
+void orc_rmsnorm_gamma(float* x, size_t n_groups, size_t dim, const float* gamma, float eps)
+{
+	const float inv_dim = 1.0f / static_cast<float>(dim);
+	for (size_t g = 0; g < n_groups; ++g)
+	{
+		float* xg = x + g * dim;
+		double s2 = 0.0;
+		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
+		const float r = static_cast<float>(1.0 / std::sqrt(s2 * inv_dim + eps));
+		for (size_t i = 0; i < dim; ++i) xg[i] = xg[i] * r * (gamma ? gamma[i] : 1.0f);
+	}
+}
+
+// RMSNorm without gamma, in place: scale = 1 / sqrt(sum / dim + eps).
+void orc_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
+{
+	for (size_t g = 0; g < n_groups; ++g)
+	{
+		float* xg = x + g * dim;
+		double s2 = 0.0;
+		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
+		const float r = static_cast<float>(1.0 / std::sqrt(s2 / static_cast<double>(dim) + eps));
+		for (size_t i = 0; i < dim; ++i) xg[i] *= r;
+	}
+}
+
+// The step before the attention core, in the reference's order: per-head
+// RMSNorm of Q (q_gamma) and K (k_gamma) when given, of V without gamma when
+// v_norm (Gemma 4), RoPE of Q and K at position (pos0 + t) * pos_scale, then
+// K and V of token t to row (pos0 + t) % rows of the buffers (BF16 with
+// round-to-nearest-even, or F32). q, k and v ([n_tok][heads * head_dim]) are
+// updated in place, as the reference updates its scratch rows.
+void orc_prep_append(float* q, float* k, float* v, int n_tok, int n_head, int n_kv, int head_dim,
+                     const float* q_gamma, const float* k_gamma, int v_norm, float eps, int n_rot, float base,
+                     float pos_scale, int mode, const float* ff, int pos0, int rows, int kv_bf16, void* K, void* V)
+{
+	const size_t q_dim = static_cast<size_t>(n_head) * head_dim, kv_dim = static_cast<size_t>(n_kv) * head_dim;
+	if (q_gamma) orc_rmsnorm_gamma(q, static_cast<size_t>(n_tok) * n_head, head_dim, q_gamma, eps);
+	if (k_gamma) orc_rmsnorm_gamma(k, static_cast<size_t>(n_tok) * n_kv, head_dim, k_gamma, eps);
+	if (v_norm) orc_rmsnorm_plain(v, static_cast<size_t>(n_tok) * n_kv, head_dim, eps);
+	for (int t = 0; t < n_tok; ++t)
+	{
+		const float rpos = static_cast<float>(pos0 + t) * pos_scale;
+		orc_rope_ff(q + t * q_dim, n_head, head_dim, n_rot, rpos, base, mode, ff);
+		orc_rope_ff(k + t * kv_dim, n_kv, head_dim, n_rot, rpos, base, mode, ff);
+	}
+	for (int t = 0; t < n_tok; ++t)
+	{
+		const size_t row = static_cast<size_t>((pos0 + t) % rows) * kv_dim;
+		for (size_t i = 0; i < kv_dim; ++i)
+		{
+			if (kv_bf16)
+			{
+				static_cast<uint16_t*>(K)[row + i] = f32_to_bf16(k[t * kv_dim + i]);
+				static_cast<uint16_t*>(V)[row + i] = f32_to_bf16(v[t * kv_dim + i]);
+			}
+			else
+			{
+				static_cast<float*>(K)[row + i] = k[t * kv_dim + i];
+				static_cast<float*>(V)[row + i] = v[t * kv_dim + i];
+			}
+		}
 	}
 }
 

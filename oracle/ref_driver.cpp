@@ -11,7 +11,10 @@
 //   ref_attn_span    calls model_attn_span (reference model.h:364);
 //   ref_bf16_from_f32 calls nnc_f32_to_bf16 (reference runtime.h:106-113);
 //   ref_rope         calls nnc_rope_f32 (reference nn_ops.h:306);
-//   ref_rmsnorm_groups calls nnc_rmsnorm_gamma_multi_f32 (reference nn_ops.h);
+//   ref_rope_ff      calls nnc_rope_f32 with frequency factors;
+//   ref_rmsnorm_groups / ref_rmsnorm_gamma call nnc_rmsnorm_gamma_multi_f32
+//       (reference nn_ops.h:79), ref_rmsnorm_plain calls nnc_rmsnorm_f32
+//       (reference nn_ops.h:73);
 //   ref_set_threads / ref_threads call nnc_set_num_threads / nnc_num_threads
 //       (reference nnc.h:104-105);
 //   ref_attend_layer drives nnc_attn_block/merge/finish through the reference's
@@ -94,6 +97,22 @@ void ref_rmsnorm_groups(float* x, size_t n_groups, size_t dim, float eps)
 {
 	std::vector<float> gamma(dim, 1.0f);
 	nnc_rmsnorm_gamma_multi_f32(x, x, n_groups, dim, gamma.data(), eps);
+}
+
+void ref_rope_ff(float* x, int n_heads, int head_dim, int n_rot, float pos, float base, int mode, const float* ff)
+{
+	nnc_rope_f32(x, static_cast<uint32_t>(n_heads), static_cast<uint32_t>(head_dim), static_cast<uint32_t>(n_rot), pos,
+	             base, mode == 0 ? NNC_ROPE_NEOX : NNC_ROPE_NORM, ff);
+}
+
+void ref_rmsnorm_gamma(float* x, size_t n_groups, size_t dim, const float* gamma, float eps)
+{
+	nnc_rmsnorm_gamma_multi_f32(x, x, n_groups, dim, gamma, eps);
+}
+
+void ref_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
+{
+	for (size_t g = 0; g < n_groups; ++g) nnc_rmsnorm_f32(x + g * dim, x + g * dim, dim, eps);
 }
 
 void ref_set_threads(int n) { nnc_set_num_threads(n); }

@@ -129,6 +129,26 @@ def main() -> int:
         for pos in (7.0, 4095.0):
             data[f"rope/{mode}/{int(pos)}"] = ref.rope(xr, 4, 128, 128, pos, 500000.0, mode)
     data["rmsnorm/out"] = ref.rmsnorm_groups(xr, 128)
+    # RoPE with frequency factors (Llama 3 long-context scaling; 1e30 entries
+    # switch a pair off, as Gemma 4's proportional RoPE does), partial rotary
+    # dims, long positions; RMSNorm with a learned gamma and without gamma.
+    ff = np.exp(rng.uniform(0.0, 3.0, 64)).astype(np.float32)
+    ff[-8:] = 1e30
+    data["rope_ff/factors"] = ff
+    for mode in (0, 1):
+        for n_rot in (128, 64):
+            for pos in (7.0, 32767.0):
+                data[f"rope_ff/{mode}/{n_rot}/{int(pos)}"] = ref.rope_ff(xr, 4, 128, n_rot, pos, 1000000.0, mode,
+                                                                          ff[: n_rot // 2])
+    gamma = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    data["rmsnorm_gamma/gamma"] = gamma
+    data["rmsnorm_gamma/out"] = ref.rmsnorm_gamma(xr, 128, gamma)
+    x80 = rng.standard_normal(6 * 80).astype(np.float32)
+    g80 = rng.uniform(0.5, 1.5, 80).astype(np.float32)
+    data["rmsnorm_gamma80/in"] = x80
+    data["rmsnorm_gamma80/gamma"] = g80
+    data["rmsnorm_gamma80/out"] = ref.rmsnorm_gamma(x80, 80, g80)
+    data["rmsnorm_plain80/out"] = ref.rmsnorm_plain(x80, 80)
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
     return 0

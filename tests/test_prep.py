@@ -1,0 +1,262 @@
+"""The step before the attention core (reference model.cpp:1616-1691): per-head
+RMSNorm of Q/K (gamma) and V (none), RoPE of Q and K, the K/V append.
+
+CPU: the oracle against the reference's own RoPE / RMSNorm outputs
+(tests/golden/reference_vectors.npz), its composition against the
+reference's pieces called in the reference's order, and closed forms.
+GPU: nnc_hip_kv_prep_append_device against the same vectors and against
+the oracle over model-shaped cases, then prep + attend end to end.
+
+Tolerances. q and F32 K/V: rtol 1e-5, atol 1e-5 (the device's cosf/sinf and
+fp32 sums differ from glibc's in the last bits). BF16 K/V: at most one
+BF16 unit in the last place per element, on at most 0.5 % of the elements
+(a value that differs in its last fp32 bits can round to the neighbouring
+BF16). End to end: the attention bound of the BF16 cache, 5e-3."""
+from __future__ import annotations
+
+import zlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import libllmcpu_amd as nh
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_vectors.npz"
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+# ---- CPU: the oracle --------------------------------------------------------------------
+
+def test_rope_ff_and_norms_match_reference_vectors(orc, gold):
+    x = gold["rope/in"]
+    ff = gold["rope_ff/factors"]
+    for mode in (0, 1):
+        for n_rot in (128, 64):
+            for pos in (7, 32767):
+                got = orc.rope_ff(x, 4, 128, n_rot, float(pos), 1000000.0, mode, ff[: n_rot // 2])
+                assert np.allclose(got, gold[f"rope_ff/{mode}/{n_rot}/{pos}"], rtol=1e-6, atol=1e-6), (mode, n_rot, pos)
+    assert np.allclose(orc.rmsnorm_gamma(x, 128, gold["rmsnorm_gamma/gamma"]), gold["rmsnorm_gamma/out"], rtol=1e-6,
+                       atol=1e-7)
+    x80 = gold["rmsnorm_gamma80/in"]
+    assert np.allclose(orc.rmsnorm_gamma(x80, 80, gold["rmsnorm_gamma80/gamma"]), gold["rmsnorm_gamma80/out"],
+                       rtol=1e-6, atol=1e-7)
+    assert np.allclose(orc.rmsnorm_plain(x80, 80), gold["rmsnorm_plain80/out"], rtol=1e-6, atol=1e-7)
+
+
+def test_rope_closed_forms(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(2 * 64).astype(np.float32)
+    for mode in (0, 1):
+        # position 0 rotates by nothing; n_rot 0 leaves everything
+        assert np.array_equal(orc.rope_ff(x, 2, 64, 64, 0.0, 10000.0, mode), x)
+        assert np.array_equal(orc.rope_ff(x, 2, 64, 0, 123.0, 10000.0, mode), x)
+        # a rotation keeps each pair's length; lanes past n_rot pass through
+        y = orc.rope_ff(x, 2, 64, 32, 77.0, 10000.0, mode).reshape(2, 64)
+        xr = x.reshape(2, 64)
+        pairs = [(i, i + 16) for i in range(16)] if mode == 0 else [(2 * i, 2 * i + 1) for i in range(16)]
+        for a, b in pairs:
+            assert np.allclose(np.hypot(y[:, a], y[:, b]), np.hypot(xr[:, a], xr[:, b]), rtol=1e-5)
+        assert np.array_equal(y[:, 32:], xr[:, 32:])
+        # the first pair turns by exactly pos radians (frequency base^0 = 1)
+        a, b = pairs[0]
+        ang = np.arctan2(y[0, b], y[0, a]) - np.arctan2(xr[0, b], xr[0, a])
+        assert abs(np.angle(np.exp(1j * (ang - 77.0)))) < 1e-4
+        # a frequency factor of 1e30 switches its pair off
+        ff = np.ones(16, np.float32)
+        ff[3] = 1e30
+        z = orc.rope_ff(x, 2, 64, 32, 77.0, 10000.0, mode, ff).reshape(2, 64)
+        a, b = pairs[3]
+        assert np.allclose(z[:, [a, b]], xr[:, [a, b]], atol=1e-6)
+    # RMSNorm without gamma gives unit RMS; gamma scales each lane
+    n = orc.rmsnorm_plain(x, 64).reshape(2, 64)
+    assert np.allclose(np.sqrt((n.astype(np.float64) ** 2).mean(axis=1)), 1.0, atol=1e-5)
+    g = np.linspace(0.5, 2.0, 64).astype(np.float32)
+    assert np.allclose(orc.rmsnorm_gamma(x, 64, g).reshape(2, 64), n * g, rtol=1e-6, atol=1e-7)
+
+
+def test_prep_append_composes_the_reference_pieces(orc, ref):
+    """orc_prep_append against the reference's own RMSNorm, RoPE and BF16
+    rounding applied in the order of reference model.cpp:1616-1691."""
+    rng = np.random.default_rng(11)
+    n_tok, n_head, n_kv, hd, rows, pos0 = 5, 8, 2, 64, 8, 6  # the batch wraps the 8-row buffer
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((n_tok, n_kv * hd)).astype(np.float32)
+    v = rng.standard_normal((n_tok, n_kv * hd)).astype(np.float32)
+    qg = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kg = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    ff = np.exp(rng.uniform(0, 2, hd // 4)).astype(np.float32)
+    kw = dict(n_rot=hd // 2, base=10000.0, pos_scale=0.5, mode=0, freq_factors=ff)
+    for bf16 in (True, False):
+        K0 = np.zeros((rows, n_kv * hd), np.uint16 if bf16 else np.float32)
+        qo, Ko, Vo = orc.prep_append(q, k, v, K0, K0.copy(), n_head=n_head, n_kv=n_kv, head_dim=hd, pos0=pos0,
+                                     kv_bf16=bf16, q_gamma=qg, k_gamma=kg, v_norm=True, **kw)
+        want_q = ref.rmsnorm_gamma(q.reshape(-1), hd, qg).reshape(n_tok, -1)
+        want_k = ref.rmsnorm_gamma(k.reshape(-1), hd, kg).reshape(n_tok, -1)
+        want_v = ref.rmsnorm_plain(v.reshape(-1), hd).reshape(n_tok, -1)
+        for t in range(n_tok):
+            rpos = np.float32(pos0 + t) * np.float32(0.5)
+            want_q[t] = ref.rope_ff(want_q[t], n_head, hd, hd // 2, float(rpos), 10000.0, 0, ff)
+            want_k[t] = ref.rope_ff(want_k[t], n_kv, hd, hd // 2, float(rpos), 10000.0, 0, ff)
+        assert np.allclose(qo, want_q, rtol=1e-6, atol=1e-6)
+        for t in range(n_tok):
+            r = (pos0 + t) % rows
+            if bf16:
+                assert np.array_equal(Ko[r], ref.bf16_round(want_k[t])), t
+                assert np.array_equal(Vo[r], ref.bf16_round(want_v[t])), t
+            else:
+                assert np.allclose(Ko[r], want_k[t], rtol=1e-6, atol=1e-6)
+                assert np.allclose(Vo[r], want_v[t], rtol=1e-6, atol=1e-6)
+        untouched = sorted(set(range(rows)) - {(pos0 + t) % rows for t in range(n_tok)})
+        assert not Ko[untouched].any() and not Vo[untouched].any()
+
+
+# ---- GPU: the device step ------------------------------------------------------------------
+
+def bf16_ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """|a - b| in BF16 units in the last place, for BF16 bit patterns of equal sign."""
+    return np.abs(a.astype(np.int32) - b.astype(np.int32))
+
+
+@pytest.mark.gpu
+def test_hip_prep_matches_reference_vectors(gold):
+    """The device step against the reference's own RoPE and RMSNorm outputs."""
+    x = gold["rope/in"].reshape(1, 4 * 128)
+    ff = gold["rope_ff/factors"]
+    dummy = np.zeros((1, 128), np.float32)
+    with nh.KVCache([8], [128], bf16=False) as kv:
+        for mode in (0, 1):
+            for n_rot in (128, 64):
+                for pos in (7, 32767):
+                    say(f"case golden rope mode {mode} n_rot {n_rot} pos {pos}")
+                    got = kv.prep_append(0, x, dummy, dummy, pos0=pos, n_head=4, n_kv=1, head_dim=128, n_rot=n_rot,
+                                         base=1000000.0, mode=mode, freq_factors=ff[: n_rot // 2])
+                    assert np.allclose(got.reshape(-1), gold[f"rope_ff/{mode}/{n_rot}/{pos}"], rtol=1e-5, atol=1e-5)
+        say("case golden rmsnorm gamma")
+        got = kv.prep_append(0, x, dummy, dummy, pos0=0, n_head=4, n_kv=1, head_dim=128,
+                             q_gamma=gold["rmsnorm_gamma/gamma"])
+        assert np.allclose(got.reshape(-1), gold["rmsnorm_gamma/out"], rtol=1e-5, atol=1e-6)
+    x80 = gold["rmsnorm_gamma80/in"].reshape(1, 6 * 80)
+    with nh.KVCache([4], [480], bf16=False) as kv:
+        say("case golden rmsnorm 80 (Q gamma, V plain, F32 cache)")
+        got = kv.prep_append(0, x80, x80, x80, pos0=1, n_head=6, n_kv=6, head_dim=80,
+                             q_gamma=gold["rmsnorm_gamma80/gamma"], v_norm=True)
+        assert np.allclose(got.reshape(-1), gold["rmsnorm_gamma80/out"], rtol=1e-5, atol=1e-6)
+        K, V = kv.read(0, 1, 1)
+        assert np.array_equal(K.reshape(-1), x80.reshape(-1))  # no K norm, no RoPE: stored as given
+        assert np.allclose(V.reshape(-1), gold["rmsnorm_plain80/out"], rtol=1e-5, atol=1e-6)
+
+
+PREP_CASES = {
+    # name: (n_head, n_kv, hd, n_tok, pos0, rows, bf16, options)
+    "llama3_norm_rope": (32, 8, 64, 16, 4000, 4096, True, dict(n_rot=64, base=500000.0, mode=1)),
+    "qwen3_qk_norm_neox": (32, 8, 128, 512, 3584, 4096, True, dict(qg=True, kg=True, n_rot=128, base=1000000.0,
+                                                                      mode=0)),
+    "gemma3_global_scaled": (4, 1, 256, 8, 8000, 8192, True, dict(qg=True, kg=True, n_rot=256, base=1000000.0,
+                                                                   mode=0, pos_scale=0.125)),
+    "gemma4_partial_ff_vnorm_ring": (8, 4, 256, 12, 250, 256, True, dict(qg=True, kg=True, v_norm=True, n_rot=64,
+                                                                          base=10000.0, mode=0, ff=True)),
+    "f32_cache_one_token": (16, 4, 128, 1, 32767, 32768, False, dict(kg=True, n_rot=128, base=10000.0, mode=1)),
+    "no_rope_hd80": (6, 2, 80, 3, 5, 16, True, dict(qg=True, kg=True, n_rot=0)),
+}
+
+
+def prep_case(name, orc):
+    n_head, n_kv, hd, n_tok, pos0, rows, bf16, o = PREP_CASES[name]
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    q = (rng.standard_normal((n_tok, n_head * hd)) * 2.0).astype(np.float32)
+    k = (rng.standard_normal((n_tok, n_kv * hd)) * 2.0).astype(np.float32)
+    v = rng.standard_normal((n_tok, n_kv * hd)).astype(np.float32)
+    kw = dict(n_rot=o.get("n_rot", 0), base=o.get("base", 10000.0), pos_scale=o.get("pos_scale", 1.0),
+              mode=o.get("mode", 0), v_norm=o.get("v_norm", False), eps=1e-6)
+    kw["q_gamma"] = rng.uniform(0.5, 1.5, hd).astype(np.float32) if o.get("qg") else None
+    kw["k_gamma"] = rng.uniform(0.5, 1.5, hd).astype(np.float32) if o.get("kg") else None
+    if o.get("ff"):
+        ff = np.exp(rng.uniform(0.0, 3.0, kw["n_rot"] // 2)).astype(np.float32)
+        ff[-4:] = 1e30
+        kw["freq_factors"] = ff
+    else:
+        kw["freq_factors"] = None
+    K0 = np.zeros((rows, n_kv * hd), np.uint16 if bf16 else np.float32)
+    want_q, want_K, want_V = orc.prep_append(q, k, v, K0, K0.copy(), n_head=n_head, n_kv=n_kv, head_dim=hd, pos0=pos0,
+                                             kv_bf16=bf16, **kw)
+    return (n_head, n_kv, hd, n_tok, pos0, rows, bf16), q, k, v, kw, (want_q, want_K, want_V)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(PREP_CASES))
+def test_hip_prep_matches_oracle(orc, name):
+    (n_head, n_kv, hd, n_tok, pos0, rows, bf16), q, k, v, kw, (want_q, want_K, want_V) = prep_case(name, orc)
+    say(f"case prep {name}: {n_tok} tokens at {pos0}, heads {n_head}/{n_kv} x {hd}, rows {rows}, bf16 {bf16}")
+    with nh.KVCache([rows], [n_kv * hd], bf16=bf16) as kv:
+        got_q = kv.prep_append(0, q, k, v, pos0=pos0, n_head=n_head, n_kv=n_kv, head_dim=hd, **kw)
+        K, V = kv.read(0, 0, rows)
+    err = float(np.abs(got_q - want_q).max())
+    say(f"  q max-abs {err:.3e}")
+    assert np.allclose(got_q, want_q, rtol=1e-5, atol=1e-5)
+    if bf16:
+        for got, want, what in ((K, want_K, "K"), (V, want_V, "V")):
+            ulps = bf16_ulps(got, want)
+            frac = float((ulps > 0).mean())
+            say(f"  {what}: {int((ulps > 0).sum())} of {ulps.size} elements differ (max {int(ulps.max())} ulp)")
+            assert ulps.max() <= 1 and frac <= 0.005, what
+    else:
+        assert np.allclose(K, want_K, rtol=1e-5, atol=1e-5)
+        assert np.allclose(V, want_V, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_hip_prep_then_attend_matches_oracle(orc):
+    """Prep + attention on the device against the oracle's prep + attention,
+    for a 64-token Qwen3-shaped batch appended after 448 cached positions."""
+    rng = np.random.default_rng(5)
+    n_head, n_kv, hd, rows = 32, 8, 128, 1024
+    n_past, n_tok = 448, 64
+    kw = dict(n_rot=128, base=1000000.0, mode=0, pos_scale=1.0, eps=1e-6,
+              q_gamma=rng.uniform(0.5, 1.5, hd).astype(np.float32), k_gamma=rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    q = rng.standard_normal((n_past + n_tok, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((n_past + n_tok, n_kv * hd)).astype(np.float32)
+    v = rng.standard_normal((n_past + n_tok, n_kv * hd)).astype(np.float32)
+    K = np.zeros((rows, n_kv * hd), np.uint16)
+    V = K.copy()
+    qo, K, V = orc.prep_append(q[:n_past], k[:n_past], v[:n_past], K, V, n_head=n_head, n_kv=n_kv, head_dim=hd, pos0=0,
+                               kv_bf16=True, **kw)
+    qo, K, V = orc.prep_append(q[n_past:], k[n_past:], v[n_past:], K, V, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                               pos0=n_past, kv_bf16=True, **kw)
+    scale = 1.0 / np.sqrt(hd)
+    want = orc.attend_layer(qo, K, V, kv_bf16=True, rows=rows, pos0=n_past, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                            scale=scale)
+    say("case prep + attend: 448 cached + 64 new tokens, qwen3 shape")
+    with nh.KVCache([rows], [n_kv * hd], bf16=True) as kv:
+        kv.prep_append(0, q[:n_past], k[:n_past], v[:n_past], pos0=0, n_head=n_head, n_kv=n_kv, head_dim=hd, **kw)
+        qg = kv.prep_append(0, q[n_past:], k[n_past:], v[n_past:], pos0=n_past, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                            **kw)
+        got = kv.attend(0, qg, pos0=n_past, n_head=n_head, n_kv=n_kv, head_dim=hd, scale=scale)
+    err = float(np.abs(got - want).max())
+    say(f"  max-abs {err:.3e}")
+    assert err <= 5e-3
+
+
+@pytest.mark.gpu
+def test_hip_prep_refuses_bad_arguments():
+    with nh.KVCache([16], [128], bf16=True) as kv:
+        for kwargs in [
+            dict(n_head=2, n_kv=1, head_dim=128, n_rot=3),  # odd n_rot
+            dict(n_head=2, n_kv=1, head_dim=128, n_rot=256),  # n_rot above head_dim
+            dict(n_head=2, n_kv=1, head_dim=128, n_rot=128, mode=2),  # no such RoPE mode
+            dict(n_head=4, n_kv=2, head_dim=64, n_rot=64, base=0.0),  # no frequency base
+            dict(n_head=2, n_kv=2, head_dim=128),  # kv_dim 256, buffer 128
+        ]:
+            q = np.zeros((1, kwargs["n_head"] * kwargs["head_dim"]), np.float32)
+            k = np.zeros((1, kwargs["n_kv"] * kwargs["head_dim"]), np.float32)
+            with pytest.raises(nh.NncError) as e:
+                kv.prep_append(0, q, k, k, pos0=0, **kwargs)
+            assert e.value.status == nh.NncStatus.INVALID_ARGUMENT, kwargs
