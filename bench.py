@@ -48,6 +48,13 @@ def decode_bytes(span: int) -> int:
     return 2 * span * KV_DIM * 2 + 2 * N_HEAD * HD * 4
 
 
+def prep_bytes(n_tok: int) -> int:
+    """Algorithmic bytes of the pre-attention step of one layer (reference
+    model.cpp:1616-1691): q read and written, k and v read (fp32), the K and V
+    rows written (BF16), the two gammas read."""
+    return n_tok * (N_HEAD * HD * 4 * 2 + KV_DIM * 4 * 2 + KV_DIM * 2 * 2) + 2 * HD * 4
+
+
 def prefill_flops(pos0: int, n_tok: int) -> int:
     spans = np.arange(pos0 + 1, pos0 + n_tok + 1, dtype=np.int64)  # causal: key 0 .. pos
     return int(4 * HD * N_HEAD * spans.sum())
@@ -259,6 +266,34 @@ def main() -> int:
     pre_launch_us = pre_ms * 1e3 / (args.prefill_steps * pre_launches)
     pre_launch_tflops = (pre_flops / pre_launches) / (pre_launch_us * 1e-6) / 1e12
 
+    # The pre-attention step (per-head RMSNorm of Q/K, RoPE, K/V append) at
+    # the same shape, after the attention timings (it rewrites q and the
+    # cache rows it appends): one token per layer, then 512-token chunks.
+    k_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
+    v_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
+    gam = hip_rt.malloc(2 * HD * 4)
+    nh.fill_normal(k_in, CHUNK * KV_DIM, 77, 0, False, stream)
+    nh.fill_normal(v_in, CHUNK * KV_DIM, 78, 0, False, stream)
+    hip_rt.to_device(gam, np.ones(2 * HD, np.float32))
+    prep = nh.NncHipPrep(N_HEAD, N_KV, HD, gam, gam + HD * 4, 0, 1e-6, HD, 1000000.0, 1.0, 0, None)
+
+    def prep_step(n_tok, pos0):
+        for li in range(N_LAYER):
+            kv.prep_append_device(li, q_pre + li * PROMPT * N_HEAD * HD * 4, k_in, v_in, pos0=pos0, n_tok=n_tok,
+                                  prep=prep)
+
+    prep_res = {}
+    for label, n_tok, pos0 in (("decode", 1, CTX - 1), ("chunk", CHUNK, PROMPT - CHUNK)):
+        prep_step(n_tok, pos0)
+        ms, _ = timed(lambda: prep_step(n_tok, pos0), 10)
+        us = ms * 1e3 / (10 * N_LAYER)
+        prep_res[label] = {"n_tok": n_tok, "us_per_layer": round(us, 3), "bytes_per_layer": prep_bytes(n_tok),
+                           "gbs": round(prep_bytes(n_tok) / (us * 1e-6) / 1e9, 1)}
+    log(f"[bench] prep decode {prep_res['decode']['us_per_layer']} us/layer, "
+        f"chunk {prep_res['chunk']['us_per_layer']} us/layer ({prep_res['chunk']['gbs']} GB/s)")
+    for p_ in (k_in, v_in, gam):
+        hip_rt.free(p_)
+
     traffic = None
     tp = Path(args.traffic)
     if tp.exists():
@@ -300,6 +335,11 @@ def main() -> int:
                                  "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
                                  "kernel": "prefill_kernel<128,4> (bf16 hi+lo QK, fp16 PV MFMA, fp32 accumulate)",
                                  "avg_launch_us": round(pre_launch_us, 3)}},
+        "prep": {"what": "per-head RMSNorm of Q and K, NEOX RoPE (base 1e6), BF16 K/V append, device memory",
+                 "decode": prep_res["decode"], "chunk": prep_res["chunk"],
+                 "roofline": {"bound": "hbm", "achieved": prep_res["chunk"]["gbs"], "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(prep_res["chunk"]["gbs"] / HBM_PEAK_GBS, 4),
+                              "kernel": "prep_kernel (512-token chunk)"}},
         "cpu_baseline": cpu,
         "device": {"cu": n_cu, "clock_mhz": clock_mhz},
         "wall_ms": {"decode": round(dec_wall, 2), "prefill": round(pre_wall, 2)},

@@ -7,6 +7,7 @@ from .nnc_hip import (  # noqa: F401
     ATTN_BLOCK,
     KVCache,
     NncError,
+    NncHipPrep,
     NncStatus,
     attn_span,
     bf16_round,

@@ -65,6 +65,27 @@ namespace nnchip
 		return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 	}
 
+	// x[l] + x[l ^ 16] on every lane (v_permlane16_swap exchanges the odd
+	// 16-lane rows of one operand with the even rows of the other).
+	__device__ __forceinline__ float add_with_other_row(float x)
+	{
+		const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+		return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+	}
+
+	// The sum of x over the wavefront, on every lane, without LDS: within each
+	// 16-lane row by DPP (quad permutations [1,0,3,2] and [2,3,0,1], then the
+	// half-row and row mirrors), then across rows with the permlane swaps.
+	__device__ __forceinline__ float wave_sum_dpp(float x)
+	{
+		x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false)); // lane ^ 1
+		x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false)); // lane ^ 2
+		x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false)); // half-row mirror
+		x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false)); // row mirror
+		x = add_with_other_row(x);
+		return add_with_other_half(x);
+	}
+
 	__device__ __forceinline__ f16x8 as_f16x8(const uint4& v) { return __builtin_bit_cast(f16x8, v); }
 	__device__ __forceinline__ f16x8 as_f16x8(const u32x4& v) { return __builtin_bit_cast(f16x8, v); }
 

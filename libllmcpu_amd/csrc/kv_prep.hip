@@ -6,13 +6,14 @@
 // runtime.h:106-113) or F32. Q is updated in place, ready for the attention
 // call; the K/V inputs are left as they are.
 //
-// One wavefront per (token, head row): the head's head_dim values are held
-// 64 lanes wide (coalesced loads and stores), the RMSNorm sum is a wavefront
-// reduction, and RoPE pairs meet through the wavefront's LDS row. The rotation
-// angles follow the reference's schedule: the per-pair frequency
-// base^(-2i/n_rot) accumulated step by step in fp32 (computed on the host, the
-// same sequence of products), times the position, divided by the pair's
-// frequency factor when there is one.
+// A work-group takes 16 head rows of one token, 4 per wavefront, all loaded at
+// once; a head's head_dim values are held 64 lanes wide (coalesced loads and
+// stores), the RMSNorm sum is a wavefront reduction (DPP and permlane swaps), and RoPE pairs meet
+// through the wavefront's LDS row. Each lane computes the rotation angles of
+// the pairs it rotates once for all its rows, following the reference's
+// schedule: the per-pair frequency base^(-2i/n_rot) accumulated step by step
+// in fp32 (computed on the host, the same sequence of products), times the
+// position, divided by the pair's frequency factor when there is one.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -20,122 +21,271 @@ namespace nnchip
 {
 	namespace
 	{
-		constexpr int kWaves = 4; // head rows per work-group
+		constexpr int kWaves = 4; // wavefronts per work-group
 		constexpr int kMaxHd = 512; // head_dim bound (the reference's RoPE table holds 256 pairs)
 
-		__device__ __forceinline__ float wave_sum(float x)
+		constexpr int kRowsPerWave = 4; // head rows per wavefront, loaded together
+		constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
+
+		// Work-group (g, t): head rows 16 g .. 16 g + 15 of token t, where rows
+		// 0 .. n_head - 1 are Q heads (updated in place), then n_kv K heads and
+		// n_kv V heads (appended to row (pos0 + t) % rows).
+		// NJ = head_dim / 64, rounded up: values per lane in a row; FULL: head_dim
+		// is exactly 64 NJ (no lane is masked).
+		// A full row's NJ consecutive values of one lane, as one wide access
+		// (src null: zeros).
+		template <int NJ>
+		__device__ __forceinline__ void load_row(const float* src, int lane, float* x)
 		{
+			if (!src)
+			{
 #pragma unroll
-			for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
-			return x;
+				for (int j = 0; j < NJ; ++j) x[j] = 0.0f;
+				return;
+			}
+			const float* s = src + lane * NJ;
+			if constexpr (NJ == 1)
+				x[0] = s[0];
+			else if constexpr (NJ == 2)
+			{
+				const float2 v = *reinterpret_cast<const float2*>(s);
+				x[0] = v.x;
+				x[1] = v.y;
+			}
+			else
+			{
+#pragma unroll
+				for (int j = 0; j < NJ; j += 4)
+				{
+					const float4 v = *reinterpret_cast<const float4*>(s + j);
+					x[j] = v.x;
+					x[j + 1] = v.y;
+					x[j + 2] = v.z;
+					x[j + 3] = v.w;
+				}
+			}
 		}
 
+		template <int NJ>
+		__device__ __forceinline__ void store_row(float* dst, int lane, const float* x)
+		{
+			float* d = dst + lane * NJ;
+			if constexpr (NJ == 1)
+				d[0] = x[0];
+			else if constexpr (NJ == 2)
+				*reinterpret_cast<float2*>(d) = make_float2(x[0], x[1]);
+			else
+			{
+#pragma unroll
+				for (int j = 0; j < NJ; j += 4) *reinterpret_cast<float4*>(d + j) = make_float4(x[j], x[j + 1], x[j + 2], x[j + 3]);
+			}
+		}
+
+		template <int NJ>
+		__device__ __forceinline__ void store_row_bf16(uint16_t* dst, int lane, const float* x)
+		{
+			uint16_t* d = dst + lane * NJ;
+			if constexpr (NJ == 1)
+				d[0] = static_cast<uint16_t>(f32_to_bf16_bits(x[0]));
+			else if constexpr (NJ == 2)
+				*reinterpret_cast<uint32_t*>(d) = pack_bf16x2(x[0], x[1]);
+			else
+			{
+#pragma unroll
+				for (int j = 0; j < NJ; j += 4)
+					*reinterpret_cast<uint2*>(d + j) = make_uint2(pack_bf16x2(x[j], x[j + 1]), pack_bf16x2(x[j + 2], x[j + 3]));
+			}
+		}
+
+		template <int NJ, bool FULL>
 		__global__ __launch_bounds__(64 * kWaves) void prep_kernel(const prep_params p)
 		{
 			__shared__ float s_x[kWaves][kMaxHd];
 			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-			const int hrow = blockIdx.x * kWaves + wave;
 			const int t = blockIdx.y;
-			if (hrow >= p.n_head + 2 * p.n_kv) return; // whole wavefront; nothing below synchronises the work-group
 			const int hd = p.head_dim;
+			const int n_hrows = p.n_head + 2 * p.n_kv;
 			const size_t q_dim = static_cast<size_t>(p.n_head) * hd, kv_dim = static_cast<size_t>(p.n_kv) * hd;
+			const int half = p.n_rot / 2;
+			// Element j of this lane in a row: NJ consecutive values per lane for a
+			// full row (one wide load or store per row), else strided by 64.
+			auto pos = [&](int j) __attribute__((always_inline)) -> int { return FULL ? lane * NJ + j : lane + 64 * j; };
 
-			// Row kind: 0 = Q head (in place), 1 = K head, 2 = V head.
-			const int kind = hrow < p.n_head ? 0 : hrow < p.n_head + p.n_kv ? 1 : 2;
-			const int head = kind == 0 ? hrow : kind == 1 ? hrow - p.n_head : hrow - p.n_head - p.n_kv;
-			const float* src = kind == 0 ? p.q + t * q_dim + static_cast<size_t>(head) * hd
-			                   : kind == 1 ? p.k + t * kv_dim + static_cast<size_t>(head) * hd
-			                               : p.v + t * kv_dim + static_cast<size_t>(head) * hd;
+			auto row_src = [&](int hrow, int& kind, int& head) __attribute__((always_inline)) -> const float*
+			{
+				kind = hrow < p.n_head ? 0 : hrow < p.n_head + p.n_kv ? 1 : 2;
+				head = kind == 0 ? hrow : kind == 1 ? hrow - p.n_head : hrow - p.n_head - p.n_kv;
+				return kind == 0 ? p.q + t * q_dim + static_cast<size_t>(head) * hd
+				       : kind == 1 ? p.k + t * kv_dim + static_cast<size_t>(head) * hd
+				                   : p.v + t * kv_dim + static_cast<size_t>(head) * hd;
+			};
 
-			constexpr int NJ = kMaxHd / 64;
-			float x[NJ];
+			// All of this wavefront's rows in flight at once.
+			float x[kRowsPerWave][NJ];
 #pragma unroll
-			for (int j = 0; j < NJ; ++j)
+			for (int r = 0; r < kRowsPerWave; ++r)
 			{
-				const int i = lane + 64 * j;
-				x[j] = i < hd ? src[i] : 0.0f;
-			}
-
-			// RMSNorm: scale = 1 / sqrt(mean of squares + eps), the mean in
-			// double as the reference takes it (times fp32 1/dim with gamma,
-			// divided by dim without, reference nn_ops.cpp:558-632).
-			const float* gamma = kind == 0 ? p.q_gamma : kind == 1 ? p.k_gamma : nullptr;
-			const bool norm = kind == 2 ? p.v_norm != 0 : gamma != nullptr;
-			if (norm)
-			{
-				float ss = 0.0f;
-#pragma unroll
-				for (int j = 0; j < NJ; ++j) ss = fmaf(x[j], x[j], ss);
-				const double sum2 = static_cast<double>(wave_sum(ss));
-				const double mean = gamma ? sum2 * static_cast<double>(1.0f / static_cast<float>(hd))
-				                          : sum2 / static_cast<double>(hd);
-				const float r = static_cast<float>(1.0 / sqrt(mean + static_cast<double>(p.eps)));
-#pragma unroll
-				for (int j = 0; j < NJ; ++j)
-				{
-					const int i = lane + 64 * j;
-					x[j] = x[j] * r;
-					if (gamma && i < hd) x[j] *= gamma[i];
-				}
-			}
-
-			// RoPE on Q and K: NEOX pairs lanes i and i + n_rot/2, NORM lanes 2i
-			// and 2i + 1 (reference nn_ops.cpp:1830-1873); lanes past n_rot pass
-			// through.
-			if (kind != 2 && p.n_rot > 0)
-			{
-				float* xs = s_x[wave];
-#pragma unroll
-				for (int j = 0; j < NJ; ++j)
-				{
-					const int i = lane + 64 * j;
-					if (i < hd) xs[i] = x[j];
-				}
-				wave_sync();
-				const int half = p.n_rot / 2;
-				const int stride = p.mode == 0 ? 1 : 2, partner = p.mode == 0 ? half : 1;
-				const float rpos = static_cast<float>(p.pos0 + t) * p.pos_scale;
-				for (int i = lane; i < half; i += 64)
-				{
-					float th = rpos * p.inv[i];
-					if (p.freq_factors) th /= p.freq_factors[i];
-					const float c = cosf(th), s = sinf(th);
-					const int i0 = i * stride, i1 = i0 + partner;
-					const float a = xs[i0], b = xs[i1];
-					xs[i0] = c * a - s * b;
-					xs[i1] = s * a + c * b;
-				}
-				wave_sync();
-#pragma unroll
-				for (int j = 0; j < NJ; ++j)
-				{
-					const int i = lane + 64 * j;
-					if (i < hd) x[j] = xs[i];
-				}
-			}
-
-			if (kind == 0)
-			{
-				float* dst = p.q + t * q_dim + static_cast<size_t>(head) * hd;
-#pragma unroll
-				for (int j = 0; j < NJ; ++j)
-				{
-					const int i = lane + 64 * j;
-					if (i < hd) dst[i] = x[j];
-				}
-				return;
-			}
-			const size_t off = static_cast<size_t>((p.pos0 + t) % p.rows) * kv_dim + static_cast<size_t>(head) * hd;
-			void* base = kind == 1 ? p.K : p.V;
-#pragma unroll
-			for (int j = 0; j < NJ; ++j)
-			{
-				const int i = lane + 64 * j;
-				if (i >= hd) continue;
-				if (p.bf16)
-					static_cast<uint16_t*>(base)[off + i] = static_cast<uint16_t>(f32_to_bf16_bits(x[j]));
+				const int hrow = blockIdx.x * kRowsPerGroup + r * kWaves + wave;
+				int kind, head;
+				const float* src = hrow < n_hrows ? row_src(hrow, kind, head) : nullptr;
+				if constexpr (FULL)
+					load_row<NJ>(src, lane, x[r]);
 				else
-					static_cast<float*>(base)[off + i] = x[j];
+				{
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						const int i = pos(j);
+						x[r][j] = (src && i < hd) ? src[i] : 0.0f;
+					}
+				}
+			}
+
+			// This lane's values of the two gammas, with the rows in flight.
+			float gq[NJ], gk[NJ];
+#pragma unroll
+			for (int j = 0; j < NJ; ++j)
+			{
+				const int i = pos(j);
+				const bool in = FULL || i < hd;
+				gq[j] = (p.q_gamma && in) ? p.q_gamma[i] : 1.0f;
+				gk[j] = (p.k_gamma && in) ? p.k_gamma[i] : 1.0f;
+			}
+
+			// This lane's rotation angles: the pairs lane, lane + 64, ... it
+			// rotates in every row (no barrier: the loads above are in flight).
+			constexpr int NP = kPrepMaxPairs / 64;
+			float c_tab[NP], s_tab[NP];
+			if (half > 0)
+			{
+				const float rpos = static_cast<float>(p.pos0 + t) * p.pos_scale;
+#pragma unroll
+				for (int u = 0; u < NP; ++u)
+				{
+					const int i = lane + 64 * u;
+					c_tab[u] = 1.0f;
+					s_tab[u] = 0.0f;
+					if (i < half)
+					{
+						float th = rpos * p.inv[i];
+						if (p.freq_factors) th /= p.freq_factors[i];
+						// sin and cos of the fp32 angle, reduced to [-pi, pi] in double
+						// first (exact to far below an fp32 ulp for the angles RoPE
+						// makes), so sincosf takes its small-argument path.
+						const double thd = static_cast<double>(th);
+						const double turns = rint(thd * 0.15915494309189535);
+						const float rr = static_cast<float>(fma(-turns, 6.283185307179586, thd));
+						sincosf(isfinite(th) ? rr : th, &s_tab[u], &c_tab[u]);
+					}
+				}
+			}
+
+#pragma unroll
+			for (int r = 0; r < kRowsPerWave; ++r)
+			{
+				const int hrow = blockIdx.x * kRowsPerGroup + r * kWaves + wave;
+				if (hrow >= n_hrows) break; // uniform over the wavefront
+				int kind, head;
+				(void)row_src(hrow, kind, head);
+				float* xr = x[r];
+
+				// RMSNorm: scale = 1 / sqrt(mean of squares + eps), the mean in
+				// double as the reference takes it (times fp32 1/dim with gamma,
+				// divided by dim without, reference nn_ops.cpp:558-632).
+				const float* gamma = kind == 0 ? p.q_gamma : kind == 1 ? p.k_gamma : nullptr;
+				const bool norm = kind == 2 ? p.v_norm != 0 : gamma != nullptr;
+				if (norm)
+				{
+					float ss = 0.0f;
+#pragma unroll
+					for (int j = 0; j < NJ; ++j) ss = fmaf(xr[j], xr[j], ss);
+					// (the reference takes the mean in double; the square root and
+					// its reciprocal in fp32 here, within an fp32 ulp of it)
+					const double sum2 = static_cast<double>(wave_sum_dpp(ss));
+					const double mean = gamma ? sum2 * static_cast<double>(1.0f / static_cast<float>(hd))
+					                          : sum2 / static_cast<double>(hd);
+					const float sc = 1.0f / sqrtf(static_cast<float>(mean + static_cast<double>(p.eps)));
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						xr[j] = xr[j] * sc;
+						if (gamma) xr[j] *= kind == 0 ? gq[j] : gk[j];
+					}
+				}
+
+				// RoPE on Q and K: NEOX pairs lanes i and i + n_rot/2, NORM lanes
+				// 2i and 2i + 1 (reference nn_ops.cpp:1830-1873); lanes past n_rot
+				// pass through.
+				if (kind != 2 && half > 0)
+				{
+					float* xs = s_x[wave];
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						const int i = pos(j);
+						if (FULL || i < hd) xs[i] = xr[j];
+					}
+					wave_sync();
+					const int stride = p.mode == 0 ? 1 : 2, partner = p.mode == 0 ? half : 1;
+#pragma unroll
+					for (int u = 0; u < NP; ++u)
+					{
+						const int i = lane + 64 * u;
+						if (i >= half) break;
+						const float c = c_tab[u], sn = s_tab[u];
+						const int i0 = i * stride, i1 = i0 + partner;
+						const float a = xs[i0], b = xs[i1];
+						xs[i0] = c * a - sn * b;
+						xs[i1] = sn * a + c * b;
+					}
+					wave_sync();
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						const int i = pos(j);
+						if (FULL || i < hd) xr[j] = xs[i];
+					}
+					wave_sync(); // the row buffer is free for the next row
+				}
+
+				if (kind == 0)
+				{
+					float* dst = p.q + t * q_dim + static_cast<size_t>(head) * hd;
+					if constexpr (FULL)
+						store_row<NJ>(dst, lane, xr);
+					else
+					{
+#pragma unroll
+						for (int j = 0; j < NJ; ++j)
+						{
+							const int i = pos(j);
+							if (i < hd) dst[i] = xr[j];
+						}
+					}
+					continue;
+				}
+				const size_t off = static_cast<size_t>((p.pos0 + t) % p.rows) * kv_dim + static_cast<size_t>(head) * hd;
+				void* base = kind == 1 ? p.K : p.V;
+				if constexpr (FULL)
+				{
+					if (p.bf16)
+						store_row_bf16<NJ>(static_cast<uint16_t*>(base) + off, lane, xr);
+					else
+						store_row<NJ>(static_cast<float*>(base) + off, lane, xr);
+				}
+				else
+				{
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						const int i = pos(j);
+						if (i >= hd) continue;
+						if (p.bf16)
+							static_cast<uint16_t*>(base)[off + i] = static_cast<uint16_t>(f32_to_bf16_bits(xr[j]));
+						else
+							static_cast<float*>(base)[off + i] = xr[j];
+					}
+				}
 			}
 		}
 	}
@@ -144,8 +294,25 @@ namespace nnchip
 	{
 		if (p.head_dim <= 0 || p.head_dim > kMaxHd || p.n_rot / 2 > kPrepMaxPairs) return false;
 		const int rows = p.n_head + 2 * p.n_kv;
-		const dim3 grid((rows + kWaves - 1) / kWaves, n_tok);
-		prep_kernel<<<grid, 64 * kWaves, 0, stream>>>(p);
+		const dim3 grid((rows + kRowsPerGroup - 1) / kRowsPerGroup, n_tok);
+		const dim3 block(64 * kWaves);
+		switch (p.head_dim)
+		{
+		case 64: prep_kernel<1, true><<<grid, block, 0, stream>>>(p); return true;
+		case 128: prep_kernel<2, true><<<grid, block, 0, stream>>>(p); return true;
+		case 256: prep_kernel<4, true><<<grid, block, 0, stream>>>(p); return true;
+		case 512: prep_kernel<8, true><<<grid, block, 0, stream>>>(p); return true;
+		default: break;
+		}
+		const int nj = (p.head_dim + 63) / 64;
+		if (nj <= 1)
+			prep_kernel<1, false><<<grid, block, 0, stream>>>(p);
+		else if (nj <= 2)
+			prep_kernel<2, false><<<grid, block, 0, stream>>>(p);
+		else if (nj <= 4)
+			prep_kernel<4, false><<<grid, block, 0, stream>>>(p);
+		else
+			prep_kernel<8, false><<<grid, block, 0, stream>>>(p);
 		return true;
 	}
 }
