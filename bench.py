@@ -41,6 +41,7 @@ N_HEAD, N_KV, HD, N_LAYER = 32, 8, 128, 36
 KV_DIM = N_KV * HD
 CTX = 32768
 PROMPT, CHUNK = 4096, 512
+SESSION_BATCH = 16  # nnc's tokens per forward pass in a session (reference model.h:330)
 SCALE = 1.0 / np.sqrt(HD)
 
 
@@ -144,7 +145,7 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "batch"], default=None,
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
                     help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
@@ -221,6 +222,13 @@ def main() -> int:
                 kv.attend_device(li, qb + c * CHUNK * N_HEAD * HD * 4, o_pre + c * CHUNK * N_HEAD * HD * 4,
                                  n_tok=CHUNK, pos0=c * CHUNK, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
 
+    def batch_step():
+        # One forward pass of an nnc session (SESSION_BATCH tokens) at the end
+        # of the context, through every layer.
+        for li in range(N_LAYER):
+            kv.attend_device(li, q_pre + li * PROMPT * N_HEAD * HD * 4, o_pre, n_tok=SESSION_BATCH,
+                             pos0=CTX - SESSION_BATCH, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+
     def timed(step, n):
         e0, e1 = hip_rt.Event(), hip_rt.Event()
         hip_rt.sync()
@@ -233,6 +241,12 @@ def main() -> int:
         hip_rt.sync()
         return e1.ms_since(e0), (time.perf_counter() - w0) * 1e3
 
+    if args.only == "batch":
+        batch_step()
+        hip_rt.sync()
+        b_ms, _ = timed(batch_step, 10)
+        log(f"[bench] session batch {b_ms / 10:.4f} ms/step")
+        return 0
     if args.only == "prefill":
         prefill_step()
         hip_rt.sync()
@@ -265,6 +279,14 @@ def main() -> int:
     pre_launches = N_LAYER * (PROMPT // CHUNK)
     pre_launch_us = pre_ms * 1e3 / (args.prefill_steps * pre_launches)
     pre_launch_tflops = (pre_flops / pre_launches) / (pre_launch_us * 1e-6) / 1e12
+
+    log("[bench] session batch")
+    batch_step()
+    hip_rt.sync()
+    b_ms, _ = timed(batch_step, 10)
+    b_us = b_ms * 1e3 / (10 * N_LAYER)
+    b_bytes = decode_bytes(CTX) + 2 * (SESSION_BATCH - 1) * N_HEAD * HD * 4
+    log(f"[bench] session batch {b_us:.2f} us/layer")
 
     # The pre-attention step (per-head RMSNorm of Q/K, RoPE, K/V append) at
     # the same shape, after the attention timings (it rewrites q and the
@@ -335,6 +357,11 @@ def main() -> int:
                                  "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
                                  "kernel": "prefill_kernel<128,4> (bf16 hi+lo QK, fp16 PV MFMA, fp32 accumulate)",
                                  "avg_launch_us": round(pre_launch_us, 3)}},
+        "session_batch": {"what": f"one {SESSION_BATCH}-token forward pass of an nnc session (its batch size, "
+                                  f"MTP verification included) ending at position {CTX - 1}, 36 layers; each token "
+                                  "bit-identical to its one-token call",
+                          "ms_per_step": round(b_ms / 10, 4), "us_per_layer": round(b_us, 3),
+                          "kv_gbs": round(b_bytes / (b_us * 1e-6) / 1e9, 1)},
         "prep": {"what": "per-head RMSNorm of Q and K, NEOX RoPE (base 1e6), BF16 K/V append, device memory",
                  "decode": prep_res["decode"], "chunk": prep_res["chunk"],
                  "roofline": {"bound": "hbm", "achieved": prep_res["chunk"]["gbs"], "peak": HBM_PEAK_GBS,

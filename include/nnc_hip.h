@@ -154,9 +154,14 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
  * a session, window is the layer's sliding window or 0. scale is
  * hparams.attention_scale (reference model.cpp:613-624). An empty span gives
  * zeros (the l == 0 rule of reference nn_ops.cpp:492).
- * n_tok == 1 runs the split-K decode kernel, n_tok > 1 the MFMA prefill
- * kernel. Supported shapes: head_dim 64, 128 or 256; group n_head / n_kv in
- * {1, 2, 4, 8}.
+ * Up to 16 tokens (an nnc session's forward pass, MODEL_PREFILL_BATCH,
+ * reference model.h:330) run the split-K kernel with each token on the split
+ * grid a one-token call gives it, so every token of such a batch gets the
+ * bits of its one-token call (the decode == batch property of reference
+ * tests.cpp:2631-2661 that MTP verification relies on). Larger BF16 batches
+ * run the MFMA prefill kernel (within tolerance, not bit-identical); larger
+ * F32 batches the split-K kernel over the batch's span. Supported shapes:
+ * head_dim 64, 128 or 256; group n_head / n_kv in {1, 2, 4, 8}.
  * NNC_ERR_INVALID_ARGUMENT: bad buffer index, NULL pointers, n_tok <= 0,
  * pos0 < 0, n_seq < 1, n_head not a multiple of n_kv, n_kv * head_dim not the
  * buffer's kv_dim.
@@ -164,7 +169,7 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
  * can hold (a full buffer with pos0 + n_tok > rows, or a ring too small for
  * the window plus the batch).
  * NNC_ERR_UNSUPPORTED_MODEL: a head_dim or group outside the supported set,
- * or a BF16 batch (n_tok > 1) over a buffer of 2 GiB or more. */
+ * or a BF16 batch of more than 16 tokens over a buffer of 2 GiB or more. */
 nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
                           int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
                           int32_t head_dim, float scale);
@@ -174,6 +179,18 @@ nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* ou
 nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok,
                                  int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
                                  int32_t n_kv, int32_t head_dim, float scale);
+
+/* As nnc_hip_attend / nnc_hip_attend_device, then Qwen3.5's output gate:
+ * out[i] *= 1 / (1 + exp(-gate[i])), with gate [n_tok][n_head * head_dim]
+ * F32 in the same memory as q (reference model.cpp:1759-1760,
+ * nn_ops.cpp:1731-1742 nnc_mul_sigmoid_f32), fused into the kernels' last
+ * write. NNC_ERR_INVALID_ARGUMENT also for a NULL gate. */
+nnc_status nnc_hip_attend_gated(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out,
+                                int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+                                int32_t n_head, int32_t n_kv, int32_t head_dim, float scale);
+nnc_status nnc_hip_attend_gated_device(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out,
+                                       int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+                                       int32_t n_head, int32_t n_kv, int32_t head_dim, float scale);
 
 /* Waits for all work queued on the cache's stream. */
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv);

@@ -38,8 +38,6 @@ namespace nnchip
 {
 	namespace
 	{
-		constexpr int kMergeThreads = 256;
-
 		template <int HD, bool BF16>
 		struct decode_shape
 		{
@@ -63,142 +61,147 @@ namespace nnchip
 		}
 
 		// The work-group's result from its wavefronts' partials in s_wpart
-		// (o[head_dim], m, l per head, per wavefront), merged in wavefront
-		// order: a partial for the split merge, or, with a single split, o / l.
-		template <int HD, int G, int W>
-		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[G][HD + 2],
-		                                                size_t slot, int split, float* out)
+		// (o[head_dim], m, l per column, per wavefront), merged in wavefront
+		// order. Column c is query head c % G of token tok0 + c / G; the first
+		// n_cols columns are filled. With several splits the result is the
+		// split's partial; with one it is o * (1 / l), the expression the split
+		// merge ends with, so a token gets the same bits either way.
+		template <int HD, int G, int C, int W>
+		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[C][HD + 2],
+		                                                int tok0, int n_cols, int split)
 		{
 			constexpr int PW = HD + 2, kWaves = W, kThreads = 64 * W;
-			const int kvh = blockIdx.y;
+			const int kvh = blockIdx.y, n_kv = gridDim.y;
 			const bool single = p.n_split == 1;
-			float* gpart = p.part + (slot * p.n_split + split) * G * PW;
-			for (int idx = threadIdx.x; idx < G * PW; idx += kThreads)
+			for (int idx = threadIdx.x; idx < n_cols * PW; idx += kThreads)
 			{
-				const int h = idx / PW, d = idx % PW;
+				const int c = idx / PW, d = idx % PW;
+				const int tok = tok0 + c / G, h = c % G;
 				float m = -INFINITY;
 #pragma unroll
-				for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_wpart[w][h][HD]);
+				for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_wpart[w][c][HD]);
 				const float m_use = m == -INFINITY ? 0.0f : m;
+				float* gpart = p.part + ((static_cast<size_t>(tok) * n_kv + kvh) * p.n_split + split) * G * PW + h * PW;
 				if (d == HD)
 				{
-					if (!single) gpart[idx] = m;
+					if (!single) gpart[d] = m;
 					continue;
 				}
 				float r = 0.0f;
 #pragma unroll
 				for (int w = 0; w < kWaves; ++w)
-					r = fmaf(s_wpart[w][h][d], fast_exp2(s_wpart[w][h][HD] - m_use), r);
+					r = fmaf(s_wpart[w][c][d], fast_exp2(s_wpart[w][c][HD] - m_use), r);
 				if (!single)
-					gpart[idx] = r;
+					gpart[d] = r;
 				else if (d < HD)
 				{
 					float l = 0.0f;
 #pragma unroll
 					for (int w = 0; w < kWaves; ++w)
-						l = fmaf(s_wpart[w][h][HD + 1], fast_exp2(s_wpart[w][h][HD] - m_use), l);
-					out[static_cast<size_t>(kvh * G + h) * HD + d] = l > 0.0f ? r / l : 0.0f;
+						l = fmaf(s_wpart[w][c][HD + 1], fast_exp2(s_wpart[w][c][HD] - m_use), l);
+					const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+					const size_t oi = (static_cast<size_t>(tok) * p.n_head + kvh * G + h) * HD + d;
+					p.out[oi] = gated(r * inv, p.gate, oi);
 				}
 			}
 		}
 
-		// Merges the n_split partials of one (token, query head) in a fixed
-		// order and writes o / l (0 when l == 0, reference nn_ops.cpp:492),
-		// with kMergeThreads threads. Each thread issues all of its loads
-		// before using them: one (m, l) pair per split, then one float4 of o
-		// for every J-th split of its quad.
-		template <int HD, int G>
-		__device__ __forceinline__ void merge_splits(const decode_params& p, size_t slot, int tok, int kvh, int h)
+		// max over the wavefront, on every lane (DPP within 16-lane rows, then
+		// the permlane swaps across rows).
+		__device__ __forceinline__ float wave_max_dpp(float x)
 		{
-			constexpr int kThreads = kMergeThreads;
-			constexpr int PW = HD + 2;
-			constexpr int QN = HD / 4; // output quads of one head
-			constexpr int J = kThreads / QN; // threads per quad
-			constexpr int MAXS = 256; // splits
-			__shared__ float s_f[MAXS];
-			__shared__ float s_red[kThreads / 64];
-			__shared__ float4 s_acc[kThreads];
+			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false)));
+			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false)));
+			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false)));
+			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false)));
+			const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+			x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+			return max_with_other_half(x);
+		}
 
-			const float* hp = p.part + (slot * p.n_split * G + h) * PW; // split s at hp + s * G * PW
-			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-			const int q = threadIdx.x % QN, j = threadIdx.x / QN;
+		// Merges the n_split partials of one (token, query head) and writes
+		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492). One wavefront:
+		// every split's (m, l) and o slice is loaded before the first use, the
+		// maximum comes from DPP and lane swaps, and o and l are summed in
+		// ascending split order, one split at a time, with its weight broadcast
+		// by v_readlane. A split outside the token's span holds m = -inf, l = 0,
+		// o = 0 and adds exact zeros, so a token's result depends only on its own
+		// splits, whatever else the launch covered.
+		template <int HD, int G>
+		__global__ __launch_bounds__(64) void decode_merge_kernel(const decode_params p)
+		{
+			constexpr int PW = HD + 2, E = HD / 64, KB = 32, MS = kDecodeMaxSplits / 64;
+			typedef float fE __attribute__((ext_vector_type(E)));
+			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
+			const int n_kv = gridDim.x / G;
+			const int lane = threadIdx.x;
+			const int ns = p.n_split;
+			const size_t sstride = static_cast<size_t>(G) * PW;
+			const float* hp = p.part + ((static_cast<size_t>(tok) * n_kv + kvh) * ns * G + h) * PW; // split s at hp + s * sstride
 
-			// One round of loads: this thread's (m, l) and the first 8 of its o quads.
-			auto load_batch = [&](int s0, float4* v) __attribute__((always_inline))
+			float m[MS], l[MS];
+#pragma unroll
+			for (int j = 0; j < MS; ++j)
+			{
+				const int s = lane + 64 * j;
+				m[j] = s < ns ? hp[s * sstride + HD] : -INFINITY;
+				l[j] = s < ns ? hp[s * sstride + HD + 1] : 0.0f;
+			}
+			fE v[KB];
+			auto load_batch = [&](int b0) __attribute__((always_inline))
 			{
 #pragma unroll
-				for (int u = 0; u < 8; ++u)
+				for (int u = 0; u < KB; ++u)
 				{
-					const int sp = s0 + u * J;
-					v[u] = sp < p.n_split ? *reinterpret_cast<const float4*>(hp + static_cast<size_t>(sp) * G * PW + 4 * q)
-					                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+					const int s = min(b0 + u, ns - 1);
+					v[u] = *reinterpret_cast<const fE*>(hp + s * sstride + E * lane);
 				}
 			};
-			float4 v[8];
-			load_batch(j, v);
-			float m = -INFINITY, l = 0.0f;
-			if (threadIdx.x < p.n_split)
-			{
-				const float* sp = hp + static_cast<size_t>(threadIdx.x) * G * PW;
-				m = sp[HD];
-				l = sp[HD + 1];
-			}
-			float mx = m;
-#pragma unroll
-			for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-			__syncthreads(); // s_red / s_f / s_acc are free (a previous call may still read them)
-			if (lane == 0) s_red[wave] = mx;
-			__syncthreads();
-			mx = s_red[0];
-#pragma unroll
-			for (int w = 1; w < kThreads / 64; ++w) mx = fmaxf(mx, s_red[w]);
-			const float m_use = mx == -INFINITY ? 0.0f : mx;
-			const float f = threadIdx.x < p.n_split ? fast_exp2(m - m_use) : 0.0f;
-			s_f[threadIdx.x] = f;
-			float lw = l * f;
-#pragma unroll
-			for (int off = 32; off > 0; off >>= 1) lw += __shfl_xor(lw, off);
-			__syncthreads();
-			if (lane == 0) s_red[wave] = lw;
-			__syncthreads();
-			float L = s_red[0];
-#pragma unroll
-			for (int w = 1; w < kThreads / 64; ++w) L += s_red[w];
+			load_batch(0);
 
-			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-			for (int s0 = j;; s0 += 8 * J)
-			{
+			float mx = m[0];
 #pragma unroll
-				for (int u = 0; u < 8; ++u)
-				{
-					const int sp = s0 + u * J;
-					const float fw = sp < p.n_split ? s_f[sp] : 0.0f;
-					acc.x = fmaf(v[u].x, fw, acc.x);
-					acc.y = fmaf(v[u].y, fw, acc.y);
-					acc.z = fmaf(v[u].z, fw, acc.z);
-					acc.w = fmaf(v[u].w, fw, acc.w);
-				}
-				if (s0 + 8 * J >= p.n_split) break;
-				load_batch(s0 + 8 * J, v);
-			}
-			s_acc[threadIdx.x] = acc;
-			__syncthreads();
-			if (threadIdx.x < QN)
-			{
-				float4 r = s_acc[threadIdx.x];
+			for (int j = 1; j < MS; ++j) mx = fmaxf(mx, m[j]);
+			mx = wave_max_dpp(mx);
+			const float m_use = mx == -INFINITY ? 0.0f : mx;
+			float f[MS];
 #pragma unroll
-				for (int jj = 1; jj < J; ++jj)
+			for (int j = 0; j < MS; ++j) f[j] = lane + 64 * j < ns ? fast_exp2(m[j] - m_use) : 0.0f;
+
+			fE acc = fE(0.0f);
+			float L = 0.0f;
+			for (int b0 = 0;; b0 += KB)
+			{
+				const int g = b0 >> 6; // uniform; KB divides 64
+				float fg = f[0], lg = l[0];
+#pragma unroll
+				for (int j = 1; j < MS; ++j)
 				{
-					const float4 w4 = s_acc[jj * QN + threadIdx.x];
-					r.x += w4.x;
-					r.y += w4.y;
-					r.z += w4.z;
-					r.w += w4.w;
+					fg = g == j ? f[j] : fg;
+					lg = g == j ? l[j] : lg;
 				}
-				const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-				float* op = p.out + static_cast<size_t>(tok) * p.n_head * HD + static_cast<size_t>(kvh * G + h) * HD + 4 * threadIdx.x;
-				*reinterpret_cast<float4*>(op) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+#pragma unroll
+				for (int u = 0; u < KB; ++u)
+				{
+					if (b0 + u < ns) // uniform
+					{
+						const int src = (b0 & 63) + u;
+						const float fw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fg), src));
+						const float lw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lg), src));
+#pragma unroll
+						for (int e = 0; e < E; ++e) acc[e] = fmaf(v[u][e], fw, acc[e]);
+						L = fmaf(lw, fw, L);
+					}
+				}
+				if (b0 + KB >= ns) break;
+				load_batch(b0 + KB);
 			}
+			const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+			const size_t oi = (static_cast<size_t>(tok) * p.n_head + kvh * G + h) * HD + E * lane;
+			fE r;
+#pragma unroll
+			for (int e = 0; e < E; ++e) r[e] = gated(acc[e] * inv, p.gate, oi + e);
+			*reinterpret_cast<fE*>(p.out + oi) = r;
 		}
 
 		template <int HD, int G, bool BF16, int W>
@@ -230,8 +233,6 @@ namespace nnchip
 
 			const size_t head_off = static_cast<size_t>(kvh) * HD;
 			const float* q = p.q + static_cast<size_t>(tok) * p.n_head * HD;
-			float* out = p.out + static_cast<size_t>(tok) * p.n_head * HD;
-			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh; // (token, KV head)
 
 			float m_run = -INFINITY; // per column (head), log2 units
 			float l_run = 0.0f; // this lane's share of the column's sum
@@ -469,7 +470,7 @@ namespace nnchip
 			}
 			__syncthreads();
 
-			write_wg_result<HD, G, W>(p, s_wpart, slot, split, out);
+			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split);
 		}
 
 		// Chunk sizes of the BF16 kernel: CH keys per wavefront chunk (a chunk's
@@ -515,11 +516,18 @@ namespace nnchip
 		//                     operand (V^T) is read back with ds_read_b64_tr_b16
 		//                     in that same key order. P is split into bf16 hi + lo,
 		//                     so both products are near-fp32 against the exact
-		//                     bf16 K and V. O^T's columns are the heads, so the
-		//                     online-softmax rescale stays in the lane.
+		//                     bf16 K and V. O^T's columns are the (token, head)
+		//                     pairs, so the online-softmax rescale stays in the
+		//                     lane.
+		// The 16 MFMA columns hold up to T = 16 / G tokens of G query heads: the
+		// tokens of a batch share every K and V load, and each column is masked
+		// to its own token's span. A chunk outside a column's span leaves that
+		// column's state bit-for-bit unchanged (its weights are exact zeros and
+		// its rescale factor exactly 1), so a token gets the same bits alone as
+		// in any batch over the same split grid.
 		// Loads run one chunk ahead: a chunk's K registers are reissued as soon
 		// as its scores are done, its V registers as soon as they are in LDS.
-		template <int HD, int G, int W, int CHK>
+		template <int HD, int G, int W, int CHK, int T>
 		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_kernel(
 			const decode_params p)
 		{
@@ -527,9 +535,10 @@ namespace nnchip
 			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
 			              NV = S::NV, VPITCH = S::VPITCH;
 			constexpr int PW = HD + 2, kWaves = W;
+			static_assert(T >= 1 && T * G <= 16, "tokens per work-group");
 
 			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
-			__shared__ float s_wpart[W][G][PW];
+			__shared__ float s_wpart[W][T * G][PW];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
@@ -537,18 +546,25 @@ namespace nnchip
 			const int grp = lane >> 4;
 			const int kvh = blockIdx.y;
 			const int split = blockIdx.x;
-			const int tok = blockIdx.z;
-			const int n_kv = gridDim.y;
+			const int tok0 = blockIdx.z * T;
+			const int n_tt = min(T, p.n_tok - tok0); // tokens of this work-group
+			const int tt = col / G; // this lane's column: token tok0 + tt, head col % G
 
-			int first, last;
-			attn_span(p.causal, p.window, p.pos0 + tok, p.n_seq, first, last);
 			const int sbase = p.split_base + split * p.split_keys;
-			const int s0 = max(first, sbase);
-			const int s1 = min(last, sbase + p.split_keys - 1);
+			const int send = sbase + p.split_keys - 1;
+			// The column's keys in this split (none for a column past the batch),
+			// and the work-group's: the union over its tokens, [first of the first
+			// token, last of the last] (both ends move forward with the position).
+			int first, last;
+			attn_span(p.causal, p.window, p.pos0 + tok0 + tt, p.n_seq, first, last);
+			const int col_s0 = tt < n_tt ? max(first, sbase) : 1;
+			const int col_s1 = tt < n_tt ? min(last, send) : 0;
+			int f0, l0, fL, lL;
+			attn_span(p.causal, p.window, p.pos0 + tok0, p.n_seq, f0, l0);
+			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
+			const int s0 = max(f0, sbase);
+			const int s1 = min(lL, send);
 			const size_t head_off = static_cast<size_t>(kvh) * HD;
-			const float* q = p.q + static_cast<size_t>(tok) * p.n_head * HD;
-			float* out = p.out + static_cast<size_t>(tok) * p.n_head * HD;
-			const size_t slot = static_cast<size_t>(tok) * n_kv + kvh;
 			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
 			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
 			uint16_t* vt = s_v[wave];
@@ -614,9 +630,10 @@ namespace nnchip
 			for (int kk = 0; kk < KK; ++kk)
 			{
 				float x[8];
-				if (col < G)
+				if (tt < n_tt)
 				{
-					const float* qp = q + static_cast<size_t>(kvh * G + col) * HD + 32 * kk + 8 * grp;
+					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + kvh * G + col % G) * HD + 32 * kk +
+					                  8 * grp;
 					const float4 a = *reinterpret_cast<const float4*>(qp);
 					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
 					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
@@ -674,7 +691,7 @@ namespace nnchip
 					for (int i = 0; i < 4; ++i)
 					{
 						const int k = cbase + 16 * t + 4 * grp + i;
-						const float v = (k >= clo && k <= chi) ? sc[t][i] : -INFINITY;
+						const float v = (k >= col_s0 && k <= col_s1) ? sc[t][i] : -INFINITY;
 						sc[t][i] = v;
 						m_loc = fmaxf(m_loc, v);
 					}
@@ -724,7 +741,7 @@ namespace nnchip
 			// Wavefront partial: each (head, d) of O^T has one owner lane.
 			l_run += __shfl_xor(l_run, 16);
 			l_run += __shfl_xor(l_run, 32);
-			if (col < G)
+			if (tt < n_tt) // col < n_tt * G <= T * G
 			{
 #pragma unroll
 				for (int db = 0; db < DB; ++db)
@@ -737,16 +754,7 @@ namespace nnchip
 				}
 			}
 			__syncthreads();
-			write_wg_result<HD, G, W>(p, s_wpart, slot, split, out);
-		}
-
-		// Grid: (n_kv * G, n_tok); one (token, query head) per work-group.
-		template <int HD, int G>
-		__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const decode_params p)
-		{
-			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
-			const int n_kv = gridDim.x / G;
-			merge_splits<HD, G>(p, static_cast<size_t>(tok) * n_kv + kvh, tok, kvh, h);
+			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split);
 		}
 
 		// Keys per wavefront chunk of the BF16 kernel (4 wavefronts, one per
@@ -774,13 +782,21 @@ namespace nnchip
 			const dim3 grid(p.n_split, n_kv, n_tok);
 			if (BF16 && !decode_valu_pv())
 			{
-				decode_bf16_kernel<HD, G, 4, bf16_chunk(HD)><<<grid, 256, 0, stream>>>(p);
+				// One token: the one-token instance (less LDS for partials);
+				// batches: 16 / G tokens per work-group. Both compute a token's
+				// column with the same operations.
+				constexpr int T = 16 / G;
+				if (n_tok == 1)
+					decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1><<<grid, 256, 0, stream>>>(p);
+				else
+					decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), T>
+						<<<dim3(p.n_split, n_kv, (n_tok + T - 1) / T), 256, 0, stream>>>(p);
 			}
 			else if (waves == 8)
 				decode_kernel<HD, G, BF16, 8><<<grid, 512, 0, stream>>>(p);
 			else
 				decode_kernel<HD, G, BF16, 4><<<grid, 256, 0, stream>>>(p);
-			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(n_kv * G, n_tok), kMergeThreads, 0, stream>>>(p);
+			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(n_kv * G, n_tok), 64, 0, stream>>>(p);
 		}
 
 		template <int HD, bool BF16>

@@ -486,8 +486,15 @@ namespace nnchip
 					acc.z += v.z;
 					acc.w += v.w;
 				}
-				float* op = p.out + static_cast<size_t>(gr / G) * q_stride + static_cast<size_t>(kvh * G + gr % G) * HD;
-				*reinterpret_cast<float4*>(op + 4 * d4) = acc;
+				const size_t oi = static_cast<size_t>(gr / G) * q_stride + static_cast<size_t>(kvh * G + gr % G) * HD + 4 * d4;
+				if (p.gate)
+				{
+					acc.x = gated(acc.x, p.gate, oi);
+					acc.y = gated(acc.y, p.gate, oi + 1);
+					acc.z = gated(acc.z, p.gate, oi + 2);
+					acc.w = gated(acc.w, p.gate, oi + 3);
+				}
+				*reinterpret_cast<float4*>(p.out + oi) = acc;
 			}
 		}
 

@@ -165,5 +165,12 @@ namespace nnchip
 
 	__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+	// Qwen3.5's output gate on one attention output (reference
+	// model.cpp:1759-1760, nn_ops.cpp:1731-1742): y * (1 / (1 + e^-g)).
+	__device__ __forceinline__ float gated(float y, const float* gate, size_t i)
+	{
+		return gate ? y * (1.0f / (1.0f + expf(-gate[i]))) : y;
+	}
+
 	constexpr float kLog2e = 1.4426950408889634f;
 }

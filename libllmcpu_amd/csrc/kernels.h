@@ -16,22 +16,28 @@ namespace nnchip
 		float* out; // [n_tok][n_head * head_dim]
 		const void* K; // [rows][kv_dim], BF16 bits or F32
 		const void* V;
+		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		float* part; // [n_tok][n_kv][n_split][group][head_dim + 2]: o, then m (log2 units), then l
 		int rows, kv_dim, n_head;
 		int pos0, n_seq, window, causal; // token t sits at pos0 + t
+		int n_tok; // tokens in this launch
 		int split_base; // first key of split 0, a multiple of split_keys
 		int split_keys; // keys per work-group, a multiple of decode_wg_keys()
-		int n_split; // work-groups per (token, KV head)
+		int n_split; // work-groups per (token, KV head), at most kDecodeMaxSplits
 		float qscale; // scale * log2(e)
 	};
+
+	constexpr int kDecodeMaxSplits = 256;
 
 	// Keys one decode work-group consumes per iteration, for a head size and
 	// element type; split_keys must be a multiple of it.
 	int decode_wg_keys(int head_dim, bool bf16);
 
-	// Launches the decode kernel over an (n_split, n_kv, n_tok) grid, then
-	// (n_split > 1) the split merge over (n_kv, n_tok); returns false when
-	// (head_dim, group, bf16) has no instantiation.
+	// Launches the decode kernel over an (n_split, n_kv, token groups) grid,
+	// then (n_split > 1) the split merge over (n_kv * group, n_tok); returns
+	// false when (head_dim, group, bf16) has no instantiation. A token's
+	// result depends only on its own span and the split grid (split_keys and
+	// the absolute split boundaries), not on the other tokens of the launch.
 	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
 	                   hipStream_t stream);
 
@@ -40,6 +46,7 @@ namespace nnchip
 	{
 		const float* q; // [n_tok][n_head * head_dim]
 		float* out; // [n_tok][n_head * head_dim]
+		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		const void* K; // [rows][kv_dim]
 		const void* V;
 		int rows, kv_dim, n_head, n_kv;

@@ -72,8 +72,13 @@ namespace
 	};
 
 	constexpr int kAttnBlock = 256; // reference model.h:229
-	constexpr int kMaxSplits = 256; // the decode kernel's final merge holds 256 weights per head
 	constexpr int32_t kDecodeChunk = 1024; // tokens per split-K launch
+	// Most tokens one forward pass of an nnc session carries
+	// (MODEL_PREFILL_BATCH, reference model.h:330; session.cpp:340), its MTP
+	// verification batches included (n_draft + 1, session.cpp:357, :516).
+	// Batches up to this size run through the split-K kernel on each token's
+	// own split grid, so every token gets the bits a one-token call gives it.
+	constexpr int32_t kSessionBatch = 16;
 }
 
 struct nnc_hip_kv
@@ -87,6 +92,7 @@ struct nnc_hip_kv
 	dev_scratch part; // decode partials
 	dev_scratch q; // staging of host q / out / append rows
 	dev_scratch out;
+	dev_scratch gate;
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 };
@@ -102,7 +108,7 @@ namespace
 			if (b.k) (void)hipFree(b.k);
 			if (b.v) (void)hipFree(b.v);
 		}
-		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->rows_k, &kv->rows_v})
+		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
 		delete kv;
@@ -166,40 +172,47 @@ namespace
 		return NNC_OK;
 	}
 
-	// Split size: about one work-group per CU over all (token, KV head)
-	// pairs, a multiple of what one work-group iteration consumes, and at
-	// most kMaxSplits splits.
-	nnc_status decode_chunk(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, int32_t n_tok, int32_t pos0,
-	                        int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
-	                        float scale)
+	// Keys per decode work-group for the span [kmin, kmax] shared out over
+	// `pairs` (token, KV head) pairs: about one work-group per CU, a multiple
+	// of what one work-group iteration consumes, at most kDecodeMaxSplits
+	// splits.
+	int split_keys_for(const nnc_hip_kv* kv, int kmin, int kmax, long long pairs, int wgk)
 	{
-		const int group = n_head / n_kv;
-		const bool bf16 = kv->bf16;
-		int kmin, kmax, unused;
-		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, kmin, unused);
-		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, unused, kmax);
-		if (kmax < kmin) return nnchip::launch_zero(out, static_cast<size_t>(n_tok) * n_head * head_dim, kv->stream)
-			                       ? NNC_OK
-			                       : NNC_ERR_IO;
-		const int wgk = nnchip::decode_wg_keys(head_dim, bf16);
-		const int span = kmax - kmin + 1;
-		const long long pairs = static_cast<long long>(n_tok) * n_kv;
+		const int span = std::max(1, kmax - kmin + 1);
 		const long long want = std::max<long long>(1, 1LL * kv->n_cu / std::max<long long>(pairs, 1));
 		long long sk = (span + want - 1) / want;
 		if (const char* e = std::getenv("NNC_HIP_DECODE_SPLIT")) // keys per work-group, for tuning
 			if (std::atoll(e) > 0) sk = std::atoll(e);
 		sk = std::max<long long>(wgk, (sk + wgk - 1) / wgk * wgk);
-		while ((kmax / sk) - (kmin / sk) + 1 > kMaxSplits) sk += wgk;
-		const int split_keys = static_cast<int>(sk);
+		while ((kmax / sk) - (kmin / sk) + 1 > nnchip::kDecodeMaxSplits) sk += wgk;
+		return static_cast<int>(sk);
+	}
+
+	// One split-K launch (and its merge) over tokens pos0 .. pos0 + n_tok - 1
+	// on the absolute split grid of split_keys keys.
+	nnc_status decode_launch(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
+	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+	                         int32_t head_dim, float scale, int split_keys)
+	{
+		const int group = n_head / n_kv;
+		int kmin, kmax, unused;
+		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, kmin, unused);
+		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, unused, kmax);
+		if (kmax < kmin)
+			return nnchip::launch_zero(out, static_cast<size_t>(n_tok) * n_head * head_dim, kv->stream) ? NNC_OK
+			                                                                                             : NNC_ERR_IO;
 		const int split_base = (kmin / split_keys) * split_keys;
 		const int n_split = kmax / split_keys - kmin / split_keys + 1;
-
+		if (n_split > nnchip::kDecodeMaxSplits)
+			return fail(NNC_ERR_IO, "decode split grid of %d splits (at most %d)", n_split, nnchip::kDecodeMaxSplits);
+		const long long pairs = static_cast<long long>(n_tok) * n_kv;
 		const size_t part_floats = static_cast<size_t>(pairs) * n_split * group * (head_dim + 2);
 		if (nnc_status s = reserve(kv, kv->part, part_floats * sizeof(float), "decode scratch")) return s;
 
 		nnchip::decode_params p{};
 		p.q = q;
 		p.out = out;
+		p.gate = gate;
 		p.K = b.k;
 		p.V = b.v;
 		p.part = static_cast<float*>(kv->part.ptr);
@@ -210,17 +223,58 @@ namespace
 		p.n_seq = n_seq;
 		p.window = window;
 		p.causal = causal ? 1 : 0;
+		p.n_tok = n_tok;
 		p.split_base = split_base;
 		p.split_keys = split_keys;
 		p.n_split = n_split;
 		p.qscale = scale * 1.4426950408889634f;
-		if (!nnchip::launch_decode(p, n_kv, n_tok, head_dim, group, bf16, kv->stream))
+		if (!nnchip::launch_decode(p, n_kv, n_tok, head_dim, group, kv->bf16, kv->stream))
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no decode kernel for head_dim %d, group %d", head_dim, group);
 		NNC_HIP_TRY(hipGetLastError(), "decode launch");
 		return NNC_OK;
 	}
 
-	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
+	// A session-sized batch: each token on the split grid a one-token call
+	// gives it (the split size of its own span over n_kv pairs). Consecutive
+	// tokens with the same split size share a launch; a token's result does
+	// not depend on the rest of its launch, so it matches the one-token call
+	// bit for bit.
+	nnc_status decode_tokens(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
+	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+	                         int32_t head_dim, float scale)
+	{
+		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16);
+		auto span_of = [&](int32_t t, int& first, int& last)
+		{ nnchip::attn_span(causal ? 1 : 0, window, pos0 + t, n_seq, first, last); };
+		auto own_split = [&](int32_t t)
+		{
+			int first, last;
+			span_of(t, first, last);
+			return split_keys_for(kv, first, last, n_kv, wgk);
+		};
+		const size_t tok_floats = static_cast<size_t>(n_head) * head_dim;
+		for (int32_t t = 0; t < n_tok;)
+		{
+			const int sk = own_split(t);
+			int f0, l0;
+			span_of(t, f0, l0);
+			int32_t u = t + 1;
+			for (; u < n_tok && own_split(u) == sk; ++u)
+			{
+				int fu, lu;
+				span_of(u, fu, lu);
+				if (lu / sk - f0 / sk + 1 > nnchip::kDecodeMaxSplits) break; // the launch's split grid stays mergeable
+			}
+			if (nnc_status s = decode_launch(kv, b, q + t * tok_floats, out + t * tok_floats,
+			                                 gate ? gate + t * tok_floats : nullptr, u - t, pos0 + t, n_seq,
+			                                 window, causal, n_head, n_kv, head_dim, scale, sk))
+				return s;
+			t = u;
+		}
+		return NNC_OK;
+	}
+
+	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, const float* gate, int32_t n_tok, int32_t pos0,
 	                       int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
 	                       float scale)
 	{
@@ -237,13 +291,18 @@ namespace
 		const int kmin = first0, kmax = last1;
 		if (kmax < kmin) return nnchip::launch_zero(out, q_floats, kv->stream) ? NNC_OK : NNC_ERR_IO;
 
-		// Prefill kernel for BF16 batches; the split-K kernel for decode and for
-		// F32 batches (exact fp32 products against F32 K/V).
-		if (n_tok > 1 && bf16)
+		// Decode and session-sized batches: the split-K kernel, each token on
+		// its own split grid. Larger batches: the prefill kernel for BF16, the
+		// split-K kernel over the batch's span for F32 (exact fp32 products
+		// against F32 K/V).
+		if (n_tok <= kSessionBatch)
+			return decode_tokens(kv, b, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+		if (bf16)
 		{
 			nnchip::prefill_params p{};
 			p.q = q;
 			p.out = out;
+			p.gate = gate;
 			p.K = b.k;
 			p.V = b.v;
 			p.rows = b.rows;
@@ -268,8 +327,13 @@ namespace
 		{
 			const int32_t nt = std::min(kDecodeChunk, n_tok - t0);
 			const size_t off = static_cast<size_t>(t0) * n_head * head_dim;
-			if (nnc_status s = decode_chunk(kv, b, q + off, out + off, nt, pos0 + t0, n_seq, window, causal, n_head, n_kv,
-			                                head_dim, scale))
+			int kmin, kmax, unused;
+			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0, n_seq, kmin, unused);
+			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
+			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * n_kv,
+			                              nnchip::decode_wg_keys(head_dim, bf16));
+			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, nt, pos0 + t0, n_seq, window, causal, n_head,
+			                                 n_kv, head_dim, scale, sk))
 				return s;
 		}
 		return NNC_OK;
@@ -299,7 +363,7 @@ namespace
 		if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
 			return fail(NNC_ERR_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
 		// The BF16 batch kernel addresses a buffer with 32-bit byte offsets.
-		if (n_tok > 1 && kv->bf16 && static_cast<uint64_t>(b.rows) * b.kv_dim * 2 > 0x7fffffffu)
+		if (n_tok > kSessionBatch && kv->bf16 && static_cast<uint64_t>(b.rows) * b.kv_dim * 2 > 0x7fffffffu)
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "a %d x %d BF16 buffer is too large for the batch kernel (2 GiB)",
 			            b.rows, b.kv_dim);
 		// Every key the batch reads must still be in the buffer: the newest
@@ -477,25 +541,41 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
 	return NNC_OK;
 }
 
+namespace
+{
+	// The host-buffer form of the op: q (and gate) staged to the device, out
+	// downloaded, the call synchronous with respect to out.
+	nnc_status attend_host(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out, int32_t n_tok,
+	                       int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
+	                       int32_t head_dim, float scale)
+	{
+		// Host pointers need no alignment: they are staged.
+		static const float aligned_probe[4] = {0, 0, 0, 0};
+		if (nnc_status s = check_attend(kv, buf, q ? aligned_probe : nullptr, out ? aligned_probe : nullptr, n_tok,
+		                                pos0, n_seq, window, causal, n_head, n_kv, head_dim))
+			return s;
+		const size_t bytes = static_cast<size_t>(n_tok) * n_head * head_dim * sizeof(float);
+		if (nnc_status s = reserve(kv, kv->q, bytes, "q staging")) return s;
+		if (nnc_status s = reserve(kv, kv->out, bytes, "out staging")) return s;
+		if (gate)
+			if (nnc_status s = reserve(kv, kv->gate, bytes, "gate staging")) return s;
+		NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, q, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
+		if (gate) NNC_HIP_TRY(hipMemcpyAsync(kv->gate.ptr, gate, bytes, hipMemcpyHostToDevice, kv->stream), "gate upload");
+		if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), static_cast<float*>(kv->out.ptr),
+		                               gate ? static_cast<const float*>(kv->gate.ptr) : nullptr, n_tok, pos0, n_seq,
+		                               window, causal, n_head, n_kv, head_dim, scale))
+			return s;
+		NNC_HIP_TRY(hipMemcpyAsync(out, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
+		NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "attention");
+		return NNC_OK;
+	}
+}
+
 nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
                           int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
                           float scale)
 {
-	// Host pointers need no alignment: they are staged.
-	static const float aligned_probe[4] = {0, 0, 0, 0};
-	if (nnc_status s = check_attend(kv, buf, q ? aligned_probe : nullptr, out ? aligned_probe : nullptr, n_tok, pos0,
-	                                n_seq, window, causal, n_head, n_kv, head_dim))
-		return s;
-	const size_t bytes = static_cast<size_t>(n_tok) * n_head * head_dim * sizeof(float);
-	if (nnc_status s = reserve(kv, kv->q, bytes, "q staging")) return s;
-	if (nnc_status s = reserve(kv, kv->out, bytes, "out staging")) return s;
-	NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, q, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
-	if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), static_cast<float*>(kv->out.ptr),
-	                               n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale))
-		return s;
-	NNC_HIP_TRY(hipMemcpyAsync(out, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
-	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "attention");
-	return NNC_OK;
+	return attend_host(kv, buf, q, nullptr, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
 }
 
 nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
@@ -504,7 +584,25 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
 {
 	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
 		return s;
-	return attend_impl(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+	return attend_impl(kv, buf, q, out, nullptr, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+}
+
+nnc_status nnc_hip_attend_gated(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out,
+                                int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+                                int32_t n_head, int32_t n_kv, int32_t head_dim, float scale)
+{
+	if (!gate) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL gate");
+	return attend_host(kv, buf, q, gate, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+}
+
+nnc_status nnc_hip_attend_gated_device(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out,
+                                       int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+                                       int32_t n_head, int32_t n_kv, int32_t head_dim, float scale)
+{
+	if (!gate) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL gate");
+	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
+		return s;
+	return attend_impl(kv, buf, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
 }
 
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv)

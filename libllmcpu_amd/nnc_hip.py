@@ -81,6 +81,8 @@ SIGNATURES = {
     "nnc_hip_kv_read": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_attend": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_device": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
+    "nnc_hip_attend_gated": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
+    "nnc_hip_attend_gated_device": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_kv_sync": (C.c_int, [_P]),
     "nnc_hip_kv_stream": (_P, [_P]),
     "nnc_hip_fill_normal": (C.c_int, [_P, _U64, _U64, _I, _B, _P]),
@@ -232,16 +234,26 @@ class KVCache:
         return k, v
 
     def attend(self, buf: int, q: np.ndarray, *, pos0: int, n_seq: int | None = None, window: int = 0,
-               causal: bool = True, n_head: int, n_kv: int, head_dim: int, scale: float) -> np.ndarray:
+               causal: bool = True, n_head: int, n_kv: int, head_dim: int, scale: float,
+               gate: np.ndarray | None = None) -> np.ndarray:
         """Attention of q [n_tok, n_head*head_dim] (float32) over buffer `buf`;
-        returns out of the same shape."""
+        returns out of the same shape. With `gate` (same shape), out is scaled
+        by sigmoid(gate) as Qwen3.5 does."""
         q = np.ascontiguousarray(q, dtype=np.float32)
         n_tok = q.size // (n_head * head_dim)
         out = np.empty((n_tok, n_head * head_dim), dtype=np.float32)
         if n_seq is None:
             n_seq = pos0 + n_tok
-        _check(self._lib.nnc_hip_attend(self.handle, buf, _ptr(q), _ptr(out), n_tok, pos0, n_seq, window,
-                                        bool(causal), n_head, n_kv, head_dim, float(scale)))
+        if gate is None:
+            _check(self._lib.nnc_hip_attend(self.handle, buf, _ptr(q), _ptr(out), n_tok, pos0, n_seq, window,
+                                            bool(causal), n_head, n_kv, head_dim, float(scale)))
+        else:
+            gate = np.ascontiguousarray(gate, dtype=np.float32)
+            if gate.size != q.size:
+                raise ValueError(f"gate has {gate.size} values, q {q.size}")
+            _check(self._lib.nnc_hip_attend_gated(self.handle, buf, _ptr(q), _ptr(gate), _ptr(out), n_tok, pos0,
+                                                  n_seq, window, bool(causal), n_head, n_kv, head_dim,
+                                                  float(scale)))
         return out
 
     def attend_device(self, buf: int, q_dev: int, out_dev: int, *, n_tok: int, pos0: int, n_seq: int | None = None,

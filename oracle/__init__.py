@@ -68,6 +68,7 @@ class _Lib:
         f("rmsnorm_groups", None, [_P, _SZ, _SZ, _F])
         f("rmsnorm_gamma", None, [_P, _SZ, _SZ, _P, _F])
         f("rmsnorm_plain", None, [_P, _SZ, _SZ, _F])
+        f("mul_sigmoid", None, [_P, _P, _SZ])
 
     def _fn(self, name, res, args):
         fn = getattr(self.lib, self.prefix + name)
@@ -138,6 +139,14 @@ class _Lib:
         x = np.ascontiguousarray(x, dtype=np.float32).copy()
         self._rmsnorm_plain(_p(x), x.size // dim, dim, eps)
         return x
+
+    def mul_sigmoid(self, y, g):
+        """y * sigmoid(g), elementwise (Qwen3.5's output gate)."""
+        y = np.ascontiguousarray(y, dtype=np.float32).copy()
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        assert g.size == y.size
+        self._mul_sigmoid(_p(y), _p(g), y.size)
+        return y
 
 
 def _layer_call(fn, extra, q, K, V, kv_bf16, rows, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale):

@@ -17,6 +17,8 @@
 //   orc_rmsnorm_plain                      reference src/libnnc/nn_ops.cpp:558-588
 //   orc_prep_append                        reference src/libnnc/model.cpp:1616-1691 (per-head
 //                                          Q/K/V norms, RoPE on Q and K, K/V append)
+//   orc_mul_sigmoid                        reference src/libnnc/nn_ops.cpp:1731-1742 (Qwen3.5's
+//                                          output gate, model.cpp:1759-1760)
 // and two checkers that are not restatements:
 //   orc_textbook_attend   double-precision softmax attention per query, the
 //                         scalar reference of reference src/appnnc/tests.cpp:2424-2446
@@ -379,6 +381,15 @@ void orc_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
 		const float r = static_cast<float>(1.0 / std::sqrt(s2 / static_cast<double>(dim) + eps));
 		for (size_t i = 0; i < dim; ++i) xg[i] *= r;
 	}
+}
+
+// y[i] *= sigmoid(g[i]): in runs of eight, y * (1 / (1 + exp(-g))); the tail
+// past the last full run as y / (1 + exp(-g)).
+void orc_mul_sigmoid(float* y, const float* g, size_t n)
+{
+	size_t i = 0;
+	for (; i + 8 <= n; ++i) y[i] = y[i] * (1.0f / (1.0f + std::exp(-g[i])));
+	for (; i < n; ++i) y[i] /= 1.0f + std::exp(-g[i]);
 }
 
 // The step before the attention core, in the reference's order: per-head

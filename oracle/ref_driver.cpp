@@ -15,6 +15,7 @@
 //   ref_rmsnorm_groups / ref_rmsnorm_gamma call nnc_rmsnorm_gamma_multi_f32
 //       (reference nn_ops.h:79), ref_rmsnorm_plain calls nnc_rmsnorm_f32
 //       (reference nn_ops.h:73);
+//   ref_mul_sigmoid  calls nnc_mul_sigmoid_f32 (reference nn_ops.h:248);
 //   ref_set_threads / ref_threads call nnc_set_num_threads / nnc_num_threads
 //       (reference nnc.h:104-105);
 //   ref_attend_layer drives nnc_attn_block/merge/finish through the reference's
@@ -114,6 +115,8 @@ void ref_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
 {
 	for (size_t g = 0; g < n_groups; ++g) nnc_rmsnorm_f32(x + g * dim, x + g * dim, dim, eps);
 }
+
+void ref_mul_sigmoid(float* y, const float* g, size_t n) { nnc_mul_sigmoid_f32(y, g, n); }
 
 void ref_set_threads(int n) { nnc_set_num_threads(n); }
 int ref_threads(void) { return nnc_num_threads(); }

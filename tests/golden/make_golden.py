@@ -149,6 +149,14 @@ def main() -> int:
     data["rmsnorm_gamma80/gamma"] = g80
     data["rmsnorm_gamma80/out"] = ref.rmsnorm_gamma(x80, 80, g80)
     data["rmsnorm_plain80/out"] = ref.rmsnorm_plain(x80, 80)
+    # Qwen3.5's output gate: a length that leaves a tail past the runs of
+    # eight, gates from -90 to 90 (both saturated ends), and exact zeros.
+    yg = rng.standard_normal(1003).astype(np.float32)
+    gg = (rng.standard_normal(1003) * 8.0).astype(np.float32)
+    gg[:6] = [0.0, 90.0, -90.0, 40.0, -40.0, 0.0]
+    data["gate/y"] = yg
+    data["gate/g"] = gg
+    data["gate/out"] = ref.mul_sigmoid(yg, gg)
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
     return 0

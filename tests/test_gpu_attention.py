@@ -121,6 +121,25 @@ def test_decode_edge_spans(orc):
         assert np.all(got == 0.0)
 
 
+def test_drafter_reads_target_cache(orc):
+    """An MTP drafter attends over its target's cache (kv_ext, reference
+    model.cpp:1664, :1707) with n_seq = the target's cur_pos, which can lie
+    below the drafter's own position: keys 0 .. n_seq - 1 (causal) or the
+    window's part of them."""
+    cfg = synth.CONFIGS["D"]
+    rows, n_seq = 2048, 1990
+    K, V = synth.cache_buffer(cfg, 0, rows, n_seq)
+    kw = dict(n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+    with nh.KVCache([rows], [cfg.kv_dim]) as kv:
+        kv.append(0, 0, K, V)
+        for pos, window in ((1995, 0), (1992, 700), (1989, 0)):
+            say(f"case drafter read pos {pos} n_seq {n_seq} window {window}")
+            q = synth.qk_rows(cfg, 0, 0, np.array([pos]), cfg.n_head)
+            got = kv.attend(0, q, pos0=pos, n_seq=n_seq, window=window, **kw)
+            want = orc.attend_layer(q, K, V, kv_bf16=True, rows=rows, pos0=pos, n_seq=n_seq, window=window, **kw)
+            assert errors(got, want)[0] <= cfg.tol
+
+
 # ---- prefill ----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("key,layer,n_seq,chunk", [
@@ -140,10 +159,11 @@ def test_prefill_parity(orc, key, layer, n_seq, chunk):
 
 
 def test_prefill_odd_batches(orc):
-    """Batches of 2, 5 and 37 tokens (rows that do not fill a tile), and a
-    bidirectional batch (the embedding path's spans) with and without a window."""
+    """Batches of 2 and 5 tokens (session-sized: the split-K kernel), 17 and 37
+    (the prefill kernel, rows that do not fill a tile), and a bidirectional
+    batch (the embedding path's spans) with and without a window."""
     cfg = synth.CONFIGS["D"]
-    for n_tok in (2, 5, 37):
+    for n_tok in (2, 5, 17, 37):
         got, want = run_case(orc, cfg, 3, n_seq=900, pos0=900 - n_tok, n_tok=n_tok)
         assert errors(got, want)[0] <= cfg.tol, n_tok
     ecfg = synth.AttnConfig(8, "embed", 4, 1, 256, 1)
