@@ -347,7 +347,7 @@ def main() -> int:
                    "kv_dtype": "bf16", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dec_launch_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_launch_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_bf16_kernel<128,4,4,64> + decode_merge_kernel<128,4> (one attend call)",
+                     "kernel": "decode_bf16_kernel<128,4,4,64,1> + decode_merge_kernel<128,4> (one attend call)",
                      "avg_launch_us": round(dec_launch_us, 3), "bytes_per_launch": decode_bytes(CTX)},
         "prefill": {"metric": "prefill-attn TFLOP/s", "value": round(pre_tflops, 1), "unit": "TFLOP/s",
                     "ms_per_step": round(pre_step_ms, 3), "steps": args.prefill_steps,
