@@ -137,6 +137,66 @@ def pmc_summary(fetch_csv: str, write_csv: str) -> dict:
 CALIBRATE_MIB = 1024
 
 
+# Qwen3-4B's weight gemvs of one layer (rows, cols): q, k, v, o, gate, up, down.
+GEMV_LAYER = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)]
+GEMV_WORKING_SET = 640 << 20  # bytes of distinct weights per format, past the 256 MB Infinity Cache
+
+
+def gemv_bytes(fmt: str, rows: int, cols: int) -> int:
+    """Weight bytes of one matrix in nnc's layouts (reference docs/design.md:141-193)."""
+    return {"bf16": 2 * rows * cols, "q8_0": rows * cols + 2 * rows * cols // 32,
+            "q4_s": rows * cols // 2 + 4 * rows * cols // 32}[fmt]
+
+
+def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
+    """The weight gemvs of Qwen3-4B layers in each of nnc's three weight
+    layouts, one activation vector (decode) and 16 (a session batch), weights
+    resident in HBM and rotated over enough layers to exceed the Infinity
+    Cache. Algorithmic bytes: the weights (with scales and biases) plus X and Y."""
+    res = {}
+    x = hip_rt.malloc(16 * 9728 * 4)
+    y = hip_rt.malloc(16 * 9728 * 4)
+    nh.fill_normal(x, 16 * 9728, 99, 0, False, stream)
+    for fmt in ("bf16", "q8_0", "q4_s"):
+        layer_bytes = sum(gemv_bytes(fmt, r, c) for r, c in GEMV_LAYER)
+        n_layers = -(-GEMV_WORKING_SET // layer_bytes)
+        mats, bufs = [], []
+        for li in range(n_layers):
+            for mi, (r, c) in enumerate(GEMV_LAYER):
+                parts = {"bf16": [2 * r * c], "q8_0": [r * c, 2 * r * c // 32],
+                         "q4_s": [r * c // 2, 2 * r * c // 32, 2 * r * c // 32]}[fmt]
+                ptrs = []
+                for j, nbytes in enumerate(parts):
+                    d = hip_rt.malloc(nbytes)
+                    # Random bits: BF16 N(0,1) pairs (weights, scales, or int8 / nibble bytes).
+                    nh.fill_normal(d, nbytes // 2, 5000 + 100 * li + 10 * mi + j, 0, True, stream)
+                    bufs.append(d)
+                    ptrs.append(d)
+                mats.append((tuple(ptrs), r, c))
+        kv.sync()
+        for n in (1, 16):
+            def step():
+                for w, r, c in mats:
+                    kv.gemv_device(fmt, w, x, y, rows=r, cols=c, n_batch=n)
+
+            step()
+            hip_rt.sync()
+            ms, _ = timed(step, 5)
+            us_layer = ms * 1e3 / (5 * n_layers)
+            nbytes = layer_bytes + sum(4 * n * (r + c) for r, c in GEMV_LAYER)
+            gbs = nbytes / (us_layer * 1e-6) / 1e9
+            res[f"{fmt}_n{n}"] = {"us_per_layer": round(us_layer, 2), "bytes_per_layer": nbytes,
+                                  "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        for d in bufs:
+            hip_rt.free(d)
+    hip_rt.free(x)
+    hip_rt.free(y)
+    return {"what": "Qwen3-4B layer weight gemvs (q, k, v, o, gate, up, down) per weight layout; n1 = one "
+                    "vector (decode), n16 = a 16-token session batch; weights in HBM, rotated past the "
+                    "Infinity Cache; seven launches per layer", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "kernels": "gemv_vec_kernel (one vector), gemv_kernel + gemv_reduce_kernel (batches)", **res}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,7 +205,7 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "batch"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "batch", "gemv"], default=None,
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
                     help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
@@ -241,6 +301,9 @@ def main() -> int:
         hip_rt.sync()
         return e1.ms_since(e0), (time.perf_counter() - w0) * 1e3
 
+    if args.only == "gemv":
+        log(f"[bench] gemv {json.dumps(gemv_bench(nh, hip_rt, kv, stream, timed))}")
+        return 0
     if args.only == "batch":
         batch_step()
         hip_rt.sync()
@@ -316,6 +379,10 @@ def main() -> int:
     for p_ in (k_in, v_in, gam):
         hip_rt.free(p_)
 
+    log("[bench] gemv")
+    gemv_res = gemv_bench(nh, hip_rt, kv, stream, timed)
+    log(f"[bench] gemv {json.dumps(gemv_res)}")
+
     traffic = None
     tp = Path(args.traffic)
     if tp.exists():
@@ -367,6 +434,7 @@ def main() -> int:
                  "roofline": {"bound": "hbm", "achieved": prep_res["chunk"]["gbs"], "peak": HBM_PEAK_GBS,
                               "unit": "GB/s", "frac": round(prep_res["chunk"]["gbs"] / HBM_PEAK_GBS, 4),
                               "kernel": "prep_kernel (512-token chunk)"}},
+        "gemv": gemv_res,
         "cpu_baseline": cpu,
         "device": {"cu": n_cu, "clock_mhz": clock_mhz},
         "wall_ms": {"decode": round(dec_wall, 2), "prefill": round(pre_wall, 2)},

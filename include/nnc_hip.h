@@ -192,6 +192,36 @@ nnc_status nnc_hip_attend_gated_device(nnc_hip_kv* kv, int32_t buf, const float*
                                        int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
                                        int32_t n_head, int32_t n_kv, int32_t head_dim, float scale);
 
+/* The weight gemvs on either side of attention (QKV and output projections,
+ * MLP, lm_head; reference model.cpp:1189-1210 picks one by tensor type):
+ *   Y[n][r] = sum_k W[r][k] * X[n][k],  n < n_batch, r < rows, k < cols,
+ * with X n_batch vectors of cols floats x_stride floats apart and Y n_batch
+ * vectors of rows floats y_stride floats apart (n_batch == 1 is the decode
+ * gemv). All pointers are device memory; the call is queued on the cache's
+ * stream (`kv` is the execution context: its stream and scratch). Weights in
+ * nnc's three layouts:
+ *   nnc_hip_gemv_bf16  W BF16 row-major [rows][cols] (reference nn_ops.h:95-96,
+ *                      :156-159 nnc_gemv_bf16w_f32x(_batch));
+ *   nnc_hip_gemv_q8_0  split Q8_0: qs int8 [rows][cols], scales BF16
+ *                      [rows][cols/32] (nn_ops.h:119-121, :161-164);
+ *   nnc_hip_gemv_q4_s  split Q4_S: qs nibbles [rows][cols/2] (byte i of a
+ *                      block holds elements i and i+16), scales and biases BF16
+ *                      [rows][cols/32]; XSUM the per-32 block sums of each X
+ *                      vector, xsum_stride apart (nnc_block_sums_f32), or NULL
+ *                      to have them computed (nn_ops.h:138-142, :168-175).
+ * rows, cols or n_batch of 0 is a no-op, as in the reference.
+ * NNC_ERR_INVALID_ARGUMENT: NULL pointers, strides below cols / rows, W or X
+ * not 16-byte aligned or x_stride not a multiple of 4.
+ * NNC_ERR_UNSUPPORTED_MODEL: cols not a multiple of 32. */
+nnc_status nnc_hip_gemv_bf16(nnc_hip_kv* kv, const void* W, const float* X, size_t x_stride, float* Y, size_t y_stride,
+                             uint32_t rows, uint32_t cols, uint32_t n_batch);
+nnc_status nnc_hip_gemv_q8_0(nnc_hip_kv* kv, const int8_t* qs, const uint16_t* scales, const float* X,
+                             size_t x_stride, float* Y, size_t y_stride, uint32_t rows, uint32_t cols,
+                             uint32_t n_batch);
+nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases,
+                             const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
+                             size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch);
+
 /* Waits for all work queued on the cache's stream. */
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv);
 

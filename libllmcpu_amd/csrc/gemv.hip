@@ -1,0 +1,545 @@
+// The weight gemvs on either side of nnc's attention (reference
+// src/libnnc/nn_ops.h:95-180; model.cpp:1189-1210 picks one by tensor type):
+// Y[t][r] = sum_k W[r][k] X[t][k] for up to 16 activation vectors against one
+// pass over the weights, W in BF16, in the Q8_0 split layout (int8 q, one
+// BF16 scale per 32-column block) or the Q4_S split layout (nibble q, BF16
+// scale and bias per block; reference docs/design.md:141-193).
+//
+// MFMA formulation (v_mfma_f32_16x16x32_bf16): 16 weight rows x 16 tokens per
+// product, one 32-column block per k-step. A = the rows' weights of the block
+// as bf16, exact for BF16 and for the integer q of Q8_0 (|q| <= 127) and Q4_S
+// (0..15). B = X^T split into bf16 hi + lo (x ~= hi + lo to about 16 bits), so
+// the product against the exact A is near-fp32 and the accumulation fp32. A
+// quantised block's product starts from zero and is scaled into the row's sum
+// with the block's scale; Q4_S adds bias * (block sum of x) in a second sum.
+//
+// Grid: (row groups of 64, K splits). A work-group of 4 wavefronts stages its
+// K range of X^T (hi, lo, and for Q4_S the block sums) in LDS once; each
+// wavefront then streams the weights of its 16 rows block by block, four
+// blocks of loads in flight. With one K split the rows go straight to Y; with
+// several, each split writes a partial and a second kernel adds the splits in
+// split order, so results are the same run to run.
+#include "device_common.h"
+#include "kernels.h"
+
+#include <algorithm>
+
+namespace nnchip
+{
+	namespace
+	{
+		constexpr int kAhead = 8; // blocks of weights in flight per wavefront (batch kernel)
+		constexpr int kVecAhead = 8; // 16-byte loads in flight per lane (one-vector kernel)
+
+		// MFMA k-slots of a 32-column block: a lane of k-group g holds slots
+		// 8 g .. 8 g + 7. For BF16 and Q8_0 slot s is column s. Q4_S packs
+		// elements i and i + 16 into byte i, so a lane reading bytes 4 g .. 4 g + 3
+		// holds columns 4 g .. 4 g + 3 (low nibbles, slots 8 g .. 8 g + 3) and
+		// 16 + 4 g .. 16 + 4 g + 3 (high nibbles, slots 8 g + 4 .. 8 g + 7); X^T is
+		// staged in the same slot order.
+
+		// Two fp32 values whose bf16 is exact (integers below 256 in magnitude)
+		// -> one packed bf16 pair: the upper halves of their bit patterns.
+		__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi)
+		{
+			return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+		}
+
+		// Eight int8 q (two dwords) -> bf16: u = q + 128 as unsigned bytes,
+		// float(u) - 128 = q exactly.
+		__device__ __forceinline__ bf16x8 q8_to_bf16x8(uint32_t w0, uint32_t w1)
+		{
+			u32x4 r;
+			const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+			auto byte = [](uint32_t u, int i) { return static_cast<float>((u >> (8 * i)) & 0xffu) - 128.0f; };
+			r[0] = pack_hi16(byte(u0, 0), byte(u0, 1));
+			r[1] = pack_hi16(byte(u0, 2), byte(u0, 3));
+			r[2] = pack_hi16(byte(u1, 0), byte(u1, 1));
+			r[3] = pack_hi16(byte(u1, 2), byte(u1, 3));
+			return as_bf16x8(r);
+		}
+
+		// Four Q4_S bytes -> bf16 slots: low nibbles then high nibbles.
+		__device__ __forceinline__ bf16x8 q4_to_bf16x8(uint32_t w)
+		{
+			u32x4 r;
+			const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+			auto byte = [](uint32_t u, int i) { return static_cast<float>((u >> (8 * i)) & 0xffu); };
+			r[0] = pack_hi16(byte(lo, 0), byte(lo, 1));
+			r[1] = pack_hi16(byte(lo, 2), byte(lo, 3));
+			r[2] = pack_hi16(byte(hi, 0), byte(hi, 1));
+			r[3] = pack_hi16(byte(hi, 2), byte(hi, 3));
+			return as_bf16x8(r);
+		}
+
+		template <int F>
+		struct a_block
+		{
+			u32x4 v; // BF16: 8 weights; Q8_0: 8 int8 in v[0..1]; Q4_S: 4 bytes in v[0]
+		};
+
+		template <int F>
+		__device__ __forceinline__ a_block<F> load_a(const gemv_params& p, int row, int blk, int grp)
+		{
+			a_block<F> a;
+			const size_t base = static_cast<size_t>(row) * p.cols + 32 * blk;
+			if constexpr (F == kGemvBf16)
+				a.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.w) + base + 8 * grp);
+			else if constexpr (F == kGemvQ8_0)
+			{
+				const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(p.w) + base + 8 * grp);
+				a.v = u32x4{w.x, w.y, 0u, 0u};
+			}
+			else
+				a.v = u32x4{*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.w) + base / 2 + 4 * grp), 0u,
+				            0u, 0u};
+			return a;
+		}
+
+		template <int F>
+		__device__ __forceinline__ bf16x8 a_operand(const a_block<F>& a)
+		{
+			if constexpr (F == kGemvBf16)
+				return as_bf16x8(a.v);
+			else if constexpr (F == kGemvQ8_0)
+				return q8_to_bf16x8(a.v[0], a.v[1]);
+			else
+				return q4_to_bf16x8(a.v[0]);
+		}
+
+		template <int F>
+		__global__ __launch_bounds__(256) void gemv_kernel(const gemv_params p)
+		{
+			// Dynamic LDS: X^T hi and lo [block][token][32 slots] (bf16), the 16
+			// rows' scales (and biases) [block][16], and the wavefronts' sums.
+			extern __shared__ __attribute__((aligned(16))) unsigned char s_raw[];
+			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+			const int col = lane & 15, grp = lane >> 4;
+			const int nt = p.n_batch;
+			const int split = blockIdx.y;
+			const int b0 = split * p.split_blocks;
+			const int nblk = min(p.split_blocks, p.cols / 32 - b0); // >= 1
+			uint16_t* s_xh = reinterpret_cast<uint16_t*>(s_raw);
+			uint16_t* s_xl = s_xh + static_cast<size_t>(p.split_blocks) * nt * 32;
+			uint16_t* s_sc = s_xl + static_cast<size_t>(p.split_blocks) * nt * 32;
+			uint16_t* s_bi = s_sc + p.split_blocks * 16;
+			float* s_xs = reinterpret_cast<float*>(s_bi + p.split_blocks * 16); // Q4_S: [block][token] sums of x
+			float* s_red = s_xs + p.split_blocks * nt; // [wavefront][16 rows][16 tokens]
+
+			// The work-group's 16 rows; wavefront w takes blocks w, w + 4, ... of
+			// the range, kAhead of them in flight, the first ones while X^T is
+			// staged.
+			const int row0 = blockIdx.x * 16;
+			const int ra = min(row0 + col, p.rows - 1); // this lane's A row (clamped; not stored)
+			const int n_mine = nblk > wave ? (nblk - wave + 3) / 4 : 0; // blocks of this wavefront
+			auto my_block = [&](int i) { return b0 + wave + 4 * min(i, max(n_mine - 1, 0)); };
+			a_block<F> ab[kAhead];
+#pragma unroll
+			for (int j = 0; j < kAhead; ++j) ab[j] = load_a<F>(p, ra, min(my_block(j), p.cols / 32 - 1), grp);
+
+			// X^T of the range, four columns per piece (consecutive threads read
+			// consecutive 16 bytes of a token's row), loads issued eight at a time.
+			const int n_pieces = nblk * nt * 8;
+			for (int i0 = 0; i0 < n_pieces; i0 += 256 * 8)
+			{
+				float4 xv[8];
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
+				{
+					const int i = i0 + threadIdx.x + 256 * u;
+					const int q = i & 7, b = (i >> 3) % nblk, t = (i >> 3) / nblk;
+					xv[u] = i < n_pieces ? *reinterpret_cast<const float4*>(p.x + t * p.x_stride + 32 * (b0 + b) + 4 * q)
+					                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				}
+#pragma unroll
+				for (int u = 0; u < 8; ++u)
+				{
+					const int i = i0 + threadIdx.x + 256 * u;
+					if (i >= n_pieces) continue;
+					const int q = i & 7, b = (i >> 3) % nblk, t = (i >> 3) / nblk;
+					// The piece's first k-slot; its four columns take four consecutive slots.
+					const int slot0 = F == kGemvQ4S ? (q < 4 ? 8 * q : 8 * (q - 4) + 4) : 4 * q;
+					const uint32_t h0 = cvt_pk_bf16(xv[u].x, xv[u].y), h1 = cvt_pk_bf16(xv[u].z, xv[u].w);
+					const uint32_t l0 = cvt_pk_bf16(xv[u].x - bf16_lo(h0), xv[u].y - bf16_hi(h0));
+					const uint32_t l1 = cvt_pk_bf16(xv[u].z - bf16_lo(h1), xv[u].w - bf16_hi(h1));
+					const size_t at = (static_cast<size_t>(b) * nt + t) * 32 + slot0;
+					*reinterpret_cast<u32x2*>(s_xh + at) = u32x2{h0, h1};
+					*reinterpret_cast<u32x2*>(s_xl + at) = u32x2{l0, l1};
+				}
+			}
+			const int nb_all = p.cols / 32;
+			if constexpr (F == kGemvQ4S)
+			{
+				// Block sums of x: the caller's, or as the reference evaluates them
+				// (reference nn_ops.cpp:1305-1316 under its -ffast-math build:
+				// lane j = (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]), then the
+				// lanes pairwise).
+				for (int i = threadIdx.x; i < nblk * nt; i += 256)
+				{
+					const int b = i % nblk, t = i / nblk;
+					float sum;
+					if (p.xsum)
+						sum = p.xsum[t * p.xsum_stride + b0 + b];
+					else
+					{
+						const float4* x4 = reinterpret_cast<const float4*>(p.x + t * p.x_stride + 32 * (b0 + b));
+						float x[32];
+#pragma unroll
+						for (int u = 0; u < 8; ++u)
+						{
+							const float4 v = x4[u];
+							x[4 * u] = v.x;
+							x[4 * u + 1] = v.y;
+							x[4 * u + 2] = v.z;
+							x[4 * u + 3] = v.w;
+						}
+						float l[8];
+#pragma unroll
+						for (int j = 0; j < 8; ++j) l[j] = (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]);
+						sum = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
+					}
+					s_xs[b * nt + t] = sum;
+				}
+			}
+			if constexpr (F != kGemvBf16)
+			{
+				// The rows' scales (and biases) of the range, [block][row], so a
+				// lane reads its four rows with one 8-byte read.
+				for (int i = threadIdx.x; i < nblk * 16; i += 256)
+				{
+					const int r = i / nblk, b = i % nblk;
+					const size_t src = static_cast<size_t>(min(row0 + r, p.rows - 1)) * nb_all + b0 + b;
+					s_sc[b * 16 + r] = p.scales[src];
+					if constexpr (F == kGemvQ4S) s_bi[b * 16 + r] = p.biases[src];
+				}
+			}
+			__syncthreads();
+
+			f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc_b = {0.0f, 0.0f, 0.0f, 0.0f};
+			const bf16x8 zero8 = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+			for (int i0 = 0; i0 < n_mine; i0 += kAhead)
+			{
+#pragma unroll
+				for (int j = 0; j < kAhead; ++j)
+				{
+					const int i = i0 + j;
+					const int bl = my_block(i) - b0; // block within the range
+					const bf16x8 a = a_operand<F>(ab[j]);
+					// The next load into this slot, kAhead blocks on (clamped: a
+					// load is never under a branch).
+					ab[j] = load_a<F>(p, ra, min(my_block(i + kAhead), nb_all - 1), grp);
+					if (i < n_mine) // uniform
+					{
+						const size_t at = (static_cast<size_t>(bl) * nt + col) * 32 + 8 * grp;
+						const bf16x8 xh = col < nt ? *reinterpret_cast<const bf16x8*>(s_xh + at) : zero8;
+						const bf16x8 xl = col < nt ? *reinterpret_cast<const bf16x8*>(s_xl + at) : zero8;
+						if constexpr (F == kGemvBf16)
+						{
+							acc = mfma16x16x32(a, xh, acc);
+							acc = mfma16x16x32(a, xl, acc);
+						}
+						else
+						{
+							f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+							d = mfma16x16x32(a, xh, d);
+							d = mfma16x16x32(a, xl, d);
+							const u32x2 sc = *reinterpret_cast<const u32x2*>(s_sc + bl * 16 + 4 * grp);
+							acc[0] = fmaf(bf16_lo(sc.x), d[0], acc[0]);
+							acc[1] = fmaf(bf16_hi(sc.x), d[1], acc[1]);
+							acc[2] = fmaf(bf16_lo(sc.y), d[2], acc[2]);
+							acc[3] = fmaf(bf16_hi(sc.y), d[3], acc[3]);
+							if constexpr (F == kGemvQ4S)
+							{
+								// The bias term: bias * (block sum of x).
+								const u32x2 bi = *reinterpret_cast<const u32x2*>(s_bi + bl * 16 + 4 * grp);
+								const float xs = col < nt ? s_xs[bl * nt + col] : 0.0f;
+								acc_b[0] = fmaf(bf16_lo(bi.x), xs, acc_b[0]);
+								acc_b[1] = fmaf(bf16_hi(bi.x), xs, acc_b[1]);
+								acc_b[2] = fmaf(bf16_lo(bi.y), xs, acc_b[2]);
+								acc_b[3] = fmaf(bf16_hi(bi.y), xs, acc_b[3]);
+							}
+						}
+					}
+				}
+			}
+
+			// The wavefronts' sums, added in wavefront order: lane (grp, col)
+			// holds rows 4 grp + i of token col.
+#pragma unroll
+			for (int i = 0; i < 4; ++i)
+				s_red[(wave * 16 + 4 * grp + i) * 16 + col] = F == kGemvQ4S ? acc[i] + acc_b[i] : acc[i];
+			__syncthreads();
+			{
+				const int r = threadIdx.x >> 4, t = threadIdx.x & 15;
+				float v = s_red[r * 16 + t];
+#pragma unroll
+				for (int w = 1; w < 4; ++w) v += s_red[(w * 16 + r) * 16 + t];
+				if (row0 + r < p.rows && t < nt)
+				{
+					if (p.n_split == 1)
+						p.y[t * p.y_stride + row0 + r] = v;
+					else
+						p.part[(static_cast<size_t>(split) * nt + t) * p.rows + row0 + r] = v;
+				}
+			}
+		}
+
+		// One activation vector (the decode gemv) on the VALU: every load is 16
+		// contiguous bytes of a weight row (a wavefront reads 1 KB of one row
+		// per instruction), x sits in LDS, and each wavefront streams pairs of
+		// rows with kVecAhead loads in flight across row boundaries; a row's
+		// lane sums meet through DPP and lane swaps.
+		template <int F>
+		struct vec_shape
+		{
+			static constexpr int CPL = F == kGemvBf16 ? 8 : (F == kGemvQ8_0 ? 16 : 32); // columns per lane per load
+			static constexpr int CW = 64 * CPL; // columns per wavefront load
+		};
+
+		template <int F>
+		struct vec_item
+		{
+			u32x4 w; // 16 bytes of the row
+			float sc, bi; // the block's scale (Q8_0, Q4_S) and bias (Q4_S)
+		};
+
+		template <int F>
+		__global__ __launch_bounds__(256) void gemv_vec_kernel(const gemv_params p)
+		{
+			using V = vec_shape<F>;
+			constexpr int CPL = V::CPL, CW = V::CW, NA = kVecAhead;
+			extern __shared__ __attribute__((aligned(16))) float s_x[]; // x, then (Q4_S) its block sums
+			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+			const int nb_all = p.cols / 32;
+
+			// Items: for each of this wavefront's row pairs, chunk c of row 0,
+			// then of row 1, for every chunk c of CW columns.
+			const int nch = (p.cols + CW - 1) / CW;
+			const int per_pair = 2 * nch;
+			const int gw = blockIdx.x * 4 + wave, n_gw = gridDim.x * 4;
+			const int n_pairs = (p.rows + 1) / 2;
+			const int my_pairs = gw < n_pairs ? (n_pairs - 1 - gw) / n_gw + 1 : 0;
+			const int n_items = my_pairs * per_pair;
+			// (A wavefront without rows still takes part in staging x.)
+			// Row of item k (clamped to the matrix) and the lane's first column.
+			auto item_pos = [&](int k, int& row, int& c0) __attribute__((always_inline))
+			{
+				k = max(0, min(k, n_items - 1));
+				const int pi = k / per_pair, rem = k % per_pair;
+				row = min(2 * (gw + pi * n_gw) + (rem & 1), p.rows - 1);
+				c0 = (rem >> 1) * CW + lane * CPL;
+			};
+			auto pair_row = [&](int k) { return 2 * (gw + (k / per_pair) * n_gw); };
+			auto load = [&](int k) __attribute__((always_inline)) -> vec_item<F>
+			{
+				int row, c0;
+				item_pos(k, row, c0);
+				const int cc = min(c0, p.cols - CPL); // lanes past the row's end re-read its last bytes (not used)
+				vec_item<F> it;
+				const size_t off = static_cast<size_t>(row) * p.cols + cc;
+				if constexpr (F == kGemvBf16)
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.w) + off);
+				else if constexpr (F == kGemvQ8_0)
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(p.w) + off);
+				else
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.w) + off / 2);
+				if constexpr (F != kGemvBf16)
+				{
+					const size_t si = static_cast<size_t>(row) * nb_all + cc / 32;
+					it.sc = bf16_bits_to_f32(p.scales[si]);
+					if constexpr (F == kGemvQ4S) it.bi = bf16_bits_to_f32(p.biases[si]);
+				}
+				return it;
+			};
+			// The lane's dot product of one item with x.
+			auto dot = [&](const vec_item<F>& it, int c0) __attribute__((always_inline)) -> float
+			{
+				if (c0 >= p.cols) return 0.0f;
+				if constexpr (F == kGemvBf16)
+				{
+					const float4 x0 = *reinterpret_cast<const float4*>(s_x + c0);
+					const float4 x1 = *reinterpret_cast<const float4*>(s_x + c0 + 4);
+					float d = 0.0f;
+					d = fmaf(bf16_lo(it.w[0]), x0.x, d);
+					d = fmaf(bf16_hi(it.w[0]), x0.y, d);
+					d = fmaf(bf16_lo(it.w[1]), x0.z, d);
+					d = fmaf(bf16_hi(it.w[1]), x0.w, d);
+					d = fmaf(bf16_lo(it.w[2]), x1.x, d);
+					d = fmaf(bf16_hi(it.w[2]), x1.y, d);
+					d = fmaf(bf16_lo(it.w[3]), x1.z, d);
+					d = fmaf(bf16_hi(it.w[3]), x1.w, d);
+					return d;
+				}
+				else if constexpr (F == kGemvQ8_0)
+				{
+					float d = 0.0f;
+#pragma unroll
+					for (int u = 0; u < 4; ++u)
+					{
+						const float4 x = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
+						const uint32_t b = it.w[u] ^ 0x80808080u; // q + 128 per byte
+						d = fmaf(static_cast<float>(b & 0xffu) - 128.0f, x.x, d);
+						d = fmaf(static_cast<float>((b >> 8) & 0xffu) - 128.0f, x.y, d);
+						d = fmaf(static_cast<float>((b >> 16) & 0xffu) - 128.0f, x.z, d);
+						d = fmaf(static_cast<float>(b >> 24) - 128.0f, x.w, d);
+					}
+					return it.sc * d;
+				}
+				else
+				{
+					// Byte i of the block: element i (low nibble), i + 16 (high).
+					float d = 0.0f;
+#pragma unroll
+					for (int u = 0; u < 4; ++u)
+					{
+						const float4 xl = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
+						const float4 xh = *reinterpret_cast<const float4*>(s_x + c0 + 16 + 4 * u);
+						const uint32_t b = it.w[u];
+						d = fmaf(static_cast<float>(b & 0xfu), xl.x, d);
+						d = fmaf(static_cast<float>((b >> 8) & 0xfu), xl.y, d);
+						d = fmaf(static_cast<float>((b >> 16) & 0xfu), xl.z, d);
+						d = fmaf(static_cast<float>((b >> 24) & 0xfu), xl.w, d);
+						d = fmaf(static_cast<float>((b >> 4) & 0xfu), xh.x, d);
+						d = fmaf(static_cast<float>((b >> 12) & 0xfu), xh.y, d);
+						d = fmaf(static_cast<float>((b >> 20) & 0xfu), xh.z, d);
+						d = fmaf(static_cast<float>(b >> 28), xh.w, d);
+					}
+					return fmaf(it.bi, s_x[p.cols + c0 / 32], it.sc * d);
+				}
+			};
+
+			// The first loads go out before x is staged.
+			vec_item<F> ring[NA];
+#pragma unroll
+			for (int j = 0; j < NA; ++j) ring[j] = load(j);
+
+			for (int i = 4 * threadIdx.x; i < p.cols; i += 1024)
+				*reinterpret_cast<float4*>(s_x + i) = *reinterpret_cast<const float4*>(p.x + i);
+			if constexpr (F == kGemvQ4S)
+			{
+				// Block sums: the caller's, or in the reference's order (reference
+				// nn_ops.cpp:1305-1316 under its -ffast-math build).
+				for (int b = threadIdx.x; b < nb_all; b += 256)
+				{
+					float sum;
+					if (p.xsum)
+						sum = p.xsum[b];
+					else
+					{
+						const float* x = p.x + 32 * b;
+						float l[8];
+#pragma unroll
+						for (int j = 0; j < 8; ++j) l[j] = (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]);
+						sum = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
+					}
+					s_x[p.cols + b] = sum;
+				}
+			}
+			__syncthreads();
+
+			float acc[2] = {0.0f, 0.0f};
+			for (int k0 = 0; k0 < n_items; k0 += NA)
+			{
+#pragma unroll
+				for (int j = 0; j < NA; ++j)
+				{
+					const int k = k0 + j;
+					int row, c0;
+					item_pos(k, row, c0);
+					(void)row;
+					const vec_item<F> it = ring[j];
+					ring[j] = load(k + NA); // clamped past the end: never under a branch
+					if (k < n_items) // uniform
+					{
+						acc[j & 1] += dot(it, c0);
+						if (k % per_pair == per_pair - 1) // the pair's last item: both rows are complete
+						{
+							const float y0 = wave_sum_dpp(acc[0]), y1 = wave_sum_dpp(acc[1]);
+							const int r0 = pair_row(k);
+							if (lane == 0)
+							{
+								p.y[r0] = y0;
+								if (r0 + 1 < p.rows) p.y[r0 + 1] = y1;
+							}
+							acc[0] = acc[1] = 0.0f;
+						}
+					}
+				}
+			}
+		}
+
+		// Y[t][r] = the splits' partials summed in split order.
+		__global__ void gemv_reduce_kernel(const gemv_params p)
+		{
+			const size_t n = static_cast<size_t>(p.n_batch) * p.rows;
+			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
+			{
+				// Eight splits' loads in flight at a time, added in split order.
+				float s = 0.0f;
+				for (int k0 = 0; k0 < p.n_split; k0 += 8)
+				{
+					float v[8];
+#pragma unroll
+					for (int u = 0; u < 8; ++u)
+						v[u] = k0 + u < p.n_split ? p.part[static_cast<size_t>(k0 + u) * n + i] : 0.0f;
+#pragma unroll
+					for (int u = 0; u < 8; ++u)
+						if (k0 + u < p.n_split) s = k0 + u == 0 ? v[u] : s + v[u];
+				}
+				const int t = static_cast<int>(i / p.rows), r = static_cast<int>(i % p.rows);
+				p.y[t * p.y_stride + r] = s;
+			}
+		}
+	}
+
+	void gemv_plan(int rows, int cols, int n_batch, int& n_split, int& split_blocks)
+	{
+		(void)rows;
+		const int nb = cols / 32;
+		// As few K splits as the LDS copy of X^T allows (one for a single
+		// vector at every nnc shape), the splits equal in size.
+		int max_blocks = 1;
+		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= kGemvLdsBudget) ++max_blocks;
+		n_split = (nb + max_blocks - 1) / max_blocks;
+		split_blocks = (nb + n_split - 1) / n_split;
+	}
+
+	bool gemv_vec_fits(int cols, int n_batch)
+	{
+		return n_batch == 1 && static_cast<size_t>(cols + cols / 32) * 4 <= kGemvLdsBudget;
+	}
+
+	bool launch_gemv(const gemv_params& p, hipStream_t stream)
+	{
+		if (gemv_vec_fits(p.cols, p.n_batch))
+		{
+			const size_t lds = static_cast<size_t>(p.cols + p.cols / 32) * 4;
+			const int n_pairs = (p.rows + 1) / 2;
+			const dim3 grid(std::max(1, std::min((n_pairs + 3) / 4, 512)));
+			switch (p.format)
+			{
+			case kGemvBf16: gemv_vec_kernel<kGemvBf16><<<grid, 256, lds, stream>>>(p); return true;
+			case kGemvQ8_0: gemv_vec_kernel<kGemvQ8_0><<<grid, 256, lds, stream>>>(p); return true;
+			case kGemvQ4S: gemv_vec_kernel<kGemvQ4S><<<grid, 256, lds, stream>>>(p); return true;
+			default: return false;
+			}
+		}
+		const dim3 grid((p.rows + 15) / 16, p.n_split);
+		const size_t lds = gemv_lds_bytes(p.split_blocks, p.n_batch);
+		switch (p.format)
+		{
+		case kGemvBf16: gemv_kernel<kGemvBf16><<<grid, 256, lds, stream>>>(p); break;
+		case kGemvQ8_0: gemv_kernel<kGemvQ8_0><<<grid, 256, lds, stream>>>(p); break;
+		case kGemvQ4S: gemv_kernel<kGemvQ4S><<<grid, 256, lds, stream>>>(p); break;
+		default: return false;
+		}
+		if (p.n_split > 1)
+		{
+			const size_t n = static_cast<size_t>(p.n_batch) * p.rows;
+			const unsigned g = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 4096));
+			gemv_reduce_kernel<<<g, 256, 0, stream>>>(p);
+		}
+		return true;
+	}
+}

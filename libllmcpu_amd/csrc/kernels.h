@@ -89,6 +89,40 @@ namespace nnchip
 
 	bool launch_fill_normal(void* dst, uint64_t n, uint64_t seed, int norm_dim, bool bf16, hipStream_t stream);
 
+	// The weight gemvs (reference nn_ops.h:95-180): Y[t] = W . X[t] for
+	// t < n_batch <= 16, W in one of nnc's three weight layouts.
+	constexpr int kGemvBf16 = 0, kGemvQ8_0 = 1, kGemvQ4S = 2;
+	constexpr int kGemvMaxBatch = 16;
+	constexpr size_t kGemvLdsBudget = 64 << 10; // dynamic LDS per gemv work-group
+
+	// LDS of a gemv work-group over `blocks` 32-column blocks and n_batch
+	// tokens: X^T hi and lo (bf16), 16 rows' scales and biases, the Q4_S block
+	// sums, and the four wavefronts' 16 x 16 sums.
+	__host__ __device__ inline size_t gemv_lds_bytes(int blocks, int n_batch)
+	{
+		return static_cast<size_t>(blocks) * (128 * n_batch + 64 + 4 * n_batch) + 4 * 256 * 4;
+	}
+
+	struct gemv_params
+	{
+		int format; // kGemvBf16, kGemvQ8_0 or kGemvQ4S
+		const void* w; // BF16 [rows][cols], Q8_0 int8 [rows][cols], Q4_S nibbles [rows][cols / 2]
+		const uint16_t* scales; // [rows][cols / 32] BF16 (Q8_0, Q4_S)
+		const uint16_t* biases; // [rows][cols / 32] BF16 (Q4_S)
+		const float* x; // [n_batch] vectors of cols floats, x_stride apart
+		const float* xsum; // Q4_S: [n_batch] runs of cols / 32 block sums, xsum_stride apart; or null
+		float* y; // [n_batch] vectors of rows floats, y_stride apart
+		float* part; // [n_split][n_batch][rows] partial sums when n_split > 1
+		size_t x_stride, xsum_stride, y_stride;
+		int rows, cols, n_batch;
+		int n_split, split_blocks; // K splits, and 32-column blocks per split
+	};
+
+	// K splits for a (rows, cols) gemv of n_batch vectors.
+	void gemv_plan(int rows, int cols, int n_batch, int& n_split, int& split_blocks);
+
+	bool launch_gemv(const gemv_params& p, hipStream_t stream);
+
 	bool launch_zero(float* dst, size_t n, hipStream_t stream);
 
 	// The span of keys position `pos` attends to (reference model.cpp:2300-2316).

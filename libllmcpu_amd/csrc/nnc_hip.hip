@@ -93,6 +93,7 @@ struct nnc_hip_kv
 	dev_scratch q; // staging of host q / out / append rows
 	dev_scratch out;
 	dev_scratch gate;
+	dev_scratch gemv_part; // weight gemv partial sums over K splits
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 };
@@ -108,7 +109,7 @@ namespace
 			if (b.k) (void)hipFree(b.k);
 			if (b.v) (void)hipFree(b.v);
 		}
-		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->rows_k, &kv->rows_v})
+		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
 		delete kv;
@@ -603,6 +604,83 @@ nnc_status nnc_hip_attend_gated_device(nnc_hip_kv* kv, int32_t buf, const float*
 	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
 		return s;
 	return attend_impl(kv, buf, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+}
+
+namespace
+{
+	// One weight gemv on the context's stream, in chunks of at most
+	// kGemvMaxBatch vectors.
+	nnc_status gemv_impl(nnc_hip_kv* kv, int format, const void* w, const uint16_t* scales, const uint16_t* biases,
+	                     const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
+	                     size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
+	{
+		if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the context (cache) is NULL");
+		if (!w || !X || !Y || (format != nnchip::kGemvBf16 && !scales) || (format == nnchip::kGemvQ4S && !biases))
+			return fail(NNC_ERR_INVALID_ARGUMENT, "NULL weight, scale, bias, input or output pointer");
+		if (rows == 0 || cols == 0 || n_batch == 0) return NNC_OK; // nothing to do, as in the reference
+		if (rows > 0x7fffffffu || cols > 0x7fffffffu)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %u x %u", rows, cols);
+		if (cols % 32 != 0)
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "gemv with %u columns (a multiple of 32 is required)", cols);
+		if (x_stride < cols || y_stride < rows || (format == nnchip::kGemvQ4S && XSUM && xsum_stride < cols / 32))
+			return fail(NNC_ERR_INVALID_ARGUMENT, "strides %zu / %zu / %zu for a %u x %u gemv", x_stride, y_stride,
+			            xsum_stride, rows, cols);
+		if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(X)) & 15 || x_stride % 4 != 0)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "weights and X must be 16-byte aligned, x_stride a multiple of 4");
+		for (uint32_t t0 = 0; t0 < n_batch; t0 += nnchip::kGemvMaxBatch)
+		{
+			const int nb = static_cast<int>(std::min<uint32_t>(n_batch - t0, nnchip::kGemvMaxBatch));
+			int n_split = 1, split_blocks = 1;
+			nnchip::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), nb, n_split, split_blocks);
+			if (n_split > 1)
+				if (nnc_status s = reserve(kv, kv->gemv_part, static_cast<size_t>(n_split) * nb * rows * sizeof(float),
+				                           "gemv scratch"))
+					return s;
+			nnchip::gemv_params p{};
+			p.format = format;
+			p.w = w;
+			p.scales = scales;
+			p.biases = biases;
+			p.x = X + t0 * x_stride;
+			p.xsum = XSUM ? XSUM + t0 * xsum_stride : nullptr;
+			p.y = Y + t0 * y_stride;
+			p.part = static_cast<float*>(kv->gemv_part.ptr);
+			p.x_stride = x_stride;
+			p.xsum_stride = xsum_stride;
+			p.y_stride = y_stride;
+			p.rows = static_cast<int>(rows);
+			p.cols = static_cast<int>(cols);
+			p.n_batch = nb;
+			p.n_split = n_split;
+			p.split_blocks = split_blocks;
+			if (!nnchip::launch_gemv(p, kv->stream)) return fail(NNC_ERR_UNSUPPORTED_MODEL, "gemv format %d", format);
+			NNC_HIP_TRY(hipGetLastError(), "gemv launch");
+		}
+		return NNC_OK;
+	}
+}
+
+nnc_status nnc_hip_gemv_bf16(nnc_hip_kv* kv, const void* W, const float* X, size_t x_stride, float* Y, size_t y_stride,
+                             uint32_t rows, uint32_t cols, uint32_t n_batch)
+{
+	return gemv_impl(kv, nnchip::kGemvBf16, W, nullptr, nullptr, X, x_stride, nullptr, 0, Y, y_stride, rows, cols,
+	                 n_batch);
+}
+
+nnc_status nnc_hip_gemv_q8_0(nnc_hip_kv* kv, const int8_t* qs, const uint16_t* scales, const float* X,
+                             size_t x_stride, float* Y, size_t y_stride, uint32_t rows, uint32_t cols,
+                             uint32_t n_batch)
+{
+	return gemv_impl(kv, nnchip::kGemvQ8_0, qs, scales, nullptr, X, x_stride, nullptr, 0, Y, y_stride, rows, cols,
+	                 n_batch);
+}
+
+nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases,
+                             const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
+                             size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
+{
+	return gemv_impl(kv, nnchip::kGemvQ4S, qs, scales, biases, X, x_stride, XSUM, xsum_stride, Y, y_stride, rows, cols,
+	                 n_batch);
 }
 
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv)

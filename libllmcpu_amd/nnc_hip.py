@@ -83,6 +83,10 @@ SIGNATURES = {
     "nnc_hip_attend_device": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_gated": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_gated_device": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
+    "nnc_hip_gemv_bf16": (C.c_int, [_P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "nnc_hip_gemv_q8_0": (C.c_int, [_P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "nnc_hip_gemv_q4_s": (C.c_int, [_P, _P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32,
+                                    C.c_uint32, C.c_uint32]),
     "nnc_hip_kv_sync": (C.c_int, [_P]),
     "nnc_hip_kv_stream": (_P, [_P]),
     "nnc_hip_fill_normal": (C.c_int, [_P, _U64, _U64, _I, _B, _P]),
@@ -299,6 +303,53 @@ class KVCache:
             self.prep_append_device(buf, ptrs[0], ptrs[1], ptrs[2], pos0=pos0, n_tok=n_tok, prep=prep)
             self.sync()
             return hip_rt.to_host(np.empty_like(q), ptrs[0])
+        finally:
+            for d in dev:
+                hip_rt.free(d)
+
+    # -- the weight gemvs, with this cache as the execution context ------------------
+    def gemv_device(self, fmt: str, w: tuple, x_dev: int, y_dev: int, *, rows: int, cols: int, n_batch: int,
+                    x_stride: int | None = None, y_stride: int | None = None, xsum_dev: int = 0,
+                    xsum_stride: int = 0) -> None:
+        """Y = W . X on device memory: fmt "bf16" (w = (W,)), "q8_0" (w = (qs, scales))
+        or "q4_s" (w = (qs, scales, biases)), each a device address; queued on the
+        cache's stream."""
+        xs = cols if x_stride is None else x_stride
+        ys = rows if y_stride is None else y_stride
+        if fmt == "bf16":
+            st = self._lib.nnc_hip_gemv_bf16(self.handle, w[0], x_dev, xs, y_dev, ys, rows, cols, n_batch)
+        elif fmt == "q8_0":
+            st = self._lib.nnc_hip_gemv_q8_0(self.handle, w[0], w[1], x_dev, xs, y_dev, ys, rows, cols, n_batch)
+        elif fmt == "q4_s":
+            st = self._lib.nnc_hip_gemv_q4_s(self.handle, w[0], w[1], w[2], x_dev, xs, xsum_dev or None,
+                                             xsum_stride, y_dev, ys, rows, cols, n_batch)
+        else:
+            raise ValueError(f"unknown weight format {fmt!r}")
+        _check(st)
+
+    def gemv(self, fmt: str, w: tuple, x: np.ndarray, *, rows: int, cols: int,
+             xsum: np.ndarray | None = None) -> np.ndarray:
+        """gemv_device from host arrays (uploaded to scratch device memory,
+        freed afterwards); returns Y [n_batch, rows]."""
+        from . import hip_rt
+
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+        n = x.shape[0]
+        arrays = [np.ascontiguousarray(a) for a in w] + [x] + ([] if xsum is None else
+                                                               [np.ascontiguousarray(xsum, dtype=np.float32)])
+        dev = []
+        try:
+            for a in arrays:
+                d = hip_rt.malloc(max(a.nbytes, 16))
+                dev.append(d)
+                hip_rt.to_device(d, a)
+            y_dev = hip_rt.malloc(n * rows * 4)
+            dev.append(y_dev)
+            nw = len(w)
+            self.gemv_device(fmt, tuple(dev[:nw]), dev[nw], y_dev, rows=rows, cols=cols, n_batch=n,
+                             xsum_dev=dev[nw + 1] if xsum is not None else 0, xsum_stride=cols // 32)
+            self.sync()
+            return hip_rt.to_host(np.empty((n, rows), np.float32), y_dev)
         finally:
             for d in dev:
                 hip_rt.free(d)

@@ -69,6 +69,13 @@ class _Lib:
         f("rmsnorm_gamma", None, [_P, _SZ, _SZ, _P, _F])
         f("rmsnorm_plain", None, [_P, _SZ, _SZ, _F])
         f("mul_sigmoid", None, [_P, _P, _SZ])
+        f("quantize_q8_0", None, [_P, _P, _P, _SZ])
+        f("quantize_q4_s", None, [_P, _P, _P, _P, _SZ])
+        f("block_sums", None, [_P, _P, _SZ])
+        _U32 = C.c_uint32
+        f("gemv_bf16", None, [_P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
+        f("gemv_q8_0", None, [_P, _P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
+        f("gemv_q4_s", None, [_P, _P, _P, _P, _SZ, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
 
     def _fn(self, name, res, args):
         fn = getattr(self.lib, self.prefix + name)
@@ -139,6 +146,60 @@ class _Lib:
         x = np.ascontiguousarray(x, dtype=np.float32).copy()
         self._rmsnorm_plain(_p(x), x.size // dim, dim, eps)
         return x
+
+    # -- the weight gemvs on either side of attention ----------------------------------
+    def quantize_q8_0(self, w):
+        """fp32 weights [rows, cols] -> (qs int8 [rows, cols], scales bf16 bits [rows, cols/32])."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        qs = np.empty(w.shape, np.int8)
+        sc = np.empty(w.shape[:-1] + (w.shape[-1] // 32,), np.uint16)
+        self._quantize_q8_0(_p(w), _p(qs), _p(sc), w.size)
+        return qs, sc
+
+    def quantize_q4_s(self, w):
+        """fp32 weights [rows, cols] -> (qs uint8 [rows, cols/2], scales, biases bf16 bits [rows, cols/32])."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        qs = np.empty(w.shape[:-1] + (w.shape[-1] // 2,), np.uint8)
+        sc = np.empty(w.shape[:-1] + (w.shape[-1] // 32,), np.uint16)
+        bi = np.empty_like(sc)
+        self._quantize_q4_s(_p(w), _p(qs), _p(sc), _p(bi), w.size)
+        return qs, sc, bi
+
+    def block_sums(self, x):
+        """Per-32 block sums of each row of x [n, cols]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape[:-1] + (x.shape[-1] // 32,), np.float32)
+        for i in range(x.size // x.shape[-1]):
+            self._block_sums(_p(x.reshape(-1, x.shape[-1])[i]), _p(out.reshape(-1, out.shape[-1])[i]), x.shape[-1])
+        return out
+
+    def gemv_bf16(self, W, X):
+        """Y [n, rows] = X [n, cols] . W^T for BF16 bits W [rows, cols]."""
+        W = np.ascontiguousarray(W, dtype=np.uint16)
+        X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, W.shape[1])
+        Y = np.zeros((X.shape[0], W.shape[0]), np.float32)
+        self._gemv_bf16(_p(W), _p(X), W.shape[1], _p(Y), W.shape[0], W.shape[0], W.shape[1], X.shape[0])
+        return Y
+
+    def gemv_q8_0(self, qs, scales, X):
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint16)
+        X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, qs.shape[1])
+        Y = np.zeros((X.shape[0], qs.shape[0]), np.float32)
+        self._gemv_q8_0(_p(qs), _p(scales), _p(X), qs.shape[1], _p(Y), qs.shape[0], qs.shape[0], qs.shape[1],
+                        X.shape[0])
+        return Y
+
+    def gemv_q4_s(self, qs, scales, biases, X, xsum=None):
+        qs = np.ascontiguousarray(qs, dtype=np.uint8)
+        cols = qs.shape[1] * 2
+        X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, cols)
+        xsum = self.block_sums(X) if xsum is None else np.ascontiguousarray(xsum, dtype=np.float32)
+        Y = np.zeros((X.shape[0], qs.shape[0]), np.float32)
+        self._gemv_q4_s(_p(qs), _p(np.ascontiguousarray(scales, dtype=np.uint16)),
+                        _p(np.ascontiguousarray(biases, dtype=np.uint16)), _p(X), cols, _p(xsum), cols // 32, _p(Y),
+                        qs.shape[0], qs.shape[0], cols, X.shape[0])
+        return Y
 
     def mul_sigmoid(self, y, g):
         """y * sigmoid(g), elementwise (Qwen3.5's output gate)."""

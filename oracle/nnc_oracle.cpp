@@ -19,6 +19,12 @@
 //                                          Q/K/V norms, RoPE on Q and K, K/V append)
 //   orc_mul_sigmoid                        reference src/libnnc/nn_ops.cpp:1731-1742 (Qwen3.5's
 //                                          output gate, model.cpp:1759-1760)
+//   orc_quantize_q8_0 / orc_quantize_q4_s  reference src/libnnc/nn_ops.cpp:1223-1290 (split
+//                                          layouts, docs/design.md:141-193)
+//   orc_block_sums                         reference src/libnnc/nn_ops.cpp:1305-1316
+//   orc_gemv_bf16 / orc_gemv_q8_0 /        reference src/libnnc/nn_ops.cpp:1000-1053, 1352-1452,
+//   orc_gemv_q4_s                          1610-1700 (the weight gemvs, single and batched;
+//                                          model.cpp:1189-1210 picks one by tensor type)
 // and two checkers that are not restatements:
 //   orc_textbook_attend   double-precision softmax attention per query, the
 //                         scalar reference of reference src/appnnc/tests.cpp:2424-2446
@@ -390,6 +396,138 @@ void orc_mul_sigmoid(float* y, const float* g, size_t n)
 	size_t i = 0;
 	for (; i + 8 <= n; ++i) y[i] = y[i] * (1.0f / (1.0f + std::exp(-g[i])));
 	for (; i < n; ++i) y[i] /= 1.0f + std::exp(-g[i]);
+}
+
+// Q8_0 split layout from fp32, one 32-element block at a time: the block's
+// absmax / 127 rounded to BF16 is the scale; q = round-to-nearest-even of
+// w / scale (w * (1 / scale)), clamped to [-127, 127]; a zero block has
+// scale 0 and q 0. The reference is built with -ffast-math (reference
+// CMakeLists.txt:66-76), which turns the division by the constant 127 into a
+// multiplication by its fp32 reciprocal; so does this restatement.
+void orc_quantize_q8_0(const float* src, int8_t* qs, uint16_t* scales, size_t n)
+{
+	for (size_t b = 0; b < n; b += 32)
+	{
+		float amax = 0.0f;
+		for (size_t k = 0; k < 32; ++k) amax = std::max(amax, std::fabs(src[b + k]));
+		const uint16_t sb = f32_to_bf16(amax * (1.0f / 127.0f));
+		const float scale = bf16_to_f32(sb);
+		scales[b / 32] = sb;
+		const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+		for (size_t k = 0; k < 32; ++k)
+		{
+			const long q = std::lrintf(src[b + k] * inv);
+			qs[b + k] = static_cast<int8_t>(std::min(127L, std::max(-127L, q)));
+		}
+	}
+}
+
+// Q4_S split layout from fp32: per 32-element block scale = (max - min) / 15
+// and bias = min, both rounded to BF16 before use; q = rne((w - bias) / scale)
+// clamped to [0, 15]; byte i of a block holds element i (low nibble) and
+// element i + 16 (high nibble). (max - min) / 15 is evaluated as
+// (max - min) * (1 / 15), as the reference's -ffast-math build does.
+void orc_quantize_q4_s(const float* src, uint8_t* qs, uint16_t* scales, uint16_t* biases, size_t n)
+{
+	for (size_t b = 0; b < n; b += 32)
+	{
+		float lo = src[b], hi = src[b];
+		for (size_t k = 1; k < 32; ++k)
+		{
+			lo = std::min(lo, src[b + k]);
+			hi = std::max(hi, src[b + k]);
+		}
+		const uint16_t sb = f32_to_bf16((hi - lo) * (1.0f / 15.0f)), bb = f32_to_bf16(lo);
+		const float scale = bf16_to_f32(sb), bias = bf16_to_f32(bb);
+		scales[b / 32] = sb;
+		biases[b / 32] = bb;
+		const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+		for (size_t k = 0; k < 16; ++k)
+		{
+			const long q0 = std::min(15L, std::max(0L, std::lrintf((src[b + k] - bias) * inv)));
+			const long q1 = std::min(15L, std::max(0L, std::lrintf((src[b + k + 16] - bias) * inv)));
+			qs[b / 2 + k] = static_cast<uint8_t>(q0 | (q1 << 4));
+		}
+	}
+}
+
+// out[b] = sum of x[32 b .. 32 b + 31] in fp32, in the order the
+// reference's -ffast-math build evaluates its eight-lane sums: lane j is
+// (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]), then the lanes pairwise as
+// its horizontal sum does (reference nn_ops.cpp:27-36).
+void orc_block_sums(const float* x, float* out, size_t n)
+{
+	for (size_t b = 0; b < n; b += 32)
+	{
+		float lane[8];
+		for (int j = 0; j < 8; ++j) lane[j] = (x[b + j] + x[b + 8 + j]) + (x[b + 16 + j] + x[b + 24 + j]);
+		out[b / 32] = ((lane[0] + lane[4]) + (lane[1] + lane[5])) + ((lane[2] + lane[6]) + (lane[3] + lane[7]));
+	}
+}
+
+// y[n][r] = sum_k W[r][k] x[n][k] with W BF16 row-major [rows][cols]; fp32
+// products summed in fp32 in column order.
+void orc_gemv_bf16(const uint16_t* W, const float* X, size_t x_stride, float* Y, size_t y_stride, uint32_t rows,
+                   uint32_t cols, uint32_t n_batch)
+{
+	for (uint32_t n = 0; n < n_batch; ++n)
+		for (uint32_t r = 0; r < rows; ++r)
+		{
+			const uint16_t* w = W + static_cast<size_t>(r) * cols;
+			const float* x = X + n * x_stride;
+			float s = 0.0f;
+			for (uint32_t k = 0; k < cols; ++k) s += bf16_to_f32(w[k]) * x[k];
+			Y[n * y_stride + r] = s;
+		}
+}
+
+// Q8_0 split layout: y = sum over blocks of scale_b * (sum_{k in b} q_k x_k).
+void orc_gemv_q8_0(const int8_t* qs, const uint16_t* scales, const float* X, size_t x_stride, float* Y,
+                   size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
+{
+	const uint32_t nb = cols / 32;
+	for (uint32_t n = 0; n < n_batch; ++n)
+		for (uint32_t r = 0; r < rows; ++r)
+		{
+			const float* x = X + n * x_stride;
+			float s = 0.0f;
+			for (uint32_t b = 0; b < nb; ++b)
+			{
+				const int8_t* q = qs + static_cast<size_t>(r) * cols + 32 * b;
+				float d = 0.0f;
+				for (int k = 0; k < 32; ++k) d += static_cast<float>(q[k]) * x[32 * b + k];
+				s += bf16_to_f32(scales[static_cast<size_t>(r) * nb + b]) * d;
+			}
+			Y[n * y_stride + r] = s;
+		}
+}
+
+// Q4_S split layout: y = sum_b scale_b * (sum_{k in b} q_k x_k) + sum_b
+// bias_b * S_b, S_b = xsum[b] (the block sums of x).
+void orc_gemv_q4_s(const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const float* X,
+                   size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y, size_t y_stride, uint32_t rows,
+                   uint32_t cols, uint32_t n_batch)
+{
+	const uint32_t nb = cols / 32;
+	for (uint32_t n = 0; n < n_batch; ++n)
+		for (uint32_t r = 0; r < rows; ++r)
+		{
+			const float* x = X + n * x_stride;
+			float s = 0.0f, t = 0.0f;
+			for (uint32_t b = 0; b < nb; ++b)
+			{
+				const uint8_t* q = qs + (static_cast<size_t>(r) * cols + 32 * b) / 2;
+				float d = 0.0f;
+				for (int k = 0; k < 16; ++k)
+				{
+					d += static_cast<float>(q[k] & 15) * x[32 * b + k];
+					d += static_cast<float>(q[k] >> 4) * x[32 * b + 16 + k];
+				}
+				s += bf16_to_f32(scales[static_cast<size_t>(r) * nb + b]) * d;
+				t += bf16_to_f32(biases[static_cast<size_t>(r) * nb + b]) * XSUM[n * xsum_stride + b];
+			}
+			Y[n * y_stride + r] = s + t;
+		}
 }
 
 // The step before the attention core, in the reference's order: per-head

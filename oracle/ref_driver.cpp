@@ -16,6 +16,10 @@
 //       (reference nn_ops.h:79), ref_rmsnorm_plain calls nnc_rmsnorm_f32
 //       (reference nn_ops.h:73);
 //   ref_mul_sigmoid  calls nnc_mul_sigmoid_f32 (reference nn_ops.h:248);
+//   ref_quantize_q8_0 / ref_quantize_q4_s / ref_block_sums / ref_gemv_bf16 /
+//       ref_gemv_q8_0 / ref_gemv_q4_s call nnc_quantize_f32_to_q8_0,
+//       nnc_quantize_f32_to_q4_s, nnc_block_sums_f32 and the batched gemvs
+//       (reference nn_ops.h:119-180, 193-205; the JIT kernels behind them);
 //   ref_set_threads / ref_threads call nnc_set_num_threads / nnc_num_threads
 //       (reference nnc.h:104-105);
 //   ref_attend_layer drives nnc_attn_block/merge/finish through the reference's
@@ -117,6 +121,37 @@ void ref_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
 }
 
 void ref_mul_sigmoid(float* y, const float* g, size_t n) { nnc_mul_sigmoid_f32(y, g, n); }
+
+void ref_quantize_q8_0(const float* src, int8_t* qs, uint16_t* scales, size_t n)
+{
+	nnc_quantize_f32_to_q8_0(src, qs, scales, n);
+}
+
+void ref_quantize_q4_s(const float* src, uint8_t* qs, uint16_t* scales, uint16_t* biases, size_t n)
+{
+	nnc_quantize_f32_to_q4_s(src, qs, scales, biases, n);
+}
+
+void ref_block_sums(const float* x, float* out, size_t n) { nnc_block_sums_f32(x, out, n); }
+
+void ref_gemv_bf16(const uint16_t* W, const float* X, size_t x_stride, float* Y, size_t y_stride, uint32_t rows,
+                   uint32_t cols, uint32_t n_batch)
+{
+	nnc_gemv_bf16w_f32x_batch(W, X, x_stride, Y, y_stride, rows, cols, n_batch);
+}
+
+void ref_gemv_q8_0(const int8_t* qs, const uint16_t* scales, const float* X, size_t x_stride, float* Y,
+                   size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
+{
+	nnc_gemv_q8_0_f32x_batch(qs, scales, X, x_stride, Y, y_stride, rows, cols, n_batch);
+}
+
+void ref_gemv_q4_s(const uint8_t* qs, const uint16_t* scales, const uint16_t* biases, const float* X,
+                   size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y, size_t y_stride, uint32_t rows,
+                   uint32_t cols, uint32_t n_batch)
+{
+	nnc_gemv_q4_s_f32x_batch(qs, scales, biases, X, x_stride, XSUM, xsum_stride, Y, y_stride, rows, cols, n_batch);
+}
 
 void ref_set_threads(int n) { nnc_set_num_threads(n); }
 int ref_threads(void) { return nnc_num_threads(); }

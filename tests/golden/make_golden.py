@@ -157,6 +157,22 @@ def main() -> int:
     data["gate/y"] = yg
     data["gate/g"] = gg
     data["gate/out"] = ref.mul_sigmoid(yg, gg)
+    # The weight gemvs: a 72 x 256 matrix (rows not a multiple of 16), three
+    # activation vectors, nnc's quantizers and its BF16 / Q8_0 / Q4_S gemvs.
+    wg = (rng.standard_normal((72, 256)) * 0.05).astype(np.float32)
+    wg[3, :32] = 0.0  # an all-zero block: scale 0
+    xg = rng.standard_normal((3, 256)).astype(np.float32)
+    data["gemv/w"] = wg
+    data["gemv/x"] = xg
+    wb = ref.bf16_round(wg)
+    data["gemv/bf16/y"] = ref.gemv_bf16(wb, xg)
+    q8 = ref.quantize_q8_0(wg)
+    data["gemv/q8_0/qs"], data["gemv/q8_0/scales"] = q8
+    data["gemv/q8_0/y"] = ref.gemv_q8_0(*q8, xg)
+    q4 = ref.quantize_q4_s(wg)
+    data["gemv/q4_s/qs"], data["gemv/q4_s/scales"], data["gemv/q4_s/biases"] = q4
+    data["gemv/xsum"] = ref.block_sums(xg)
+    data["gemv/q4_s/y"] = ref.gemv_q4_s(*q4, xg)
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
     return 0

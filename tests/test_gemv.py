@@ -1,0 +1,201 @@
+"""The weight gemvs on either side of attention (reference
+src/libnnc/nn_ops.h:95-180, nn_ops.cpp:1000-1053, 1200-1316, 1352-1700):
+BF16, Q8_0 split and Q4_S split weights, one activation vector or a batch of
+up to 16.
+
+CPU: the oracle's quantizers and block sums bit-exact against the reference
+(vectors and compiled code), its gemvs against the reference's JIT kernels
+and a float64 product of the dequantised weights, and closed forms. GPU: the
+HIP gemvs against the oracle. Bound for every gemv comparison, per output:
+|y - y_ref| <= 1e-5 * sum_k |w_rk x_k| (fp32 accumulation of the products;
+the GPU's activations enter as bf16 hi + lo, 16 significant bits)."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_vectors.npz"
+REL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def bf16_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def dequant(fmt, w):
+    """Float64 weights [rows, cols] from a layout tuple."""
+    if fmt == "bf16":
+        return bf16_f32(w[0]).astype(np.float64)
+    if fmt == "q8_0":
+        qs, sc = w
+        return qs.astype(np.float64) * np.repeat(bf16_f32(sc).astype(np.float64), 32, axis=1)
+    qs, sc, bi = w
+    rows, half = qs.shape
+    q = np.empty((rows, half * 2), np.float64)
+    blocks = qs.reshape(rows, -1, 16)
+    q.reshape(rows, -1, 32)[:, :, :16] = blocks & 15
+    q.reshape(rows, -1, 32)[:, :, 16:] = blocks >> 4
+    return q * np.repeat(bf16_f32(sc), 32, axis=1) + np.repeat(bf16_f32(bi), 32, axis=1)
+
+
+def bound(fmt, w, x):
+    return REL * (np.abs(x.astype(np.float64)) @ np.abs(dequant(fmt, w)).T) + 1e-30
+
+
+def layouts(orc, wf):
+    return {"bf16": (orc.bf16_round(wf),), "q8_0": orc.quantize_q8_0(wf), "q4_s": orc.quantize_q4_s(wf)}
+
+
+def oracle_gemv(orc, fmt, w, x):
+    return {"bf16": orc.gemv_bf16, "q8_0": orc.gemv_q8_0, "q4_s": orc.gemv_q4_s}[fmt](*w, x)
+
+
+# ---- CPU: the oracle -------------------------------------------------------------------
+
+def test_quantizers_and_block_sums_match_reference_vectors(orc, gold):
+    w, x = gold["gemv/w"], gold["gemv/x"]
+    for got, want in zip(orc.quantize_q8_0(w), (gold["gemv/q8_0/qs"], gold["gemv/q8_0/scales"])):
+        assert np.array_equal(got, want)
+    for got, want in zip(orc.quantize_q4_s(w),
+                         (gold["gemv/q4_s/qs"], gold["gemv/q4_s/scales"], gold["gemv/q4_s/biases"])):
+        assert np.array_equal(got, want)
+    assert np.array_equal(orc.block_sums(x), gold["gemv/xsum"])
+
+
+def test_gemvs_match_reference_vectors(orc, gold):
+    w, x = gold["gemv/w"], gold["gemv/x"]
+    lay = {"bf16": (orc.bf16_round(w),), "q8_0": (gold["gemv/q8_0/qs"], gold["gemv/q8_0/scales"]),
+           "q4_s": (gold["gemv/q4_s/qs"], gold["gemv/q4_s/scales"], gold["gemv/q4_s/biases"])}
+    for fmt, wl in lay.items():
+        got = oracle_gemv(orc, fmt, wl, x)
+        assert np.all(np.abs(got - gold[f"gemv/{fmt}/y"]) <= bound(fmt, wl, x)), fmt
+
+
+def test_quantizers_and_gemvs_match_reference_code(orc, ref):
+    rng = np.random.default_rng(11)
+    for rows, cols, n in ((64, 256, 1), (260, 512, 3), (1024, 2560, 16)):
+        wf = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        x = rng.standard_normal((n, cols)).astype(np.float32)
+        for a, b in zip(orc.quantize_q8_0(wf), ref.quantize_q8_0(wf)):
+            assert np.array_equal(a, b)
+        for a, b in zip(orc.quantize_q4_s(wf), ref.quantize_q4_s(wf)):
+            assert np.array_equal(a, b)
+        assert np.array_equal(orc.block_sums(x), ref.block_sums(x))
+        for fmt, wl in layouts(orc, wf).items():
+            got = oracle_gemv(orc, fmt, wl, x)
+            want = oracle_gemv(ref, fmt, wl, x)
+            assert np.all(np.abs(got - want) <= bound(fmt, wl, x)), (fmt, rows, cols, n)
+
+
+def test_gemvs_match_float64_product(orc):
+    rng = np.random.default_rng(12)
+    wf = (rng.standard_normal((96, 512)) * 0.1).astype(np.float32)
+    x = rng.standard_normal((4, 512)).astype(np.float32)
+    for fmt, wl in layouts(orc, wf).items():
+        exact = x.astype(np.float64) @ dequant(fmt, wl).T
+        assert np.all(np.abs(oracle_gemv(orc, fmt, wl, x) - exact) <= bound(fmt, wl, x)), fmt
+
+
+def test_gemv_closed_forms(orc):
+    # One weight per row: y_r = w_r * x_{k(r)} exactly; Q8_0 of a block holding
+    # a single value v: scale = |v| / 127 rounded to BF16, q = +-127.
+    cols, rows = 64, 8
+    wf = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        wf[r, 5 * r] = 0.25 * (r + 1) * (-1) ** r
+    x = np.arange(cols, dtype=np.float32)[None, :] / 8
+    y = orc.gemv_bf16(orc.bf16_round(wf), x)[0]
+    assert np.array_equal(y, np.array([wf[r, 5 * r] * x[0, 5 * r] for r in range(rows)], np.float32))
+    qs, sc = orc.quantize_q8_0(wf)
+    assert all(abs(int(qs[r, 5 * r])) == 127 for r in range(rows))
+    yq = orc.gemv_q8_0(qs, sc, x)[0]
+    assert np.allclose(yq, y, rtol=1e-2)
+    # Q4_S of a constant block: scale 0, bias = the value: y = v * (block sum of x).
+    wc = np.full((2, 32), 0.5, np.float32)
+    q4 = orc.quantize_q4_s(wc)
+    assert np.all(q4[1] == 0) and np.all(bf16_f32(q4[2]) == 0.5)
+    xc = np.ones((1, 32), np.float32)
+    assert np.array_equal(orc.gemv_q4_s(*q4, xc)[0], np.array([16.0, 16.0], np.float32))
+
+
+# ---- GPU: the HIP gemvs ------------------------------------------------------------------
+
+GPU_SHAPES = [
+    (256, 512, 1),      # one K split
+    (4096, 2560, 1),    # Qwen3-4B q projection, decode
+    (1024, 2560, 5),    # k / v projection, an MTP verification batch
+    (2560, 9728, 16),   # MLP down, a full session batch (many K splits)
+    (72, 96, 3),        # rows not a multiple of 16, three blocks
+    (9728, 2560, 16),   # MLP gate / up
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,n", GPU_SHAPES, ids=[f"{r}x{c}x{n}" for r, c, n in GPU_SHAPES])
+def test_hip_gemv_matches_oracle(orc, rows, cols, n):
+    import libllmcpu_amd as nh
+
+    rng = np.random.default_rng(rows * 7 + cols + n)
+    wf = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    x = (rng.standard_normal((n, cols)) * 2).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        for fmt, wl in layouts(orc, wf).items():
+            print(f"case gemv {fmt} {rows} x {cols}, {n} vectors", flush=True)
+            got = kv.gemv(fmt, wl, x, rows=rows, cols=cols)
+            want = oracle_gemv(orc, fmt, wl, x)
+            err = np.abs(got.astype(np.float64) - want)
+            b = bound(fmt, wl, x)
+            print(f"  max |err| / bound {float((err / b).max()):.3f}", flush=True)
+            assert np.all(err <= b), fmt
+            if fmt == "q4_s":  # the caller's block sums instead of the kernel's
+                got2 = kv.gemv(fmt, wl, x, rows=rows, cols=cols, xsum=orc.block_sums(x))
+                assert np.array_equal(got2, got)
+
+
+@pytest.mark.gpu
+def test_hip_gemv_strides_and_errors(orc):
+    import libllmcpu_amd as nh
+    from libllmcpu_amd import hip_rt
+
+    rows, cols, n = 48, 128, 3
+    rng = np.random.default_rng(5)
+    wf = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    qs, sc = orc.quantize_q8_0(wf)
+    xs, ys = cols + 32, rows + 8
+    xp = np.zeros((n, xs), np.float32)
+    xp[:, :cols] = x
+    dev = [hip_rt.malloc(a.nbytes) for a in (qs, sc, xp)]
+    y_dev = hip_rt.malloc(n * ys * 4)
+    try:
+        for d, a in zip(dev, (qs, sc, xp)):
+            hip_rt.to_device(d, a)
+        hip_rt.to_device(y_dev, np.full((n, ys), 7.0, np.float32))
+        with nh.KVCache([16], [64]) as kv:
+            print("case gemv strides", flush=True)
+            kv.gemv_device("q8_0", (dev[0], dev[1]), dev[2], y_dev, rows=rows, cols=cols, n_batch=n, x_stride=xs,
+                           y_stride=ys)
+            kv.sync()
+            y = hip_rt.to_host(np.empty((n, ys), np.float32), y_dev)
+            want = orc.gemv_q8_0(qs, sc, x)
+            assert np.all(np.abs(y[:, :rows] - want) <= bound("q8_0", (qs, sc), x))
+            assert np.all(y[:, rows:] == 7.0)  # the gap between output rows is untouched
+            print("case gemv errors", flush=True)
+            with pytest.raises(nh.NncError) as e:
+                kv.gemv_device("q8_0", (dev[0], dev[1]), dev[2], y_dev, rows=rows, cols=cols - 16, n_batch=n)
+            assert e.value.status == nh.NncStatus.UNSUPPORTED_MODEL
+            with pytest.raises(nh.NncError) as e:
+                kv.gemv_device("q8_0", (dev[0], dev[1]), dev[2], y_dev, rows=rows, cols=cols, n_batch=n,
+                               x_stride=cols - 1)
+            assert e.value.status == nh.NncStatus.INVALID_ARGUMENT
+            kv.gemv_device("q8_0", (dev[0], dev[1]), dev[2], y_dev, rows=rows, cols=cols, n_batch=0)  # no-op
+    finally:
+        for d in dev + [y_dev]:
+            hip_rt.free(d)
