@@ -66,7 +66,11 @@ typedef struct nnc_hip_kv nnc_hip_kv;
  * kv_dim[i] elements (BF16 when bf16, else F32), zero-filled, plus one HIP
  * stream. Mirrors model_kv_init's buffer allocation (reference
  * model.cpp:1908-1957; rows come from the same rule: n_ctx, or a ring of
- * round_up(window + n_batch, 256) rows for a sliding layer).
+ * round_up(window + n_batch, 256) rows for a sliding layer). A BF16 cache
+ * also keeps an fp16 copy of every buffer, written by every append, for the
+ * prefill kernel (twice the device memory; NNC_HIP_F16_SHADOW=0 in the
+ * environment at creation leaves it out, and prefill then runs about 13 %
+ * slower). The nnc-visible buffers stay BF16 in nnc's layout.
  * NNC_ERR_INVALID_ARGUMENT: n_buf <= 0, a NULL pointer, rows or kv_dim <= 0.
  * NNC_ERR_OUT_OF_MEMORY: the device allocation failed.
  * NNC_ERR_UNSUPPORTED_CPU: no usable HIP device (the nearest existing status:
@@ -77,7 +81,8 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 /* Frees the buffers, the scratch and the stream. NULL is a no-op. */
 void nnc_hip_kv_free(nnc_hip_kv* kv);
 
-/* Total device bytes held by the K/V buffers (reference model.h:325, bytes). */
+/* Total device bytes held by the K/V buffers, fp16 copies included
+ * (reference model.h:325, bytes). */
 uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv);
 
 /* Writes n_tok rows for positions pos0 .. pos0 + n_tok - 1 into buffer

@@ -46,6 +46,8 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace nnchip
 {
 	namespace
@@ -214,8 +216,11 @@ namespace nnchip
 			// Byte offsets are 32-bit (the host keeps a buffer under 2 GiB).
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
-			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
-			const char* vbase = static_cast<const char*>(p.V) + head_bytes;
+			// The fp16 shadow when the buffer has one and every value in it is
+			// exact (Q then goes in fp16 too, if it fits; see below).
+			const bool shadow = p.K16 != nullptr && __builtin_amdgcn_readfirstlane(*p.range) == 0;
+			const char* kbase = static_cast<const char*>(shadow ? p.K16 : p.K) + head_bytes;
+			const char* vbase = static_cast<const char*>(shadow ? p.V16 : p.V) + head_bytes;
 
 			// Step i of the wavefront: its first key and the last key of its
 			// segment; its descriptors are based at the block's first row and in
@@ -260,40 +265,73 @@ namespace nnchip
 			// The first step's tiles go out before Q is read, so the latencies overlap.
 			if (n_steps > 0) load_tiles(0);
 
-			// Q, pre-scaled into log2 units, as bf16 hi + lo in LDS, in the K
-			// tiles' layout (row r, 16-byte slot s at s ^ kswz(r)): thread t
-			// converts the eighth t % 8 of row t / 8.
+			// Q, pre-scaled into log2 units, in LDS in the K tiles' layout (row r,
+			// 16-byte slot s at s ^ kswz(r)): thread t converts the eighth t % 8
+			// of row t / 8. With the shadow, Q goes in fp16 (one MFMA per product
+			// against the exact fp16 K) unless some value of the work-group's Q
+			// is past fp16's range; otherwise as bf16 hi + lo (two MFMAs against
+			// the exact bf16 K).
 			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kQlo);
 			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + S::kQhi);
+			constexpr int E = HD / 8; // elements per thread
+			const int qr = threadIdx.x >> 3, qseg = threadIdx.x & 7;
+			float xq[E];
+			bool q_big = false;
 			{
-				constexpr int E = HD / 8; // elements per thread
-				const int r = threadIdx.x >> 3, seg = threadIdx.x & 7;
-				const int grow = row0 + r;
+				const int grow = row0 + qr;
 				const bool ok = grow < n_rows;
 				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
-				                                  static_cast<size_t>(kvh * G + grow % G) * HD + seg * E
+				                                  static_cast<size_t>(kvh * G + grow % G) * HD + qseg * E
 				                            : 0);
 #pragma unroll
-				for (int c = 0; c < E / 8; ++c)
+				for (int c = 0; c < E / 4; ++c)
 				{
-					float x[8];
-					if (ok)
-					{
-						const float4 a = *reinterpret_cast<const float4*>(qp + 8 * c);
-						const float4 b = *reinterpret_cast<const float4*>(qp + 8 * c + 4);
-						x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-						x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+					const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 4 * c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+					xq[4 * c] = a.x * p.qscale;
+					xq[4 * c + 1] = a.y * p.qscale;
+					xq[4 * c + 2] = a.z * p.qscale;
+					xq[4 * c + 3] = a.w * p.qscale;
+				}
 #pragma unroll
-						for (int e = 0; e < 8; ++e) x[e] *= p.qscale;
-					}
-					else
-					{
+				for (int e = 0; e < E; ++e) q_big |= !(fabsf(xq[e]) <= 65504.0f);
+			}
+			// Whether any thread of the work-group holds such a value: one word
+			// per wavefront in the Q lo region (written below only after every
+			// thread has read the words).
+			bool any_big = false;
+			if (shadow) // uniform over the work-group
+			{
+				uint32_t* words = reinterpret_cast<uint32_t*>(s_raw + S::kQlo);
+				const bool wave_big = __builtin_amdgcn_ballot_w64(q_big) != 0;
+				if (lane == 0) words[wave] = wave_big ? 1u : 0u;
+				__syncthreads();
 #pragma unroll
-						for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-					}
+				for (int w = 0; w < kWaves; ++w) any_big |= words[w] != 0;
+				__syncthreads();
+			}
+			const bool use16 = shadow && !any_big;
+			if (shadow && !use16)
+			{
+				// Rare: the first tiles came from the shadow; fetch the bf16 ones.
+				dma_done();
+				kbase = static_cast<const char*>(p.K) + head_bytes;
+				vbase = static_cast<const char*>(p.V) + head_bytes;
+				if (n_steps > 0) load_tiles(0);
+			}
+#pragma unroll
+			for (int c = 0; c < E / 8; ++c)
+			{
+				const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
+				if (use16)
+				{
+					const u32x4 h16 = {pack_f16x2(xq[8 * c], xq[8 * c + 1]), pack_f16x2(xq[8 * c + 2], xq[8 * c + 3]),
+					                   pack_f16x2(xq[8 * c + 4], xq[8 * c + 5]), pack_f16x2(xq[8 * c + 6], xq[8 * c + 7])};
+					*reinterpret_cast<u32x4*>(s_qhi + off) = h16;
+				}
+				else
+				{
 					bf16x8 hi, lo;
-					split_bf16x8(x, hi, lo);
-					const int off = r * HD + 8 * ((seg * (E / 8) + c) ^ kswz<HD>(r));
+					split_bf16x8(xq + 8 * c, hi, lo);
 					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
 					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
 				}
@@ -330,120 +368,162 @@ namespace nnchip
 			const int tq = (lane >> 4) & 1, ti = lane & 15;
 			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-			for (int i = 0; i < n_steps; ++i)
+			// The key loop, in one of two instantiations: fp16 K, V and Q (the
+			// shadow), or bf16 K and V with Q as hi + lo.
+			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
 			{
-				int seg_last;
-				const int kw0 = step_key(i, seg_last);
-				dma_done(); // this step's tiles have landed
-
-				// S^T - m (32 keys x 32 rows), while V^T converts to fp16: keys
-				// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
-				// A wavefront in one of its MFMA phases raises its issue priority,
-				// so the other wavefront of the SIMD fills the matrix core's shadow
-				// with its softmax (measured: 4.6 % faster per prefill step).
-				__builtin_amdgcn_s_setprio(1);
-				f32x16 sc = c_init;
-#pragma unroll
-				for (int t = 0; t < KT; ++t)
+				constexpr bool F16 = decltype(f16_tag)::value;
+				for (int i = 0; i < n_steps; ++i)
 				{
-					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
-					if constexpr (S::QREG)
-					{
-						sc = mfma32x32x16(a, qhi[t], sc);
-						sc = mfma32x32x16(a, qlo[t], sc);
-					}
-					else
-					{
-						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
-						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
-					}
-				}
-				f16x8 vta[2][DBK];
-#pragma unroll
-				for (int c = 0; c < 2; ++c)
-#pragma unroll
-					for (int b = 0; b < DBK; ++b)
+					int seg_last;
+					const int kw0 = step_key(i, seg_last);
+					dma_done(); // this step's tiles have landed
+
+					// S^T - m (32 keys x 32 rows), while V^T converts to fp16: keys
+					// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
+					// A wavefront in one of its MFMA phases raises its issue priority,
+					// so the other wavefront of the SIMD fills the matrix core's shadow
+					// with its softmax (measured: 4.6 % faster per prefill step).
+					__builtin_amdgcn_s_setprio(1);
+					f32x16 sc = c_init;
+					f16x8 vta[2][DBK];
+					// V^T as read: lane (g, c) of a transposing read holds keys
+					// 16 c' + 4 h + g .. of the tile rows below (both halves).
+					auto vt_pair = [&](int c, int b) __attribute__((always_inline)) -> u32x4
 					{
 						const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), hf = 4 * (ti & 1);
 						const int ra = 16 * c + 4 * h + (ti >> 2), rb = ra + 8;
 						const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + hf);
 						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + hf);
-						vta[c][b] = as_f16x8(bf16x8_to_f16x8(u32x4{lo.x, lo.y, hi.x, hi.y}));
-					}
-				// One MFMA, one LDS read, five VALU instructions at a time through
-				// the QK phase (measured: 1 % faster than the compiler's order).
-#pragma unroll
-				for (int z = 0; z < 2 * KT; ++z)
-				{
-					__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-					__builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-					__builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-				}
-				__builtin_amdgcn_s_setprio(0);
-				// Both tiles are read: the next step's rows. A DMA's LDS write is
-				// not ordered after earlier LDS reads still in flight, so those
-				// complete first.
-				lds_reads_done();
-				if (i + 1 < n_steps) load_tiles(i + 1);
-
-				// Mask keys outside the row's span or past the segment (only on
-				// steps that cross an edge).
-				if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
-				{
-					const int hi_key = min(rlast, seg_last);
-#pragma unroll
-					for (int e = 0; e < 16; ++e)
+						return u32x4{lo.x, lo.y, hi.x, hi.y};
+					};
+					if constexpr (F16)
 					{
-						const int k = kw0 + 8 * (e / 4) + 4 * h + (e % 4);
-						if (k < rfirst || k > hi_key) sc[e] = -INFINITY;
+						// fp16 K and Q: one MFMA per 16 elements of d; V^T is already fp16.
+	#pragma unroll
+						for (int t = 0; t < KT; ++t)
+						{
+							const f16x8 a = *reinterpret_cast<const f16x8*>(kt + q_slot(t));
+							if constexpr (S::QREG)
+								sc = mfma32x32x16(a, __builtin_bit_cast(f16x8, qhi[t]), sc);
+							else
+								sc = mfma32x32x16(a, *reinterpret_cast<const f16x8*>(s_qhi + q_slot(t)), sc);
+						}
+	#pragma unroll
+						for (int c = 0; c < 2; ++c)
+	#pragma unroll
+							for (int b = 0; b < DBK; ++b) vta[c][b] = as_f16x8(vt_pair(c, b));
+	#pragma unroll
+						for (int z = 0; z < KT; ++z)
+						{
+							__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+							__builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+						}
 					}
-				}
-
-				// Raise the row's offset when its scores outgrow it by more than
-				// kLazy (or on its first visible key): rare, and O's rescale with it.
-				float mx = sc[0];
-#pragma unroll
-				for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
-				mx = max_with_other_half(mx);
-				const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
-				if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
-				{
-					const bool fresh = m_off == -INFINITY;
-					const float d = grow ? mx : 0.0f;
-					const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
-					if (grow) m_off = (fresh ? 0.0f : m_off) + d;
-					const float ci = m_off == -INFINITY ? 0.0f : -m_off;
-#pragma unroll
-					for (int e = 0; e < 16; ++e) c_init[e] = ci;
-#pragma unroll
-					for (int b = 0; b < DBK; ++b) acc_o[b] *= alpha;
-					l_acc *= alpha;
-					sc -= d;
-				}
-
-				// P^T as the B operand, per 16-key half c (k-slot j holds key
-				// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row sums
-				// from the same fp16 weights.
-#pragma unroll
-				for (int c = 0; c < 2; ++c)
-				{
-					u32x4 pw;
-#pragma unroll
-					for (int q = 0; q < 4; ++q)
+					else
 					{
-						// (a scalar copy: clang's bit_cast of a vector element
-						// reads element 0 whatever the index)
-						const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
-						pw[q] = w2;
-						l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
+						// bf16 K, Q as hi + lo: two MFMAs; V^T converted to fp16.
+	#pragma unroll
+						for (int t = 0; t < KT; ++t)
+						{
+							const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
+							if constexpr (S::QREG)
+							{
+								sc = mfma32x32x16(a, qhi[t], sc);
+								sc = mfma32x32x16(a, qlo[t], sc);
+							}
+							else
+							{
+								sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
+								sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
+							}
+						}
+	#pragma unroll
+						for (int c = 0; c < 2; ++c)
+	#pragma unroll
+							for (int b = 0; b < DBK; ++b) vta[c][b] = as_f16x8(bf16x8_to_f16x8(vt_pair(c, b)));
+						// One MFMA, one LDS read, five VALU instructions at a time
+						// through the QK phase (measured: 1 % faster than the
+						// compiler's order).
+	#pragma unroll
+						for (int z = 0; z < 2 * KT; ++z)
+						{
+							__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+							__builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+							__builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+						}
 					}
-					const f16x8 pb = as_f16x8(pw);
-					__builtin_amdgcn_s_setprio(1);
-#pragma unroll
-					for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(vta[c][b], pb, acc_o[b]);
 					__builtin_amdgcn_s_setprio(0);
+					// Both tiles are read: the next step's rows. A DMA's LDS write is
+					// not ordered after earlier LDS reads still in flight, so those
+					// complete first.
+					lds_reads_done();
+					if (i + 1 < n_steps) load_tiles(i + 1);
+
+					// Mask keys outside the row's span or past the segment (only on
+					// steps that cross an edge).
+					if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
+					{
+						const int hi_key = min(rlast, seg_last);
+	#pragma unroll
+						for (int e = 0; e < 16; ++e)
+						{
+							const int k = kw0 + 8 * (e / 4) + 4 * h + (e % 4);
+							if (k < rfirst || k > hi_key) sc[e] = -INFINITY;
+						}
+					}
+
+					// Raise the row's offset when its scores outgrow it by more than
+					// kLazy (or on its first visible key): rare, and O's rescale with it.
+					float mx = sc[0];
+	#pragma unroll
+					for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+					mx = max_with_other_half(mx);
+					const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
+					if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
+					{
+						const bool fresh = m_off == -INFINITY;
+						const float d = grow ? mx : 0.0f;
+						const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
+						if (grow) m_off = (fresh ? 0.0f : m_off) + d;
+						const float ci = m_off == -INFINITY ? 0.0f : -m_off;
+	#pragma unroll
+						for (int e = 0; e < 16; ++e) c_init[e] = ci;
+	#pragma unroll
+						for (int b = 0; b < DBK; ++b) acc_o[b] *= alpha;
+						l_acc *= alpha;
+						sc -= d;
+					}
+
+					// P^T as the B operand, per 16-key half c (k-slot j holds key
+					// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row sums
+					// from the same fp16 weights.
+	#pragma unroll
+					for (int c = 0; c < 2; ++c)
+					{
+						u32x4 pw;
+	#pragma unroll
+						for (int q = 0; q < 4; ++q)
+						{
+							// (a scalar copy: clang's bit_cast of a vector element
+							// reads element 0 whatever the index)
+							const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
+							pw[q] = w2;
+							l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
+						}
+						const f16x8 pb = as_f16x8(pw);
+						__builtin_amdgcn_s_setprio(1);
+	#pragma unroll
+						for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(vta[c][b], pb, acc_o[b]);
+						__builtin_amdgcn_s_setprio(0);
+					}
 				}
-			}
+
+			};
+			if (use16)
+				key_loop(std::true_type{});
+			else
+				key_loop(std::false_type{});
 
 			// Merge the wavefronts: o = sum_w o_w 2^(m_w - M) / sum_w l_w 2^(m_w - M),
 			// 0 when no key was seen (reference nn_ops.cpp:492). The row

@@ -165,6 +165,16 @@ namespace nnchip
 
 	__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+	// The fp16 copy of a BF16 K/V element kept for the prefill kernel (RNE;
+	// exact for every finite bf16 up to 65504 in magnitude down to 2^-14, and
+	// within 2^-25 below). Sets `bad` for a finite value past fp16's range.
+	__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint32_t b, bool& bad)
+	{
+		const float f = bf16_bits_to_f32(b);
+		bad |= fabsf(f) > 65504.0f && fabsf(f) < INFINITY;
+		return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+	}
+
 	// Qwen3.5's output gate on one attention output (reference
 	// model.cpp:1759-1760, nn_ops.cpp:1731-1742): y * (1 / (1 + e^-g)).
 	__device__ __forceinline__ float gated(float y, const float* gate, size_t i)

@@ -11,19 +11,49 @@ namespace nnchip
 		// The KV append of reference model.cpp:1668-1691: position pos0 + t goes
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
+		// With a shadow (K16, V16 not null) the fp16 copies of the same rows
+		// are written too, and `range` is set when a value does not fit fp16.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
-		                                   int rows, int kv_dim, int pos0, int n_tok)
+		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* K16, uint16_t* V16,
+		                                   int* range)
 		{
 			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+			bool bad = false;
 			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
 			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
 			{
 				const int t = static_cast<int>(i / kv_dim);
 				const int c = static_cast<int>(i % kv_dim);
 				const size_t dst = static_cast<size_t>((pos0 + t) % rows) * kv_dim + c;
-				K[dst] = static_cast<uint16_t>(f32_to_bf16_bits(k_rows[i]));
-				V[dst] = static_cast<uint16_t>(f32_to_bf16_bits(v_rows[i]));
+				const uint32_t kb = f32_to_bf16_bits(k_rows[i]), vb = f32_to_bf16_bits(v_rows[i]);
+				K[dst] = static_cast<uint16_t>(kb);
+				V[dst] = static_cast<uint16_t>(vb);
+				if (K16)
+				{
+					K16[dst] = bf16_to_f16_bits(kb, bad);
+					V16[dst] = bf16_to_f16_bits(vb, bad);
+				}
 			}
+			if (bad) *range = 1;
+		}
+
+		// The fp16 copies of rows pos0 .. pos0 + n_tok - 1 (mod rows) of BF16
+		// buffers written by a plain copy.
+		__global__ void shadow_rows_kernel(const uint16_t* K, const uint16_t* V, uint16_t* K16, uint16_t* V16,
+		                                   int* range, int rows, int kv_dim, int pos0, int n_tok)
+		{
+			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+			bool bad = false;
+			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
+			{
+				const int t = static_cast<int>(i / kv_dim);
+				const int c = static_cast<int>(i % kv_dim);
+				const size_t dst = static_cast<size_t>((pos0 + t) % rows) * kv_dim + c;
+				K16[dst] = bf16_to_f16_bits(K[dst], bad);
+				V16[dst] = bf16_to_f16_bits(V[dst], bad);
+			}
+			if (bad) *range = 1;
 		}
 
 		__global__ void append_f32_kernel(float* K, float* V, const float* k_rows, const float* v_rows, int rows,
@@ -118,12 +148,13 @@ namespace nnchip
 	}
 
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
-	                       int n_tok, bool bf16, hipStream_t stream)
+	                       int n_tok, bool bf16, hipStream_t stream, void* K16, void* V16, int* range)
 	{
 		const size_t n = static_cast<size_t>(n_tok) * kv_dim;
 		if (bf16)
-			append_bf16_kernel<<<grid_for(n, 256), 256, 0, stream>>>(static_cast<uint16_t*>(K), static_cast<uint16_t*>(V),
-			                                                          k_rows, v_rows, rows, kv_dim, pos0, n_tok);
+			append_bf16_kernel<<<grid_for(n, 256), 256, 0, stream>>>(
+				static_cast<uint16_t*>(K), static_cast<uint16_t*>(V), k_rows, v_rows, rows, kv_dim, pos0, n_tok,
+				static_cast<uint16_t*>(K16), static_cast<uint16_t*>(V16), range);
 		else
 			append_f32_kernel<<<grid_for(n, 256), 256, 0, stream>>>(static_cast<float*>(K), static_cast<float*>(V), k_rows,
 			                                                         v_rows, rows, kv_dim, pos0, n_tok);
@@ -139,6 +170,16 @@ namespace nnchip
 		}
 		else
 			fill_normal_kernel<<<grid_for(n, 256), 256, 0, stream>>>(dst, n, seed, bf16);
+		return true;
+	}
+
+	bool launch_shadow_rows(const void* K, const void* V, void* K16, void* V16, int* range, int rows, int kv_dim,
+	                        int pos0, int n_tok, hipStream_t stream)
+	{
+		const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+		shadow_rows_kernel<<<grid_for(n, 256), 256, 0, stream>>>(
+			static_cast<const uint16_t*>(K), static_cast<const uint16_t*>(V), static_cast<uint16_t*>(K16),
+			static_cast<uint16_t*>(V16), range, rows, kv_dim, pos0, n_tok);
 		return true;
 	}
 

@@ -286,6 +286,19 @@ namespace nnchip
 							static_cast<float*>(base)[off + i] = xr[j];
 					}
 				}
+				if (p.bf16 && p.K16)
+				{
+					// The fp16 shadow of the same row (from its BF16 value).
+					uint16_t* sh = static_cast<uint16_t*>(kind == 1 ? p.K16 : p.V16) + off;
+					bool bad = false;
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+					{
+						const int i = pos(j);
+						if (i < hd) sh[i] = bf16_to_f16_bits(f32_to_bf16_bits(xr[j]), bad);
+					}
+					if (bad) *p.range = 1;
+				}
 			}
 		}
 	}

@@ -60,6 +60,11 @@ namespace
 	{
 		void* k = nullptr;
 		void* v = nullptr;
+		// BF16 caches: fp16 copies of k and v for the prefill kernel, kept by
+		// every append (its MFMAs then take Q in fp16 and need no conversion
+		// of V); null when disabled (NNC_HIP_F16_SHADOW=0).
+		void* k16 = nullptr;
+		void* v16 = nullptr;
 		int32_t rows = 0;
 		int32_t kv_dim = 0;
 	};
@@ -79,6 +84,14 @@ namespace
 	// Batches up to this size run through the split-K kernel on each token's
 	// own split grid, so every token gets the bits a one-token call gives it.
 	constexpr int32_t kSessionBatch = 16;
+
+	// NNC_HIP_F16_SHADOW=0 keeps no fp16 copy of BF16 caches (half the device
+	// memory; the prefill kernel then converts V and splits Q on the fly).
+	bool f16_shadow_enabled()
+	{
+		const char* e = std::getenv("NNC_HIP_F16_SHADOW");
+		return !(e && e[0] == '0');
+	}
 }
 
 struct nnc_hip_kv
@@ -94,6 +107,7 @@ struct nnc_hip_kv
 	dev_scratch out;
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
+	int* range = nullptr; // per buffer: nonzero once a value outside fp16's range was appended (device)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 };
@@ -106,9 +120,10 @@ namespace
 		if (kv->stream) (void)hipStreamSynchronize(kv->stream);
 		for (auto& b : kv->bufs)
 		{
-			if (b.k) (void)hipFree(b.k);
-			if (b.v) (void)hipFree(b.v);
+			for (void* ptr : {b.k, b.v, b.k16, b.v16})
+				if (ptr) (void)hipFree(ptr);
 		}
+		if (kv->range) (void)hipFree(kv->range);
 		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
@@ -169,6 +184,12 @@ namespace
 			                           n * row_bytes, kind, kv->stream),
 			            "K/V append");
 			done += n;
+		}
+		if (b.k16)
+		{
+			nnchip::launch_shadow_rows(b.k, b.v, b.k16, b.v16, kv->range + buf, b.rows, b.kv_dim, pos0, n_tok,
+			                           kv->stream);
+			NNC_HIP_TRY(hipGetLastError(), "K/V append");
 		}
 		return NNC_OK;
 	}
@@ -306,6 +327,9 @@ namespace
 			p.gate = gate;
 			p.K = b.k;
 			p.V = b.v;
+			p.K16 = b.k16;
+			p.V16 = b.v16;
+			p.range = b.k16 ? kv->range + buf : nullptr;
 			p.rows = b.rows;
 			p.kv_dim = b.kv_dim;
 			p.n_head = n_head;
@@ -406,7 +430,14 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 	if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking);
 	if (e != hipSuccess) return bail(hip_fail(e, "device setup"));
 	const size_t esize = bf16 ? 2 : 4;
+	const bool shadow = bf16 && f16_shadow_enabled();
 	kv->bufs.resize(static_cast<size_t>(n_buf));
+	if (shadow)
+	{
+		e = hipMalloc(&kv->range, sizeof(int) * static_cast<size_t>(n_buf));
+		if (e == hipSuccess) e = hipMemsetAsync(kv->range, 0, sizeof(int) * static_cast<size_t>(n_buf), kv->stream);
+		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
+	}
 	for (int32_t i = 0; i < n_buf; ++i)
 	{
 		kv_buffer& b = kv->bufs[i];
@@ -417,6 +448,14 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 		if (e == hipSuccess) e = hipMalloc(&b.v, n);
 		if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, n, kv->stream);
 		if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, n, kv->stream);
+		if (shadow)
+		{
+			if (e == hipSuccess) e = hipMalloc(&b.k16, n);
+			if (e == hipSuccess) e = hipMalloc(&b.v16, n);
+			if (e == hipSuccess) e = hipMemsetAsync(b.k16, 0, n, kv->stream);
+			if (e == hipSuccess) e = hipMemsetAsync(b.v16, 0, n, kv->stream);
+			kv->bytes += 2 * n;
+		}
 		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 		kv->bytes += 2 * n;
 	}
@@ -461,7 +500,8 @@ nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos
 {
 	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
 	const kv_buffer& b = kv->bufs[buf];
-	nnchip::launch_append_f32(b.k, b.v, k_rows, v_rows, b.rows, b.kv_dim, pos0, n_tok, kv->bf16, kv->stream);
+	nnchip::launch_append_f32(b.k, b.v, k_rows, v_rows, b.rows, b.kv_dim, pos0, n_tok, kv->bf16, kv->stream, b.k16,
+	                          b.v16, b.k16 ? kv->range + buf : nullptr);
 	NNC_HIP_TRY(hipGetLastError(), "K/V append");
 	return NNC_OK;
 }
@@ -494,6 +534,9 @@ nnc_status nnc_hip_kv_prep_append_device(nnc_hip_kv* kv, int32_t buf, int32_t po
 	p.v = v;
 	p.K = b.k;
 	p.V = b.v;
+	p.K16 = b.k16;
+	p.V16 = b.v16;
+	p.range = b.k16 ? kv->range + buf : nullptr;
 	p.q_gamma = pr.q_gamma;
 	p.k_gamma = pr.k_gamma;
 	p.freq_factors = pr.freq_factors;

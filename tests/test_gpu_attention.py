@@ -180,6 +180,43 @@ def test_prefill_odd_batches(orc):
         assert errors(got, want)[0] <= 5e-3, w
 
 
+def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
+    """BF16 caches keep an fp16 copy for the prefill kernel (fp16 Q and K, no
+    V conversion). A value past fp16's range in the cache, or in a work-group's
+    Q, sends the prefill through the bf16 path; without the copy
+    (NNC_HIP_F16_SHADOW=0) it always runs there. Every variant stays within the
+    BF16 bound of the oracle."""
+    cfg = synth.CONFIGS["D"]
+    n_seq, n_tok = 1024, 64
+    pos0 = n_seq - n_tok
+    K, V = synth.cache_buffer(cfg, 0, n_seq, n_seq)
+    q = synth.qk_rows(cfg, 0, 0, np.arange(pos0, n_seq), cfg.n_head)
+    kw = dict(n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+
+    def run(K, V, q, label):
+        say(f"case prefill {label}")
+        with nh.KVCache([n_seq], [cfg.kv_dim]) as kv:
+            kv.append(0, 0, K, V)
+            got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+        want = orc.attend_layer(q, K, V, kv_bf16=True, rows=n_seq, pos0=pos0, n_seq=n_seq, **kw)
+        ea = errors(got, want)[0]
+        say(f"  max-abs {ea:.3e}")
+        assert ea <= cfg.tol, label
+        return got
+
+    base = run(K, V, q, "fp16 shadow")
+    monkeypatch.setenv("NNC_HIP_F16_SHADOW", "0")
+    plain = run(K, V, q, "no shadow (bf16 K/V, Q hi + lo)")
+    monkeypatch.delenv("NNC_HIP_F16_SHADOW")
+    assert not np.array_equal(base, plain)  # the two paths round differently
+    K2 = K.copy()
+    K2[100, 5] = nh.bf16_round(np.array([1.0e5], np.float32))[0]  # past fp16's range
+    run(K2, V, q, "cache value past fp16 range")
+    q2 = q.copy()
+    q2[3, 7] = 1.0e6  # q * scale * log2(e) past fp16's range in one work-group
+    run(K, V, q2, "Q value past fp16 range")
+
+
 def test_f32_batch_uses_exact_path(orc):
     """F32 K/V batches run the split-K kernel per token: the F32 bound holds."""
     cfg = synth.CONFIGS["A"]
