@@ -68,10 +68,10 @@ namespace nnchip
 		// merge ends with, so a token gets the same bits either way.
 		template <int HD, int G, int C, int W>
 		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[C][HD + 2],
-		                                                int tok0, int n_cols, int split, int kvh)
+		                                                int tok0, int n_cols, int split)
 		{
 			constexpr int PW = HD + 2, kWaves = W, kThreads = 64 * W;
-			const int n_kv = gridDim.y;
+			const int kvh = blockIdx.y, n_kv = gridDim.y;
 			const bool single = p.n_split == 1;
 			for (int idx = threadIdx.x; idx < n_cols * PW; idx += kThreads)
 			{
@@ -132,8 +132,8 @@ namespace nnchip
 		{
 			constexpr int PW = HD + 2, E = HD / 64, KB = 32, MS = kDecodeMaxSplits / 64;
 			typedef float fE __attribute__((ext_vector_type(E)));
+			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
 			const int n_kv = gridDim.x / G;
-			const int kvh = blockIdx.x % n_kv, h = blockIdx.x / n_kv, tok = blockIdx.y;
 			const int lane = threadIdx.x;
 			const int ns = p.n_split;
 			const size_t sstride = static_cast<size_t>(G) * PW;
@@ -470,7 +470,7 @@ namespace nnchip
 			}
 			__syncthreads();
 
-			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split, kvh);
+			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split);
 		}
 
 		// Chunk sizes of the BF16 kernel: CH keys per wavefront chunk (a chunk's
@@ -544,13 +544,8 @@ namespace nnchip
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
 			const int col = lane & 15;
 			const int grp = lane >> 4;
-			// Work-groups are dealt to the XCDs round-robin by linear index; with
-			// the KV head as the fastest index a head's splits share one XCD,
-			// whose L2 then holds their partials for the merge (which maps its
-			// work-groups the same way).
-			const int lin = blockIdx.x + gridDim.x * blockIdx.y;
-			const int kvh = lin % gridDim.y;
-			const int split = lin / gridDim.y;
+			const int kvh = blockIdx.y;
+			const int split = blockIdx.x;
 			const int tok0 = blockIdx.z * T;
 			const int n_tt = min(T, p.n_tok - tok0); // tokens of this work-group
 			const int tt = col / G; // this lane's column: token tok0 + tt, head col % G
@@ -759,7 +754,7 @@ namespace nnchip
 				}
 			}
 			__syncthreads();
-			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split, kvh);
+			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split);
 		}
 
 		// Keys per wavefront chunk of the BF16 kernel (4 wavefronts, one per
