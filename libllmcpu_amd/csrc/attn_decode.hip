@@ -68,10 +68,10 @@ namespace nnchip
 		// merge ends with, so a token gets the same bits either way.
 		template <int HD, int G, int C, int W>
 		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[C][HD + 2],
-		                                                int tok0, int n_cols, int split)
+		                                                int tok0, int n_cols, int split, int kvh)
 		{
 			constexpr int PW = HD + 2, kWaves = W, kThreads = 64 * W;
-			const int kvh = blockIdx.y, n_kv = gridDim.y;
+			const int n_kv = gridDim.y;
 			const bool single = p.n_split == 1;
 			for (int idx = threadIdx.x; idx < n_cols * PW; idx += kThreads)
 			{
@@ -470,7 +470,7 @@ namespace nnchip
 			}
 			__syncthreads();
 
-			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split);
+			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split, kvh);
 		}
 
 		// Chunk sizes of the BF16 kernel: CH keys per wavefront chunk (a chunk's
@@ -544,9 +544,23 @@ namespace nnchip
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
 			const int col = lane & 15;
 			const int grp = lane >> 4;
-			const int kvh = blockIdx.y;
-			const int split = blockIdx.x;
-			const int tok0 = blockIdx.z * T;
+			// A batch's token groups of one (split, KV head) pair go to one XCD
+			// in consecutive slots (work-groups are dealt to the XCDs round-robin
+			// by linear index), so they stream the same K/V rows through one L2.
+			int kvh = blockIdx.y, split = blockIdx.x, zg = blockIdx.z;
+			{
+				const int nxy = gridDim.x * gridDim.y, nz = gridDim.z;
+				const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+				if (nz > 1 && nxy % 8 == 0)
+				{
+					const int xcd = lin % 8, slot = lin / 8;
+					zg = slot % nz;
+					const int pair = 8 * (slot / nz) + xcd;
+					split = pair % gridDim.x;
+					kvh = pair / gridDim.x;
+				}
+			}
+			const int tok0 = zg * T;
 			const int n_tt = min(T, p.n_tok - tok0); // tokens of this work-group
 			const int tt = col / G; // this lane's column: token tok0 + tt, head col % G
 
@@ -754,7 +768,7 @@ namespace nnchip
 				}
 			}
 			__syncthreads();
-			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split);
+			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split, kvh);
 		}
 
 		// Keys per wavefront chunk of the BF16 kernel (4 wavefronts, one per
