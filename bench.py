@@ -426,7 +426,7 @@ def main() -> int:
                                  "avg_launch_us": round(pre_launch_us, 3)}},
         "session_batch": {"what": f"one {SESSION_BATCH}-token forward pass of an nnc session (its batch size, "
                                   f"MTP verification included) ending at position {CTX - 1}, 36 layers; each token "
-                                  "bit-identical to its one-token call",
+                                  "bit-identical to its one-token call (decode_bf16_multi_kernel)",
                           "ms_per_step": round(b_ms / 10, 4), "us_per_layer": round(b_us, 3),
                           "kv_gbs": round(b_bytes / (b_us * 1e-6) / 1e9, 1)},
         "prep": {"what": "per-head RMSNorm of Q and K, NEOX RoPE (base 1e6), BF16 K/V append, device memory",

@@ -771,6 +771,264 @@ namespace nnchip
 			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split, kvh);
 		}
 
+		// The BF16 kernel for a session batch: NTL tiles of 16 MFMA columns,
+		// 16 * NTL / G tokens per work-group, so a 16-token batch streams each
+		// K and V row once. Q (hi and lo) sits in LDS; per chunk the scores of
+		// every tile come from the same K registers and the V^T tile is read
+		// back once per tile. Each column goes through exactly the operations
+		// of decode_bf16_kernel (same products, same order), so a token gets
+		// the bits of its one-token call here too.
+		template <int HD, int G, int W, int CHK, int NTL>
+		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_multi_kernel(
+			const decode_params p)
+		{
+			using S = bf16_shape<HD, CHK>;
+			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
+			              NV = S::NV, VPITCH = S::VPITCH;
+			constexpr int PW = HD + 2, kWaves = W, T = 16 * NTL / G;
+			static_assert(NTL >= 2 && (16 * NTL) % G == 0, "tiles per work-group");
+
+			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
+			__shared__ float s_wpart[W][16][PW];
+			__shared__ __attribute__((aligned(16))) u32x4 s_q[NTL][KK][2][64]; // B operands, hi and lo
+
+			const int lane = threadIdx.x & 63;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+			const int col = lane & 15;
+			const int grp = lane >> 4;
+			const int kvh = blockIdx.y;
+			const int split = blockIdx.x;
+			const int tok0 = blockIdx.z * T;
+			const int n_tt = min(T, p.n_tok - tok0);
+
+			const int sbase = p.split_base + split * p.split_keys;
+			const int send = sbase + p.split_keys - 1;
+			int col_s0[NTL], col_s1[NTL];
+#pragma unroll
+			for (int tl = 0; tl < NTL; ++tl)
+			{
+				const int tt = (16 * tl + col) / G;
+				int first, last;
+				attn_span(p.causal, p.window, p.pos0 + tok0 + tt, p.n_seq, first, last);
+				col_s0[tl] = tt < n_tt ? max(first, sbase) : 1;
+				col_s1[tl] = tt < n_tt ? min(last, send) : 0;
+			}
+			int f0, l0, fL, lL;
+			attn_span(p.causal, p.window, p.pos0 + tok0, p.n_seq, f0, l0);
+			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
+			const int s0 = max(f0, sbase);
+			const int s1 = min(lL, send);
+			const size_t head_off = static_cast<size_t>(kvh) * HD;
+			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
+			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
+			uint16_t* vt = s_v[wave];
+
+			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
+			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
+			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
+			const bool has_chunk = c_wave <= c_last;
+			const int n_wchunks = has_chunk ? (c_last - c_wave) / kWaves + 1 : 0;
+			const int c_wlast = c_wave + (n_wchunks - 1) * kWaves;
+
+			u32x4 kreg[NT][KK];
+			u32x4 vreg[NV];
+			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
+			{
+				cbase = sbase + c * CH;
+				clo = max(s0, cbase);
+				chi = min(s1, cbase + CH - 1);
+				rb = clo % p.rows;
+			};
+			auto load_k = [&](int c) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+				{
+					const int k = min(max(cbase + 16 * t + col, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					const uint16_t* kp = Kg + row * p.kv_dim + 8 * grp;
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk) kreg[t][kk] = *reinterpret_cast<const u32x4*>(kp + 32 * kk);
+				}
+			};
+			auto load_v = [&](int c) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+				{
+					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
+					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
+					vreg[j] = *reinterpret_cast<const u32x4*>(Vg + row * p.kv_dim + 8 * (lane % LPK));
+				}
+			};
+
+			if (has_chunk)
+			{
+				load_k(c_wave);
+				load_v(c_wave);
+			}
+
+			// Q^T of every tile into LDS as the B operands, scaled into log2
+			// units and split into bf16 hi + lo (entry (tl, kk, l) is lane l's
+			// 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
+			for (int i = threadIdx.x; i < NTL * KK * 64; i += 64 * W)
+			{
+				const int l = i & 63, kk = (i >> 6) % KK, tl = (i >> 6) / KK;
+				const int gc = 16 * tl + (l & 15), tt = gc / G;
+				float x[8];
+				if (tt < n_tt)
+				{
+					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + kvh * G + gc % G) * HD + 32 * kk +
+					                  8 * (l >> 4);
+					const float4 a = *reinterpret_cast<const float4*>(qp);
+					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
+					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+					x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+					for (int j = 0; j < 8; ++j) x[j] *= p.qscale;
+				}
+				else
+				{
+#pragma unroll
+					for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+				}
+				bf16x8 hi, lo;
+				split_bf16x8(x, hi, lo);
+				s_q[tl][kk][0][l] = __builtin_bit_cast(u32x4, hi);
+				s_q[tl][kk][1][l] = __builtin_bit_cast(u32x4, lo);
+			}
+			__syncthreads();
+
+			float m_run[NTL], l_run[NTL];
+			f32x4 acc_o[NTL][DB];
+#pragma unroll
+			for (int tl = 0; tl < NTL; ++tl)
+			{
+				m_run[tl] = -INFINITY;
+				l_run[tl] = 0.0f;
+#pragma unroll
+				for (int db = 0; db < DB; ++db) acc_o[tl][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+			}
+
+			auto chunk = [&](int cw) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(cw, cbase, clo, chi, rb);
+
+				f32x4 sc[NTL][NT];
+#pragma unroll
+				for (int tl = 0; tl < NTL; ++tl)
+#pragma unroll
+					for (int t = 0; t < NT; ++t) sc[tl][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+				for (int tl = 0; tl < NTL; ++tl)
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk)
+					{
+						const bf16x8 qh = __builtin_bit_cast(bf16x8, s_q[tl][kk][0][lane]);
+						const bf16x8 ql = __builtin_bit_cast(bf16x8, s_q[tl][kk][1][lane]);
+#pragma unroll
+						for (int t = 0; t < NT; ++t)
+						{
+							const bf16x8 a = as_bf16x8(kreg[t][kk]);
+							sc[tl][t] = mfma16x16x32(a, qh, sc[tl][t]);
+							sc[tl][t] = mfma16x16x32(a, ql, sc[tl][t]);
+						}
+					}
+				load_k(cw + kWaves);
+
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
+				load_v(cw + kWaves);
+				wave_sync();
+
+#pragma unroll
+				for (int tl = 0; tl < NTL; ++tl)
+				{
+					float m_loc = -INFINITY;
+#pragma unroll
+					for (int t = 0; t < NT; ++t)
+#pragma unroll
+						for (int i = 0; i < 4; ++i)
+						{
+							const int k = cbase + 16 * t + 4 * grp + i;
+							const float v = (k >= col_s0[tl] && k <= col_s1[tl]) ? sc[tl][t][i] : -INFINITY;
+							sc[tl][t][i] = v;
+							m_loc = fmaxf(m_loc, v);
+						}
+					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
+					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
+					const float m_new = fmaxf(m_run[tl], m_loc);
+					const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+					const float alpha = fast_exp2(m_run[tl] - m_use);
+					m_run[tl] = m_new;
+					float lsum = 0.0f;
+					bf16x8 phi[NC], plo[NC];
+#pragma unroll
+					for (int c = 0; c < NC; ++c)
+					{
+						float w[8];
+#pragma unroll
+						for (int i = 0; i < 4; ++i)
+						{
+							w[i] = fast_exp2(sc[tl][2 * c][i] - m_use);
+							w[4 + i] = fast_exp2(sc[tl][2 * c + 1][i] - m_use);
+						}
+#pragma unroll
+						for (int i = 0; i < 8; ++i) lsum += w[i];
+						split_bf16x8(w, phi[c], plo[c]);
+					}
+					l_run[tl] = l_run[tl] * alpha + lsum;
+#pragma unroll
+					for (int db = 0; db < DB; ++db) acc_o[tl][db] *= alpha;
+#pragma unroll
+					for (int c = 0; c < NC; ++c)
+#pragma unroll
+						for (int db = 0; db < DB; ++db)
+						{
+							const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
+							const u32x2 lo = vt_read(r0);
+							const u32x2 hi = vt_read(r0 + 16 * VPITCH);
+							const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+							acc_o[tl][db] = mfma16x16x32(a, phi[c], acc_o[tl][db]);
+							acc_o[tl][db] = mfma16x16x32(a, plo[c], acc_o[tl][db]);
+						}
+				}
+				wave_sync(); // V is read before the next chunk overwrites it
+			};
+			for (int i = 0; i < n_wchunks; ++i, c_wave += kWaves) chunk(c_wave);
+
+			// One tile at a time through the wavefront merge.
+#pragma unroll
+			for (int tl = 0; tl < NTL; ++tl)
+			{
+				float lr = l_run[tl];
+				lr += __shfl_xor(lr, 16);
+				lr += __shfl_xor(lr, 32);
+				const int n_cols = min(16, n_tt * G - 16 * tl); // uniform
+				if (col < n_cols)
+				{
+#pragma unroll
+					for (int db = 0; db < DB; ++db)
+#pragma unroll
+						for (int i = 0; i < 4; ++i) s_wpart[wave][col][16 * db + 4 * grp + i] = acc_o[tl][db][i];
+					if (grp == 0)
+					{
+						s_wpart[wave][col][HD] = m_run[tl];
+						s_wpart[wave][col][HD + 1] = lr;
+					}
+				}
+				__syncthreads();
+				if (n_cols > 0) write_wg_result<HD, G, 16, W>(p, s_wpart, tok0 + 16 * tl / G, n_cols, split, kvh);
+				__syncthreads(); // the partials are read before the next tile overwrites them
+			}
+		}
+
 		// Keys per wavefront chunk of the BF16 kernel (4 wavefronts, one per
 		// SIMD). Measured at 32k keys: 8 wavefronts of 32-key chunks (two per
 		// SIMD) run 2% slower.
@@ -799,12 +1057,25 @@ namespace nnchip
 				// One token: the one-token instance (less LDS for partials);
 				// batches: 16 / G tokens per work-group. Both compute a token's
 				// column with the same operations.
-				constexpr int T = 16 / G;
+				constexpr int T = 16 / G, TM = 64 / G; // tokens per work-group: one tile, four tiles
 				if (n_tok == 1)
 					decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1><<<grid, 256, 0, stream>>>(p);
 				else
-					decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), T>
-						<<<dim3(p.n_split, n_kv, (n_tok + T - 1) / T), 256, 0, stream>>>(p);
+				{
+					bool multi = false;
+					if constexpr (HD <= 128) // (at head_dim 256 four tiles do not fit the registers)
+					{
+						if (n_tok > T)
+						{
+							multi = true;
+							decode_bf16_multi_kernel<HD, G, 4, bf16_chunk(HD), 4>
+								<<<dim3(p.n_split, n_kv, (n_tok + TM - 1) / TM), 256, 0, stream>>>(p);
+						}
+					}
+					if (!multi)
+						decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), T>
+							<<<dim3(p.n_split, n_kv, (n_tok + T - 1) / T), 256, 0, stream>>>(p);
+				}
 			}
 			else if (waves == 8)
 				decode_kernel<HD, G, BF16, 8><<<grid, 512, 0, stream>>>(p);
