@@ -125,6 +125,26 @@ namespace nnchip
 			__builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)lds, 16, voffset, 0, 0, 0);
 		}
 
+		// DMA j of a tile: 16 bytes per lane from buffer offset voffset into
+		// the tile at byte 1024 j + 16 l. The instruction offset (1024 (j % 4))
+		// is added to both the buffer offset (and its range check) and the LDS
+		// address, so DMAs j = 4 g .. 4 g + 3 share the LDS base tile + 4096 g:
+		// one M0 value for four DMAs. voffset >= 1024 j always holds for the
+		// tiles here (row r of DMA j starts at r * row_bytes >= 1024 j).
+		__device__ __forceinline__ void load_lds16_grouped(__amdgpu_buffer_rsrc_t rsrc, uint16_t* tile, int j,
+		                                                   uint32_t voffset)
+		{
+			typedef __attribute__((address_space(3))) void* lds_ptr;
+			const lds_ptr base = (lds_ptr)(reinterpret_cast<char*>(tile) + 4096 * (j >> 2));
+			switch (j & 3) // j is a constant after unrolling; the offset must be an immediate
+			{
+			case 0: __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, base, 16, voffset, 0, 0, 0); break;
+			case 1: __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, base, 16, voffset - 1024u, 0, 1024, 0); break;
+			case 2: __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, base, 16, voffset - 2048u, 0, 2048, 0); break;
+			default: __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, base, 16, voffset - 3072u, 0, 3072, 0); break;
+			}
+		}
+
 		// Waits until every LDS access this wavefront issued has completed
 		// (s_waitcnt lgkmcnt(0); the vector-memory and export counters at
 		// their maximum, i.e. not waited on: gfx9 encoding vmcnt[3:0] = 0xf,
@@ -231,16 +251,26 @@ namespace nnchip
 				seg_last = second ? kmax : wrap_key - 1;
 				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + wave * kWK;
 			};
+			// In bytes from the buffer's start: the wavefront's block at step i
+			// is at seg_off + i * step_bytes (seg_off per segment: the block of
+			// step 0, or of step n1 moved back n1 steps), and the segment ends
+			// at seg_end (its last row's head slice included). Everything stays
+			// below 2^32 since a buffer is under 2 GiB.
+			const uint32_t step_bytes = static_cast<uint32_t>(kStep) * row_bytes;
+			const uint32_t seg1_off = static_cast<uint32_t>(rb0 + wave * kWK) * row_bytes;
+			const uint32_t seg2_off = static_cast<uint32_t>(wave * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
+			const uint32_t seg1_end = static_cast<uint32_t>(rb0 + len1 - 1) * row_bytes + HD * 2;
+			const uint32_t seg2_end = static_cast<uint32_t>(kmax - wrap_key) * row_bytes + HD * 2; // used when len2 > 0
 			auto step_rsrc = [&](int i, const char* base) __attribute__((always_inline))
 			{
-				int seg_last;
-				const int kw0 = step_key(i, seg_last);
 				const bool second = i >= n1;
-				const int r = second ? kw0 - wrap_key : rb0 + (kw0 - kmin); // the block's first row
-				const int r_last = second ? kmax - wrap_key : rb0 + len1 - 1; // the segment's last row
-				const int64_t n = static_cast<int64_t>(r_last - r) * row_bytes + HD * 2;
-				return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + static_cast<int64_t>(r) * row_bytes), 0,
-				                                         static_cast<int>(n > 0 ? n : 0), kBufferFlags);
+				const uint32_t off = (second ? seg2_off : seg1_off) + static_cast<uint32_t>(i) * step_bytes;
+				const uint32_t end = second ? seg2_end : seg1_end;
+				// (the clamp becomes a VALU saturating subtract: readfirstlane keeps
+				// the descriptor in SGPRs)
+				const uint32_t n = __builtin_amdgcn_readfirstlane(end > off ? end - off : 0u);
+				return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + off), 0, static_cast<int>(n),
+				                                         kBufferFlags);
 			};
 
 			// Tile layout: DMA j fills tile rows j KPL .. + KPL, lane l the 16
@@ -253,13 +283,22 @@ namespace nnchip
 			{
 				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
 				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
+				// Each group of four DMAs shares one LDS base (the instruction
+				// offset moves the LDS and buffer addresses alike), so the K tile,
+				// then the V tile, needs one LDS base per 4 KiB.
 #pragma unroll
 				for (int jj = 0; jj < NV; ++jj)
 				{
 					const int row = jj * KPL + t_row;
 					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					load_lds16(rk, kt + jj * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
-					load_lds16(rv, vt + jj * KPL * HD, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
+					load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
+				}
+#pragma unroll
+				for (int jj = 0; jj < NV; ++jj)
+				{
+					const int row = jj * KPL + t_row;
+					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
+					load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
 				}
 			};
 			// The first step's tiles go out before Q is read, so the latencies overlap.
