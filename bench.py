@@ -139,6 +139,7 @@ CALIBRATE_MIB = 1024
 
 # Qwen3-4B's weight gemvs of one layer (rows, cols): q, k, v, o, gate, up, down.
 GEMV_LAYER = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)]
+LM_HEAD = (151936, 2560)  # Qwen3-4B vocabulary x n_embd
 GEMV_WORKING_SET = 640 << 20  # bytes of distinct weights per format, past the 256 MB Infinity Cache
 
 
@@ -189,6 +190,24 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
                                   "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         for d in bufs:
             hip_rt.free(d)
+    # Greedy decode's lm_head: the argmax of the BF16 projection onto the
+    # vocabulary (Qwen3-4B ties it to the token embeddings), 778 MB per call;
+    # the call waits for its result, so the time includes the index's copy
+    # back and the host's return.
+    rows, cols = LM_HEAD
+    w = hip_rt.malloc(2 * rows * cols)
+    nh.fill_normal(w, rows * cols, 7777, 0, True, stream)
+    kv.sync()
+    kv.gemv_argmax_device(w, x, rows=rows, cols=cols)
+    n_calls = 10
+    _, wall_ms = timed(lambda: kv.gemv_argmax_device(w, x, rows=rows, cols=cols), n_calls)
+    us = wall_ms * 1e3 / n_calls
+    nbytes = 2 * rows * cols + 4 * cols
+    res["lm_head_argmax"] = {"rows": rows, "cols": cols, "us_per_call": round(us, 2), "bytes": nbytes,
+                             "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                             "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             "kernels": "gemv_vec_kernel<bf16, argmax> + gemv_argmax_final_kernel"}
+    hip_rt.free(w)
     hip_rt.free(x)
     hip_rt.free(y)
     return {"what": "Qwen3-4B layer weight gemvs (q, k, v, o, gate, up, down) per weight layout; n1 = one "

@@ -227,6 +227,18 @@ nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* 
                              const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
                              size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch);
 
+/* Greedy decode's lm_head projection: the row of the largest element of
+ * y = W x for a BF16 W [rows][cols] and one vector x, without writing y
+ * (reference nn_ops.h:98-113, nn_ops.cpp:1055-1150 nnc_gemv_bf16w_argmax_f32x;
+ * caller model_argmax, model.cpp:2181-2190). *index (host memory) receives
+ * the smallest such row; NaN and -inf are never chosen, and 0 is returned
+ * when no element is above -inf (the reference's threaded and 4-row paths);
+ * -1 when rows or cols is 0. W and x are device memory; the call waits for
+ * the cache's stream. Errors as nnc_hip_gemv_bf16; cols must also fit the
+ * one-vector kernel (at most 15 872). */
+nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* x, uint32_t rows, uint32_t cols,
+                                    int32_t* index);
+
 /* Waits for all work queued on the cache's stream. */
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv);
 

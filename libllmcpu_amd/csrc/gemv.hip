@@ -303,9 +303,20 @@ namespace nnchip
 			float sc, bi; // the block's scale (Q8_0, Q4_S) and bias (Q4_S)
 		};
 
-		template <int F>
+		// The argmax order: (v, r) beats (bv, br) when v is above -inf (NaN never
+		// is) and larger, or equal with a smaller row; br = -1 is "none". The
+		// smallest row of the largest value wins whatever order rows are met in.
+		__device__ __forceinline__ bool argmax_better(float v, int r, float bv, int br)
+		{
+			return r >= 0 && v > -INFINITY && (br < 0 || v > bv || (v == bv && r < br));
+		}
+
+		// ARGMAX (BF16 only): no y; each wavefront keeps its best row and the
+		// work-group writes its best (value, row) to p.best[blockIdx.x].
+		template <int F, bool ARGMAX = false>
 		__global__ __launch_bounds__(256) void gemv_vec_kernel(const gemv_params p)
 		{
+			static_assert(!ARGMAX || F == kGemvBf16, "argmax of a BF16 gemv only");
 			using V = vec_shape<F>;
 			constexpr int CPL = V::CPL, CW = V::CW, NA = kVecAhead;
 			extern __shared__ __attribute__((aligned(16))) float s_x[]; // x, then (Q4_S) its block sums
@@ -413,31 +424,40 @@ namespace nnchip
 #pragma unroll
 			for (int j = 0; j < NA; ++j) ring[j] = load(j);
 
-			for (int i = 4 * threadIdx.x; i < p.cols; i += 1024)
-				*reinterpret_cast<float4*>(s_x + i) = *reinterpret_cast<const float4*>(p.x + i);
-			if constexpr (F == kGemvQ4S)
+			// x into LDS, thread t taking elements 4 t .. 4 t + 3 of each 1024.
+			// Q4_S without the caller's block sums: the eight threads of a block
+			// hold its quarters q = t % 8, and three lane exchanges add them in
+			// the reference's order (reference nn_ops.cpp:1305-1316 under its
+			// -ffast-math build: l_j = (x_j + x_8+j) + (x_16+j + x_24+j), then
+			// ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7))), so x is read
+			// once.
+			const bool own_sums = F == kGemvQ4S && p.xsum == nullptr; // uniform
+			for (int i0 = 0; i0 < p.cols; i0 += 1024)
 			{
-				// Block sums: the caller's, or in the reference's order (reference
-				// nn_ops.cpp:1305-1316 under its -ffast-math build).
-				for (int b = threadIdx.x; b < nb_all; b += 256)
+				const int i = i0 + 4 * threadIdx.x;
+				const bool ok = i < p.cols; // a block's eight threads agree (cols % 32 == 0)
+				const float4 v = ok ? *reinterpret_cast<const float4*>(p.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				if (ok) *reinterpret_cast<float4*>(s_x + i) = v;
+				if (own_sums)
 				{
-					float sum;
-					if (p.xsum)
-						sum = p.xsum[b];
-					else
+					auto add_from = [](const float4& a, int m) __attribute__((always_inline)) -> float4
 					{
-						const float* x = p.x + 32 * b;
-						float l[8];
-#pragma unroll
-						for (int j = 0; j < 8; ++j) l[j] = (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]);
-						sum = ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
-					}
-					s_x[p.cols + b] = sum;
+						return make_float4(a.x + __shfl_xor(a.x, m), a.y + __shfl_xor(a.y, m), a.z + __shfl_xor(a.z, m),
+						                   a.w + __shfl_xor(a.w, m));
+					};
+					const float4 a = add_from(v, 2); // q = 0: x_j + x_8+j; q = 4: x_16+j + x_24+j (j < 4)
+					const float4 l = add_from(a, 4); // q = 0: l_0..3; q = 1: l_4..7
+					const float4 u = add_from(l, 1); // q = 0: l_k + l_k+4
+					if (ok && (threadIdx.x & 7) == 0) s_x[p.cols + i / 32] = (u.x + u.y) + (u.z + u.w);
 				}
 			}
+			if (F == kGemvQ4S && !own_sums)
+				for (int b = threadIdx.x; b < nb_all; b += 256) s_x[p.cols + b] = p.xsum[b];
 			__syncthreads();
 
 			float acc[2] = {0.0f, 0.0f};
+			float best_v = -INFINITY; // ARGMAX: this wavefront's best row so far (lane 0)
+			int best_r = -1;
 			for (int k0 = 0; k0 < n_items; k0 += NA)
 			{
 #pragma unroll
@@ -456,7 +476,20 @@ namespace nnchip
 						{
 							const float y0 = wave_sum_dpp(acc[0]), y1 = wave_sum_dpp(acc[1]);
 							const int r0 = pair_row(k);
-							if (lane == 0)
+							if constexpr (ARGMAX)
+							{
+								if (argmax_better(y0, r0, best_v, best_r))
+								{
+									best_v = y0;
+									best_r = r0;
+								}
+								if (r0 + 1 < p.rows && argmax_better(y1, r0 + 1, best_v, best_r))
+								{
+									best_v = y1;
+									best_r = r0 + 1;
+								}
+							}
+							else if (lane == 0)
 							{
 								p.y[r0] = y0;
 								if (r0 + 1 < p.rows) p.y[r0 + 1] = y1;
@@ -466,6 +499,67 @@ namespace nnchip
 					}
 				}
 			}
+			if constexpr (ARGMAX)
+			{
+				// The work-group's best: the four wavefronts' (lane 0's), after x
+				// in LDS, then one (value, row) pair per work-group.
+				float* s_best = s_x + p.cols;
+				if (lane == 0)
+				{
+					s_best[2 * wave] = best_v;
+					s_best[2 * wave + 1] = __int_as_float(best_r);
+				}
+				__syncthreads();
+				if (threadIdx.x == 0)
+				{
+					float bv = -INFINITY;
+					int br = -1;
+#pragma unroll
+					for (int w = 0; w < 4; ++w)
+					{
+						const float wv = s_best[2 * w];
+						const int wr = __float_as_int(s_best[2 * w + 1]);
+						if (argmax_better(wv, wr, bv, br))
+						{
+							bv = wv;
+							br = wr;
+						}
+					}
+					p.best[blockIdx.x] = make_float2(bv, __int_as_float(br));
+				}
+			}
+		}
+
+		// The argmax over the work-groups' best pairs: one work-group of 256.
+		__global__ __launch_bounds__(256) void gemv_argmax_final_kernel(const gemv_params p, int n_best)
+		{
+			__shared__ float s_v[256];
+			__shared__ int s_r[256];
+			float bv = -INFINITY;
+			int br = -1;
+			for (int i = threadIdx.x; i < n_best; i += 256)
+			{
+				const float2 b = p.best[i];
+				if (argmax_better(b.x, __float_as_int(b.y), bv, br))
+				{
+					bv = b.x;
+					br = __float_as_int(b.y);
+				}
+			}
+			s_v[threadIdx.x] = bv;
+			s_r[threadIdx.x] = br;
+			__syncthreads();
+			for (int h = 128; h > 0; h >>= 1)
+			{
+				if (threadIdx.x < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
+				                                     s_r[threadIdx.x]))
+				{
+					s_v[threadIdx.x] = s_v[threadIdx.x + h];
+					s_r[threadIdx.x] = s_r[threadIdx.x + h];
+				}
+				__syncthreads();
+			}
+			if (threadIdx.x == 0) *p.argmax = s_r[0] >= 0 ? s_r[0] : 0;
 		}
 
 		// Y[t][r] = the splits' partials summed in split order.
@@ -505,6 +599,12 @@ namespace nnchip
 		split_blocks = (nb + n_split - 1) / n_split;
 	}
 
+	int gemv_vec_groups(int rows)
+	{
+		const int n_pairs = (rows + 1) / 2;
+		return std::max(1, std::min((n_pairs + 3) / 4, 512));
+	}
+
 	bool gemv_vec_fits(int cols, int n_batch)
 	{
 		return n_batch == 1 && static_cast<size_t>(cols + cols / 32) * 4 <= kGemvLdsBudget;
@@ -515,8 +615,7 @@ namespace nnchip
 		if (gemv_vec_fits(p.cols, p.n_batch))
 		{
 			const size_t lds = static_cast<size_t>(p.cols + p.cols / 32) * 4;
-			const int n_pairs = (p.rows + 1) / 2;
-			const dim3 grid(std::max(1, std::min((n_pairs + 3) / 4, 512)));
+			const dim3 grid(gemv_vec_groups(p.rows));
 			switch (p.format)
 			{
 			case kGemvBf16: gemv_vec_kernel<kGemvBf16><<<grid, 256, lds, stream>>>(p); return true;
@@ -540,6 +639,16 @@ namespace nnchip
 			const unsigned g = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 4096));
 			gemv_reduce_kernel<<<g, 256, 0, stream>>>(p);
 		}
+		return true;
+	}
+
+	bool launch_gemv_argmax(const gemv_params& p, hipStream_t stream)
+	{
+		if (p.format != kGemvBf16 || !gemv_vec_fits(p.cols, 1)) return false;
+		const int groups = gemv_vec_groups(p.rows);
+		const size_t lds = (static_cast<size_t>(p.cols) + 8) * 4; // x, then the wavefronts' best pairs
+		gemv_vec_kernel<kGemvBf16, true><<<groups, 256, lds, stream>>>(p);
+		gemv_argmax_final_kernel<<<1, 256, 0, stream>>>(p, groups);
 		return true;
 	}
 }

@@ -128,12 +128,27 @@ namespace nnchip
 		size_t x_stride, xsum_stride, y_stride;
 		int rows, cols, n_batch;
 		int n_split, split_blocks; // K splits, and 32-column blocks per split
+		// argmax of y instead of y (BF16, one vector): each work-group's best
+		// (value, row) pair, then the row
+		float2* best; // [work-groups] (value, row as int bits; row -1 when none)
+		int* argmax; // the result
 	};
 
 	// K splits for a (rows, cols) gemv of n_batch vectors.
 	void gemv_plan(int rows, int cols, int n_batch, int& n_split, int& split_blocks);
 
 	bool launch_gemv(const gemv_params& p, hipStream_t stream);
+
+	// Work-groups of the one-vector kernel for `rows` rows (the number of
+	// best pairs launch_gemv_argmax writes), and whether a gemv of `cols`
+	// columns and n_batch vectors runs on it.
+	int gemv_vec_groups(int rows);
+	bool gemv_vec_fits(int cols, int n_batch);
+
+	// argmax_r y[r] for a BF16 gemv of one vector (p.best, p.argmax set):
+	// the smallest row of the largest value above -inf, NaN never chosen, 0
+	// when there is none. Needs gemv_vec_fits(p.cols, 1).
+	bool launch_gemv_argmax(const gemv_params& p, hipStream_t stream);
 
 	bool launch_zero(float* dst, size_t n, hipStream_t stream);
 

@@ -703,6 +703,45 @@ namespace
 	}
 }
 
+nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* x, uint32_t rows, uint32_t cols,
+                                    int32_t* index)
+{
+	if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the context (cache) is NULL");
+	if (!W || !x || !index) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL weight, input or index pointer");
+	if (rows == 0 || cols == 0)
+	{
+		*index = -1; // reference nn_ops.cpp:1058
+		return NNC_OK;
+	}
+	if (rows > 0x7fffffffu || cols > 0x7fffffffu) return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %u x %u", rows, cols);
+	if (cols % 32 != 0 || !nnchip::gemv_vec_fits(static_cast<int>(cols), 1))
+		return fail(NNC_ERR_UNSUPPORTED_MODEL, "argmax gemv with %u columns (a multiple of 32, at most 15872)", cols);
+	if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15)
+		return fail(NNC_ERR_INVALID_ARGUMENT, "weights and x must be 16-byte aligned");
+	const int groups = nnchip::gemv_vec_groups(static_cast<int>(rows));
+	const size_t best_bytes = static_cast<size_t>(groups) * sizeof(float2);
+	if (nnc_status s = reserve(kv, kv->gemv_part, best_bytes + sizeof(int32_t), "gemv scratch")) return s;
+	nnchip::gemv_params p{};
+	p.format = nnchip::kGemvBf16;
+	p.w = W;
+	p.x = x;
+	p.x_stride = cols;
+	p.rows = static_cast<int>(rows);
+	p.cols = static_cast<int>(cols);
+	p.n_batch = 1;
+	p.n_split = 1;
+	p.split_blocks = static_cast<int>(cols / 32);
+	p.best = static_cast<float2*>(kv->gemv_part.ptr);
+	p.argmax = reinterpret_cast<int*>(static_cast<char*>(kv->gemv_part.ptr) + best_bytes);
+	if (!nnchip::launch_gemv_argmax(p, kv->stream)) return fail(NNC_ERR_UNSUPPORTED_MODEL, "argmax gemv");
+	NNC_HIP_TRY(hipGetLastError(), "argmax gemv launch");
+	int32_t r = 0;
+	NNC_HIP_TRY(hipMemcpyAsync(&r, p.argmax, sizeof(r), hipMemcpyDeviceToHost, kv->stream), "argmax download");
+	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "argmax gemv");
+	*index = r;
+	return NNC_OK;
+}
+
 nnc_status nnc_hip_gemv_bf16(nnc_hip_kv* kv, const void* W, const float* X, size_t x_stride, float* Y, size_t y_stride,
                              uint32_t rows, uint32_t cols, uint32_t n_batch)
 {

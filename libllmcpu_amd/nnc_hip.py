@@ -84,6 +84,7 @@ SIGNATURES = {
     "nnc_hip_attend_gated": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_gated_device": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_gemv_bf16": (C.c_int, [_P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "nnc_hip_gemv_bf16_argmax": (C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
     "nnc_hip_gemv_q8_0": (C.c_int, [_P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
     "nnc_hip_gemv_q4_s": (C.c_int, [_P, _P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32,
                                     C.c_uint32, C.c_uint32]),
@@ -350,6 +351,30 @@ class KVCache:
                              xsum_dev=dev[nw + 1] if xsum is not None else 0, xsum_stride=cols // 32)
             self.sync()
             return hip_rt.to_host(np.empty((n, rows), np.float32), y_dev)
+        finally:
+            for d in dev:
+                hip_rt.free(d)
+
+    def gemv_argmax_device(self, w_dev: int, x_dev: int, *, rows: int, cols: int) -> int:
+        """argmax_r (W . x)[r] for BF16 W on the device (the lm_head of greedy
+        decode; nnc_gemv_bf16w_argmax_f32x); waits for the cache's stream."""
+        idx = C.c_int32(-2)
+        _check(self._lib.nnc_hip_gemv_bf16_argmax(self.handle, w_dev, x_dev, rows, cols, C.byref(idx)))
+        return int(idx.value)
+
+    def gemv_argmax(self, w: np.ndarray, x: np.ndarray) -> int:
+        """gemv_argmax_device from host arrays (BF16 bits w [rows, cols], x [cols])."""
+        from . import hip_rt
+
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        dev = []
+        try:
+            for a in (w, x):
+                d = hip_rt.malloc(max(a.nbytes, 16))
+                dev.append(d)
+                hip_rt.to_device(d, a)
+            return self.gemv_argmax_device(dev[0], dev[1], rows=w.shape[0], cols=w.shape[1])
         finally:
             for d in dev:
                 hip_rt.free(d)

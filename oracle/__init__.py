@@ -74,6 +74,7 @@ class _Lib:
         f("block_sums", None, [_P, _P, _SZ])
         _U32 = C.c_uint32
         f("gemv_bf16", None, [_P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
+        f("gemv_bf16_argmax", _I, [_P, _P, _U32, _U32])
         f("gemv_q8_0", None, [_P, _P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
         f("gemv_q4_s", None, [_P, _P, _P, _P, _SZ, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
 
@@ -180,6 +181,13 @@ class _Lib:
         Y = np.zeros((X.shape[0], W.shape[0]), np.float32)
         self._gemv_bf16(_p(W), _p(X), W.shape[1], _p(Y), W.shape[0], W.shape[0], W.shape[1], X.shape[0])
         return Y
+
+    def gemv_bf16_argmax(self, W, x):
+        """argmax_r (W . x)[r] for BF16 bits W [rows, cols] (greedy decode's
+        lm_head): -1 when W is empty."""
+        W = np.ascontiguousarray(W, dtype=np.uint16)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        return int(self._gemv_bf16_argmax(_p(W), _p(x), W.shape[0], W.shape[1] if W.ndim == 2 else 0))
 
     def gemv_q8_0(self, qs, scales, X):
         qs = np.ascontiguousarray(qs, dtype=np.int8)

@@ -25,6 +25,7 @@
 //   orc_gemv_bf16 / orc_gemv_q8_0 /        reference src/libnnc/nn_ops.cpp:1000-1053, 1352-1452,
 //   orc_gemv_q4_s                          1610-1700 (the weight gemvs, single and batched;
 //                                          model.cpp:1189-1210 picks one by tensor type)
+//   orc_gemv_bf16_argmax                   nn_ops.cpp:1055-1197 (lm_head argmax, model.cpp:2181-2190)
 // and two checkers that are not restatements:
 //   orc_textbook_attend   double-precision softmax attention per query, the
 //                         scalar reference of reference src/appnnc/tests.cpp:2424-2446
@@ -45,6 +46,7 @@
 #include <cstring>
 #include <random>
 #include <thread>
+#include <limits>
 #include <vector>
 
 extern "C" {
@@ -479,6 +481,28 @@ void orc_gemv_bf16(const uint16_t* W, const float* X, size_t x_stride, float* Y,
 			for (uint32_t k = 0; k < cols; ++k) s += bf16_to_f32(w[k]) * x[k];
 			Y[n * y_stride + r] = s;
 		}
+}
+
+// argmax_r y[r] of the BF16 gemv above (reference nn_ops.cpp:1055-1197,
+// nnc_gemv_bf16w_argmax_f32x): -1 for an empty matrix; when rows is a multiple
+// of 4 and cols of 8 (its fast paths, threaded or not) the first row whose
+// value is above every earlier one, starting from -inf, else 0; otherwise
+// (its fallback) the first row above every earlier one starting from y[0].
+int orc_gemv_bf16_argmax(const uint16_t* W, const float* x, uint32_t rows, uint32_t cols)
+{
+	if (rows == 0 || cols == 0) return -1;
+	std::vector<float> y(rows);
+	orc_gemv_bf16(W, x, cols, y.data(), rows, rows, cols, 1);
+	const bool fast = rows % 4 == 0 && cols % 8 == 0;
+	int best = 0;
+	float bv = fast ? -std::numeric_limits<float>::infinity() : y[0];
+	for (uint32_t r = fast ? 0 : 1; r < rows; ++r)
+		if (y[r] > bv)
+		{
+			bv = y[r];
+			best = static_cast<int>(r);
+		}
+	return best;
 }
 
 // Q8_0 split layout: y = sum over blocks of scale_b * (sum_{k in b} q_k x_k).

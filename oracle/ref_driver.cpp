@@ -17,7 +17,8 @@
 //       (reference nn_ops.h:73);
 //   ref_mul_sigmoid  calls nnc_mul_sigmoid_f32 (reference nn_ops.h:248);
 //   ref_quantize_q8_0 / ref_quantize_q4_s / ref_block_sums / ref_gemv_bf16 /
-//       ref_gemv_q8_0 / ref_gemv_q4_s call nnc_quantize_f32_to_q8_0,
+//       ref_gemv_bf16_argmax / ref_gemv_q8_0 / ref_gemv_q4_s call
+//       nnc_gemv_bf16w_argmax_f32x, nnc_quantize_f32_to_q8_0,
 //       nnc_quantize_f32_to_q4_s, nnc_block_sums_f32 and the batched gemvs
 //       (reference nn_ops.h:119-180, 193-205; the JIT kernels behind them);
 //   ref_set_threads / ref_threads call nnc_set_num_threads / nnc_num_threads
@@ -138,6 +139,11 @@ void ref_gemv_bf16(const uint16_t* W, const float* X, size_t x_stride, float* Y,
                    uint32_t cols, uint32_t n_batch)
 {
 	nnc_gemv_bf16w_f32x_batch(W, X, x_stride, Y, y_stride, rows, cols, n_batch);
+}
+
+int ref_gemv_bf16_argmax(const uint16_t* W, const float* x, uint32_t rows, uint32_t cols)
+{
+	return nnc_gemv_bf16w_argmax_f32x(W, x, rows, cols);
 }
 
 void ref_gemv_q8_0(const int8_t* qs, const uint16_t* scales, const float* X, size_t x_stride, float* Y,

@@ -173,6 +173,19 @@ def main() -> int:
     data["gemv/q4_s/qs"], data["gemv/q4_s/scales"], data["gemv/q4_s/biases"] = q4
     data["gemv/xsum"] = ref.block_sums(xg)
     data["gemv/q4_s/y"] = ref.gemv_q4_s(*q4, xg)
+    # The lm_head argmax: uniform(-1, 1) weights and x as in the reference's
+    # own test, on its fast path (rows % 4 == 0, cols % 8 == 0: 64 x 256, with
+    # the best row duplicated later, so the first copy must win) and its
+    # fallback (7 x 40).
+    for name, (rows, cols) in (("fast", (64, 256)), ("fallback", (7, 40))):
+        wa = ref.bf16_round(rng.uniform(-1.0, 1.0, (rows, cols)).astype(np.float32))
+        xa = rng.uniform(-1.0, 1.0, cols).astype(np.float32)
+        if name == "fast":
+            top = ref.gemv_bf16_argmax(wa, xa)
+            wa[rows - 3 if top != rows - 3 else rows - 1] = wa[top]  # a tie with the best row
+        data[f"argmax/{name}/w"] = wa
+        data[f"argmax/{name}/x"] = xa
+        data[f"argmax/{name}/index"] = np.int32(ref.gemv_bf16_argmax(wa, xa))
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
     return 0

@@ -199,3 +199,114 @@ def test_hip_gemv_strides_and_errors(orc):
     finally:
         for d in dev + [y_dev]:
             hip_rt.free(d)
+
+
+# ---- the lm_head argmax (reference nn_ops.cpp:1055-1197, model.cpp:2181-2190) ----------
+
+def bf16_rows(rng, rows, cols):
+    """BF16 bits of uniform(-1, 1) weights, drawn as bit patterns (fast at lm_head sizes)."""
+    mag = rng.integers(0x3C00, 0x3F80, size=(rows, cols), dtype=np.uint16)  # [2^-7, 1)
+    return mag | (rng.integers(0, 2, size=(rows, cols), dtype=np.uint16) << 15)
+
+
+def argmax_ok(w, x, got, want):
+    """The reference test's criterion (tests.cpp:603-619): the same row, or rows
+    whose float64 values are within 1e-3 * max(1, |best|)."""
+    if got == want:
+        return True
+    if got < 0 or want < 0:
+        return False
+    y_got, y_want = (float(bf16_f32(w[r]).astype(np.float64) @ x.astype(np.float64)) for r in (got, want))
+    return abs(y_got - y_want) <= 1e-3 * max(1.0, abs(y_want))
+
+
+def test_argmax_matches_reference_vectors(orc, gold):
+    for name in ("fast", "fallback"):
+        w, x = gold[f"argmax/{name}/w"], gold[f"argmax/{name}/x"]
+        assert orc.gemv_bf16_argmax(w, x) == int(gold[f"argmax/{name}/index"]), name
+
+
+def test_argmax_matches_reference_code(orc, ref):
+    # The reference test's shapes (tests.cpp:572-574) and larger ones, to its
+    # criterion (the oracle sums the fp32 products in column order, the
+    # reference's JIT kernel in its own order).
+    rng = np.random.default_rng(0xA12A)
+    for rows, cols in ((4, 32), (16, 256), (2048, 256), (256, 1536), (7, 5), (300, 64), (1024, 2560)):
+        w = orc.bf16_round(rng.uniform(-1, 1, (rows, cols)).astype(np.float32))
+        x = rng.uniform(-1, 1, cols).astype(np.float32)
+        got, want = orc.gemv_bf16_argmax(w, x), ref.gemv_bf16_argmax(w, x)
+        assert argmax_ok(w, x, got, want), (rows, cols, got, want)
+
+
+def test_argmax_closed_forms(orc):
+    rng = np.random.default_rng(3)
+    w = bf16_rows(rng, 64, 32)
+    x = np.ones(32, np.float32)
+    assert orc.gemv_bf16_argmax(np.zeros((0, 32), np.uint16), x) == -1
+    assert orc.gemv_bf16_argmax(w[:, :0], x[:0]) == -1
+    # One row of all ones against x = 1 wins with 32; two copies: the first.
+    w[40] = 0x3F80
+    assert orc.gemv_bf16_argmax(w, x) == 40
+    w[12] = 0x3F80
+    assert orc.gemv_bf16_argmax(w, x) == 12
+    # NaN rows are never chosen; all NaN (or all -inf): row 0.
+    w[12] = 0x7FC0
+    assert orc.gemv_bf16_argmax(w, x) == 40
+    assert orc.gemv_bf16_argmax(np.full((8, 32), 0x7FC0, np.uint16), x) == 0
+    assert orc.gemv_bf16_argmax(np.full((8, 32), 0xFF80, np.uint16), x) == 0  # -inf weights, y = -inf
+
+
+GPU_ARGMAX_SHAPES = [
+    (4, 32), (16, 256), (2048, 256), (256, 1536),  # the reference test's fast-path shapes
+    (1001, 2560),  # rows not a multiple of 4 (nor of a work-group's rows)
+    (151936, 2560),  # Qwen3-4B's lm_head (tied embeddings), 778 MB
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols", GPU_ARGMAX_SHAPES, ids=[f"{r}x{c}" for r, c in GPU_ARGMAX_SHAPES])
+def test_hip_gemv_argmax_matches_oracle(orc, rows, cols):
+    import libllmcpu_amd as nh
+
+    rng = np.random.default_rng(rows + cols)
+    w = bf16_rows(rng, rows, cols)
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        print(f"case argmax {rows} x {cols}", flush=True)
+        got = kv.gemv_argmax(w, x)
+        want = orc.gemv_bf16_argmax(w, x)
+        print(f"  got {got}, oracle {want}", flush=True)
+        assert argmax_ok(w, x, got, want)
+        # Plant a tie with the winner at an earlier and a later row: the earlier wins.
+        top = got
+        early, late = (top // 3, min(rows - 1, top + 1 + (rows - top) // 2)) if rows > 2 else (0, rows - 1)
+        if early != top and late != top:
+            w[early] = w[top]
+            w[late] = w[top]
+            print(f"case argmax {rows} x {cols}, ties at {early}, {top}, {late}", flush=True)
+            assert kv.gemv_argmax(w, x) == early
+
+
+@pytest.mark.gpu
+def test_hip_gemv_argmax_special_values(orc):
+    import libllmcpu_amd as nh
+
+    rng = np.random.default_rng(8)
+    rows, cols = 4096, 256
+    w = bf16_rows(rng, rows, cols)
+    x = np.abs(rng.uniform(0.1, 1, cols)).astype(np.float32)  # positive: -inf weights give y = -inf
+    with nh.KVCache([16], [64]) as kv:
+        print("case argmax special values", flush=True)
+        w[100] = 0x3F80  # the winner: 1.0 everywhere
+        w[50] = 0x7FC0  # a NaN row is never chosen
+        assert kv.gemv_argmax(w, x) == 100
+        assert kv.gemv_argmax(np.full((rows, cols), 0x7FC0, np.uint16), x) == 0  # all NaN
+        assert kv.gemv_argmax(np.full((rows, cols), 0xFF80, np.uint16), x) == 0  # all -inf
+        wn = np.full((rows, cols), 0xFF80, np.uint16)
+        wn[3000] = 0xBF80  # one finite row (-sum x) among -inf rows
+        assert kv.gemv_argmax(wn, x) == 3000
+        assert kv.gemv_argmax(w[:0], x) == -1
+        print("case argmax errors", flush=True)
+        with pytest.raises(nh.NncError) as e:
+            kv.gemv_argmax(w[:, :48], x[:48])
+        assert e.value.status == nh.NncStatus.UNSUPPORTED_MODEL
