@@ -229,15 +229,24 @@ nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* 
 
 /* Greedy decode's lm_head projection: the row of the largest element of
  * y = W x for a BF16 W [rows][cols] and one vector x, without writing y
- * (reference nn_ops.h:98-113, nn_ops.cpp:1055-1150 nnc_gemv_bf16w_argmax_f32x;
+ * (reference nn_ops.h:98-113, nn_ops.cpp:1055-1197 nnc_gemv_bf16w_argmax_f32x;
  * caller model_argmax, model.cpp:2181-2190). *index (host memory) receives
  * the smallest such row; NaN and -inf are never chosen, and 0 is returned
- * when no element is above -inf (the reference's threaded and 4-row paths);
- * -1 when rows or cols is 0. W and x are device memory; the call waits for
- * the cache's stream. Errors as nnc_hip_gemv_bf16; cols must also fit the
- * one-vector kernel (at most 15 872). */
+ * when no element is above -inf; when rows is not a multiple of 4, 0 also
+ * when y[0] is NaN (the reference's fallback scans from y[0]); -1 when rows
+ * or cols is 0. W and x are device memory; the call waits for the cache's
+ * stream. Errors as nnc_hip_gemv_bf16; cols must also fit the one-vector
+ * kernel (at most 15 872). */
 nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* x, uint32_t rows, uint32_t cols,
                                     int32_t* index);
+
+/* The same over logits already on the device (the quantised lm_head's
+ * scan after its gemv, reference model.cpp:2192-2195): the first r with
+ * y[r] > y[best] for every earlier best, starting from best = 0, i.e. the
+ * smallest row of the largest value, NaN never chosen, and 0 when y[0] is
+ * NaN or nothing is above -inf (also for n == 0). y is device memory; the
+ * call waits for the cache's stream. */
+nnc_status nnc_hip_argmax_f32(nnc_hip_kv* kv, const float* y, uint32_t n, int32_t* index);
 
 /* Waits for all work queued on the cache's stream. */
 nnc_status nnc_hip_kv_sync(nnc_hip_kv* kv);

@@ -478,6 +478,7 @@ namespace nnchip
 							const int r0 = pair_row(k);
 							if constexpr (ARGMAX)
 							{
+								if (r0 == 0 && lane == 0) p.argmax[1] = __builtin_isnan(y0);
 								if (argmax_better(y0, r0, best_v, best_r))
 								{
 									best_v = y0;
@@ -559,7 +560,41 @@ namespace nnchip
 				}
 				__syncthreads();
 			}
-			if (threadIdx.x == 0) *p.argmax = s_r[0] >= 0 ? s_r[0] : 0;
+			if (threadIdx.x == 0) p.argmax[0] = s_r[0] >= 0 && !(p.first_sticks && p.argmax[1]) ? s_r[0] : 0;
+		}
+
+		// The argmax's first pass over a float vector: each work-group's best
+		// (value, row) pair; y[0]'s NaN flag.
+		__global__ __launch_bounds__(256) void argmax_part_kernel(const gemv_params p)
+		{
+			__shared__ float s_v[256];
+			__shared__ int s_r[256];
+			float bv = -INFINITY;
+			int br = -1;
+			for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows; i += gridDim.x * 256)
+			{
+				const float v = p.y[i];
+				if (i == 0) p.argmax[1] = __builtin_isnan(v);
+				if (argmax_better(v, i, bv, br))
+				{
+					bv = v;
+					br = i;
+				}
+			}
+			s_v[threadIdx.x] = bv;
+			s_r[threadIdx.x] = br;
+			__syncthreads();
+			for (int h = 128; h > 0; h >>= 1)
+			{
+				if (threadIdx.x < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
+				                                     s_r[threadIdx.x]))
+				{
+					s_v[threadIdx.x] = s_v[threadIdx.x + h];
+					s_r[threadIdx.x] = s_r[threadIdx.x + h];
+				}
+				__syncthreads();
+			}
+			if (threadIdx.x == 0) p.best[blockIdx.x] = make_float2(s_v[0], __int_as_float(s_r[0]));
 		}
 
 		// Y[t][r] = the splits' partials summed in split order.
@@ -648,6 +683,14 @@ namespace nnchip
 		const int groups = gemv_vec_groups(p.rows);
 		const size_t lds = (static_cast<size_t>(p.cols) + 8) * 4; // x, then the wavefronts' best pairs
 		gemv_vec_kernel<kGemvBf16, true><<<groups, 256, lds, stream>>>(p);
+		gemv_argmax_final_kernel<<<1, 256, 0, stream>>>(p, groups);
+		return true;
+	}
+
+	bool launch_argmax(const gemv_params& p, hipStream_t stream)
+	{
+		const int groups = std::max(1, std::min((p.rows + 1023) / 1024, kArgmaxGroups));
+		argmax_part_kernel<<<groups, 256, 0, stream>>>(p);
 		gemv_argmax_final_kernel<<<1, 256, 0, stream>>>(p, groups);
 		return true;
 	}

@@ -131,7 +131,8 @@ namespace nnchip
 		// argmax of y instead of y (BF16, one vector): each work-group's best
 		// (value, row) pair, then the row
 		float2* best; // [work-groups] (value, row as int bits; row -1 when none)
-		int* argmax; // the result
+		int* argmax; // the result, then whether y[0] is NaN
+		int first_sticks; // 1: the result is 0 when y[0] is NaN (the reference's linear scan from y[0])
 	};
 
 	// K splits for a (rows, cols) gemv of n_batch vectors.
@@ -149,6 +150,11 @@ namespace nnchip
 	// the smallest row of the largest value above -inf, NaN never chosen, 0
 	// when there is none. Needs gemv_vec_fits(p.cols, 1).
 	bool launch_gemv_argmax(const gemv_params& p, hipStream_t stream);
+
+	// The same argmax over a float vector y of p.rows elements (p.y read, p.best
+	// and p.argmax set; at most kArgmaxGroups pairs).
+	constexpr int kArgmaxGroups = 512;
+	bool launch_argmax(const gemv_params& p, hipStream_t stream);
 
 	bool launch_zero(float* dst, size_t n, hipStream_t stream);
 

@@ -720,9 +720,10 @@ nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* 
 		return fail(NNC_ERR_INVALID_ARGUMENT, "weights and x must be 16-byte aligned");
 	const int groups = nnchip::gemv_vec_groups(static_cast<int>(rows));
 	const size_t best_bytes = static_cast<size_t>(groups) * sizeof(float2);
-	if (nnc_status s = reserve(kv, kv->gemv_part, best_bytes + sizeof(int32_t), "gemv scratch")) return s;
+	if (nnc_status s = reserve(kv, kv->gemv_part, best_bytes + 2 * sizeof(int32_t), "gemv scratch")) return s;
 	nnchip::gemv_params p{};
 	p.format = nnchip::kGemvBf16;
+	p.first_sticks = rows % 4 != 0; // the reference's fallback scans from y[0] (nn_ops.cpp:1184-1196)
 	p.w = W;
 	p.x = x;
 	p.x_stride = cols;
@@ -738,6 +739,33 @@ nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* 
 	int32_t r = 0;
 	NNC_HIP_TRY(hipMemcpyAsync(&r, p.argmax, sizeof(r), hipMemcpyDeviceToHost, kv->stream), "argmax download");
 	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "argmax gemv");
+	*index = r;
+	return NNC_OK;
+}
+
+nnc_status nnc_hip_argmax_f32(nnc_hip_kv* kv, const float* y, uint32_t n, int32_t* index)
+{
+	if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the context (cache) is NULL");
+	if (!y || !index) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL input or index pointer");
+	if (n == 0)
+	{
+		*index = 0; // the reference's scan starts at row 0 (model.cpp:2192-2194)
+		return NNC_OK;
+	}
+	if (n > 0x7fffffffu) return fail(NNC_ERR_INVALID_ARGUMENT, "argmax of %u elements", n);
+	const size_t best_bytes = static_cast<size_t>(nnchip::kArgmaxGroups) * sizeof(float2);
+	if (nnc_status s = reserve(kv, kv->gemv_part, best_bytes + 2 * sizeof(int32_t), "gemv scratch")) return s;
+	nnchip::gemv_params p{};
+	p.y = const_cast<float*>(y);
+	p.rows = static_cast<int>(n);
+	p.best = static_cast<float2*>(kv->gemv_part.ptr);
+	p.argmax = reinterpret_cast<int*>(static_cast<char*>(kv->gemv_part.ptr) + best_bytes);
+	p.first_sticks = 1;
+	nnchip::launch_argmax(p, kv->stream);
+	NNC_HIP_TRY(hipGetLastError(), "argmax launch");
+	int32_t r = 0;
+	NNC_HIP_TRY(hipMemcpyAsync(&r, p.argmax, sizeof(r), hipMemcpyDeviceToHost, kv->stream), "argmax download");
+	NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "argmax");
 	*index = r;
 	return NNC_OK;
 }

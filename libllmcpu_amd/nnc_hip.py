@@ -85,6 +85,7 @@ SIGNATURES = {
     "nnc_hip_attend_gated_device": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_gemv_bf16": (C.c_int, [_P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
     "nnc_hip_gemv_bf16_argmax": (C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
+    "nnc_hip_argmax_f32": (C.c_int, [_P, _P, C.c_uint32, C.POINTER(C.c_int32)]),
     "nnc_hip_gemv_q8_0": (C.c_int, [_P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
     "nnc_hip_gemv_q4_s": (C.c_int, [_P, _P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32,
                                     C.c_uint32, C.c_uint32]),
@@ -378,6 +379,20 @@ class KVCache:
         finally:
             for d in dev:
                 hip_rt.free(d)
+
+    def argmax(self, y: np.ndarray) -> int:
+        """nnc_hip_argmax_f32 of host logits y (uploaded to scratch device memory)."""
+        from . import hip_rt
+
+        y = np.ascontiguousarray(y, dtype=np.float32).reshape(-1)
+        d = hip_rt.malloc(max(y.nbytes, 16))
+        try:
+            hip_rt.to_device(d, y)
+            idx = C.c_int32(-2)
+            _check(self._lib.nnc_hip_argmax_f32(self.handle, d, y.size, C.byref(idx)))
+            return int(idx.value)
+        finally:
+            hip_rt.free(d)
 
     def sync(self) -> None:
         _check(self._lib.nnc_hip_kv_sync(self.handle))

@@ -75,6 +75,8 @@ class _Lib:
         _U32 = C.c_uint32
         f("gemv_bf16", None, [_P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
         f("gemv_bf16_argmax", _I, [_P, _P, _U32, _U32])
+        if self.prefix == "orc_":
+            f("argmax_f32", _I, [_P, _U32])
         f("gemv_q8_0", None, [_P, _P, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
         f("gemv_q4_s", None, [_P, _P, _P, _P, _SZ, _P, _SZ, _P, _SZ, _U32, _U32, _U32])
 
@@ -188,6 +190,11 @@ class _Lib:
         W = np.ascontiguousarray(W, dtype=np.uint16)
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
         return int(self._gemv_bf16_argmax(_p(W), _p(x), W.shape[0], W.shape[1] if W.ndim == 2 else 0))
+
+    def argmax_f32(self, y):
+        """The quantised lm_head's scan over logits y (oracle only)."""
+        y = np.ascontiguousarray(y, dtype=np.float32).reshape(-1)
+        return int(self._argmax_f32(_p(y), y.size))
 
     def gemv_q8_0(self, qs, scales, X):
         qs = np.ascontiguousarray(qs, dtype=np.int8)

@@ -26,6 +26,7 @@
 //   orc_gemv_q4_s                          1610-1700 (the weight gemvs, single and batched;
 //                                          model.cpp:1189-1210 picks one by tensor type)
 //   orc_gemv_bf16_argmax                   nn_ops.cpp:1055-1197 (lm_head argmax, model.cpp:2181-2190)
+//   orc_argmax_f32                         model.cpp:2192-2195 (the quantised lm_head's scan)
 // and two checkers that are not restatements:
 //   orc_textbook_attend   double-precision softmax attention per query, the
 //                         scalar reference of reference src/appnnc/tests.cpp:2424-2446
@@ -502,6 +503,17 @@ int orc_gemv_bf16_argmax(const uint16_t* W, const float* x, uint32_t rows, uint3
 			bv = y[r];
 			best = static_cast<int>(r);
 		}
+	return best;
+}
+
+// The quantised lm_head's argmax over its logits (reference
+// model.cpp:2192-2195): best starts at 0, and a row replaces it when its value
+// is strictly larger.
+int orc_argmax_f32(const float* y, uint32_t n)
+{
+	int best = 0;
+	for (uint32_t r = 1; r < n; ++r)
+		if (y[r] > y[best]) best = static_cast<int>(r);
 	return best;
 }
 

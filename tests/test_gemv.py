@@ -310,3 +310,70 @@ def test_hip_gemv_argmax_special_values(orc):
         with pytest.raises(nh.NncError) as e:
             kv.gemv_argmax(w[:, :48], x[:48])
         assert e.value.status == nh.NncStatus.UNSUPPORTED_MODEL
+
+
+def test_vector_argmax_closed_forms(orc):
+    # The quantised lm_head's scan (reference model.cpp:2192-2195): the first
+    # strictly larger row from row 0.
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    assert orc.argmax_f32(np.array([], np.float32)) == 0
+    assert orc.argmax_f32(np.array([1, 3, 2, 3], np.float32)) == 1
+    assert orc.argmax_f32(np.array([nan, 3, 5], np.float32)) == 0  # row 0 NaN: nothing is larger
+    assert orc.argmax_f32(np.array([1, nan, 5, nan], np.float32)) == 2
+    assert orc.argmax_f32(np.array([-inf, -inf, -inf], np.float32)) == 0
+    assert orc.argmax_f32(np.array([-inf, nan, -2], np.float32)) == 2
+    rng = np.random.default_rng(4)
+    for n in (2, 17, 1000):
+        y = rng.standard_normal(n).astype(np.float32)
+        y[rng.integers(1, n, n // 5 + 1)] = nan
+        assert orc.argmax_f32(y) == int(np.nanargmax(y))  # first occurrence of the largest non-NaN
+
+
+def test_argmax_fallback_row0_nan_matches_reference(orc, ref):
+    # The reference's 4-row / threaded paths skip a NaN row 0, its fallback
+    # (rows not a multiple of 4) keeps it; the oracle restates both.
+    rng = np.random.default_rng(6)
+    for rows in (7, 8, 1001, 1024):
+        w = bf16_rows(rng, rows, 256)
+        w[0] = 0x7FC0
+        x = rng.uniform(-1, 1, 256).astype(np.float32)
+        want = ref.gemv_bf16_argmax(w, x)
+        assert orc.gemv_bf16_argmax(w, x) == want, rows
+        assert (want == 0) == (rows % 4 != 0), rows
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 5, 1000, 151936, 262144])
+def test_hip_argmax_f32_matches_oracle(orc, n):
+    import libllmcpu_amd as nh
+
+    rng = np.random.default_rng(n)
+    y = rng.standard_normal(n).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        print(f"case argmax over {n} logits", flush=True)
+        assert kv.argmax(y) == orc.argmax_f32(y)
+        if n > 4:
+            top = int(np.argmax(y))
+            y[[n // 3, (2 * n) // 3]] = y[top]  # ties
+            y[rng.integers(1, n, 3)] = np.nan
+            y[top] = np.nan if top != 0 else y[top]
+            print(f"case argmax over {n} logits, ties and NaN", flush=True)
+            assert kv.argmax(y) == orc.argmax_f32(y)
+            y[0] = np.nan
+            assert kv.argmax(y) == orc.argmax_f32(y) == 0
+            assert kv.argmax(np.full(n, -np.inf, np.float32)) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [7, 1000, 1001])
+def test_hip_gemv_argmax_row0_nan(orc, rows):
+    import libllmcpu_amd as nh
+
+    rng = np.random.default_rng(rows)
+    w = bf16_rows(rng, rows, 256)
+    w[0] = 0x7FC0
+    x = rng.uniform(-1, 1, 256).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        print(f"case argmax {rows} x 256, row 0 NaN", flush=True)
+        got, want = kv.gemv_argmax(w, x), orc.gemv_bf16_argmax(w, x)
+        assert got == want if rows % 4 != 0 else argmax_ok(w, x, got, want)
