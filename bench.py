@@ -238,7 +238,8 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
-              "multi-GPU path; see DESIGN.md for how the op would shard)", file=sys.stderr)
+              "multi-GPU path; the op would shard by KV head, or by key range with one exchange of "
+              "(o, m, l) partials per token and layer)", file=sys.stderr)
         return 2
 
     import libllmcpu_amd as nh
