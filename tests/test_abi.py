@@ -93,6 +93,14 @@ def test_calls_on_a_null_cache_are_refused(lib):
     lib.nnc_hip_kv_free(None)  # a no-op
     assert lib.nnc_hip_fill_normal(None, 10, 1, 0, False, None) == nh.NncStatus.INVALID_ARGUMENT
     assert lib.nnc_hip_fill_normal(q.ctypes.data, 10, 1, 3, False, None) == nh.NncStatus.INVALID_ARGUMENT
+    # The gemvs and argmaxes check their arguments before touching a device.
+    idx = C.c_int32(-7)
+    st = lib.nnc_hip_gemv_bf16(None, q.ctypes.data, q.ctypes.data, 32, q.ctypes.data, 2, 2, 32, 1)
+    assert st == nh.NncStatus.INVALID_ARGUMENT
+    st = lib.nnc_hip_gemv_bf16_argmax(None, q.ctypes.data, q.ctypes.data, 2, 32, C.byref(idx))
+    assert st == nh.NncStatus.INVALID_ARGUMENT and idx.value == -7
+    st = lib.nnc_hip_argmax_f32(None, q.ctypes.data, 64, C.byref(idx))
+    assert st == nh.NncStatus.INVALID_ARGUMENT and idx.value == -7
 
 
 def test_missing_library_fails_loudly(tmp_path):
