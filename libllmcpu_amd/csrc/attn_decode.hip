@@ -18,7 +18,7 @@
 //            transposed (ds_read_b64_tr_b16) as the A operand; P^T, split into
 //            bf16 hi + lo, is the B operand straight from the score registers
 //            (the key order inside a 32-key step is permuted to match).
-//            F32 caches (decode_kernel): on the VALU in fp32, each lane owning
+//            F32 caches (f32_decode_kernel): on the VALU in fp32, each lane owning
 //            consecutive elements of one V row and reading the key's weights
 //            for all heads of the group from LDS.
 // The four wavefront partials merge in LDS; the work-group's partial
@@ -31,18 +31,18 @@
 #include "device_common.h"
 #include "kernels.h"
 
-#include <cstdlib>
 #include <type_traits>
 
 namespace nnchip
 {
 	namespace
 	{
-		template <int HD, bool BF16>
-		struct decode_shape
+		// Shape of the F32 kernel: CH keys per wavefront chunk.
+		template <int HD>
+		struct f32_shape
 		{
-			static constexpr int VEC = BF16 ? 8 : 4; // elements per 16-byte load
-			static constexpr int CH = (BF16 ? 8192 : 4096) / HD; // keys per wave chunk
+			static constexpr int VEC = 4; // elements per 16-byte load
+			static constexpr int CH = 4096 / HD; // keys per wave chunk
 			static constexpr int NT = CH / 16; // MFMA tiles per chunk
 			static constexpr int KK = HD / 32; // MFMA k-steps over head_dim
 			static constexpr int LPK = HD / VEC; // lanes per key in the V layout
@@ -60,48 +60,86 @@ namespace nnchip
 			return r >= rows ? r - rows : r;
 		}
 
-		// The work-group's result from its wavefronts' partials in s_wpart
-		// (o[head_dim], m, l per column, per wavefront), merged in wavefront
-		// order. Column c is query head c % G of token tok0 + c / G; the first
-		// n_cols columns are filled. With several splits the result is the
-		// split's partial; with one it is o * (1 / l), the expression the split
-		// merge ends with, so a token gets the same bits either way.
-		template <int HD, int G, int C, int W>
-		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float (*s_wpart)[C][HD + 2],
-		                                                int tok0, int n_cols, int split, int kvh)
+		// KV head hh of head group hg. Pairs take heads two apart, {0, 2},
+		// {1, 3}, {4, 6}, ..., when n_kv is a multiple of 4: on this part the
+		// 512-byte halves of a 1 KiB span stream at different rates when many
+		// work-groups read them (measured at head_dim 128: heads 0, 1, 4, 5
+		// of adjacent pairs finished 2.5 us after heads 2, 3, 6, 7 in a 26 us
+		// call), and a pair two heads apart reads one of each.
+		template <int HPW>
+		__device__ __forceinline__ int head_of(int hg, int hh, int n_kv)
 		{
-			constexpr int PW = HD + 2, kWaves = W, kThreads = 64 * W;
-			const int n_kv = gridDim.y;
+			if constexpr (HPW == 2)
+				if (n_kv % 4 == 0) return (hg >> 1) * 4 + (hg & 1) + 2 * hh;
+			return hg * HPW + hh;
+		}
+
+		// Floats per (token, query head) partial, in LDS and in the global
+		// scratch: o[head_dim], m (log2 units), l, two unused (16-byte rows).
+		template <int HD>
+		constexpr int part_pitch() { return HD + 4; }
+
+		// The work-group's result from its wavefronts' partials in s_wpart
+		// (o[head_dim], m, l per column, per wavefront). The work-group holds
+		// the HPW KV heads of head group hg (head_of); wavefront w works for
+		// head w % HPW of the group as its lane w / HPW, and a head's lanes
+		// merge in lane order. Column c is query head c % G of token
+		// tok0 + c / G; the first n_cols columns are filled. With several
+		// splits the result is the split's partial; with one it is
+		// o * (1 / l), the expression the split merge ends with, so a token
+		// gets the same bits either way. Each thread takes four consecutive
+		// elements of one column. (Wavefront w's partial of column c starts at
+		// s_wpart + w * wstride + c * part_pitch<HD>().)
+		template <int HD, int G, int W, int HPW>
+		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float* s_wpart, int wstride,
+		                                                int tok0, int n_cols, int split, int hg)
+		{
+			constexpr int PL = part_pitch<HD>(), LPH = W / HPW, kThreads = 64 * W, Q4 = HD / 4;
 			const bool single = p.n_split == 1;
-			for (int idx = threadIdx.x; idx < n_cols * PW; idx += kThreads)
+			for (int idx = threadIdx.x; idx < HPW * n_cols * Q4; idx += kThreads)
 			{
-				const int c = idx / PW, d = idx % PW;
-				const int tok = tok0 + c / G, h = c % G;
+				const int hh = idx / (n_cols * Q4), c = (idx / Q4) % n_cols, d = 4 * (idx % Q4);
+				const int tok = tok0 + c / G, h = c % G, kvh = head_of<HPW>(hg, hh, p.n_kv);
+				float mw[LPH], f[LPH];
 				float m = -INFINITY;
 #pragma unroll
-				for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_wpart[w][c][HD]);
-				const float m_use = m == -INFINITY ? 0.0f : m;
-				float* gpart = p.part + ((static_cast<size_t>(tok) * n_kv + kvh) * p.n_split + split) * G * PW + h * PW;
-				if (d == HD)
+				for (int l = 0; l < LPH; ++l)
 				{
-					if (!single) gpart[d] = m;
-					continue;
+					mw[l] = s_wpart[(l * HPW + hh) * wstride + c * PL + HD];
+					m = fmaxf(m, mw[l]);
 				}
-				float r = 0.0f;
+				const float m_use = m == -INFINITY ? 0.0f : m;
 #pragma unroll
-				for (int w = 0; w < kWaves; ++w)
-					r = fmaf(s_wpart[w][c][d], fast_exp2(s_wpart[w][c][HD] - m_use), r);
-				if (!single)
-					gpart[d] = r;
-				else if (d < HD)
+				for (int l = 0; l < LPH; ++l) f[l] = fast_exp2(mw[l] - m_use);
+				float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				float l_sum = 0.0f;
+#pragma unroll
+				for (int l = 0; l < LPH; ++l)
 				{
-					float l = 0.0f;
-#pragma unroll
-					for (int w = 0; w < kWaves; ++w)
-						l = fmaf(s_wpart[w][c][HD + 1], fast_exp2(s_wpart[w][c][HD] - m_use), l);
-					const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+					const float* wp = s_wpart + (l * HPW + hh) * wstride + c * PL;
+					const float4 v = *reinterpret_cast<const float4*>(wp + d);
+					r.x = fmaf(v.x, f[l], r.x);
+					r.y = fmaf(v.y, f[l], r.y);
+					r.z = fmaf(v.z, f[l], r.z);
+					r.w = fmaf(v.w, f[l], r.w);
+					l_sum = fmaf(wp[HD + 1], f[l], l_sum);
+				}
+				if (!single)
+				{
+					float* gpart = p.part + ((static_cast<size_t>(tok) * p.n_kv + kvh) * p.n_split + split) * G * PL + h * PL;
+					*reinterpret_cast<float4*>(gpart + d) = r;
+					if (d == 0) *reinterpret_cast<float2*>(gpart + HD) = make_float2(m, l_sum);
+				}
+				else
+				{
+					const float inv = l_sum > 0.0f ? 1.0f / l_sum : 0.0f;
 					const size_t oi = (static_cast<size_t>(tok) * p.n_head + kvh * G + h) * HD + d;
-					p.out[oi] = gated(r * inv, p.gate, oi);
+					float4 o;
+					o.x = gated(r.x * inv, p.gate, oi);
+					o.y = gated(r.y * inv, p.gate, oi + 1);
+					o.z = gated(r.z * inv, p.gate, oi + 2);
+					o.w = gated(r.w * inv, p.gate, oi + 3);
+					*reinterpret_cast<float4*>(p.out + oi) = o;
 				}
 			}
 		}
@@ -119,102 +157,148 @@ namespace nnchip
 			return max_with_other_half(x);
 		}
 
-		// Merges the n_split partials of one (token, query head) and writes
-		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492). One wavefront:
-		// every split's (m, l) and o slice is loaded before the first use, the
-		// maximum comes from DPP and lane swaps, and o and l are summed in
-		// ascending split order, one split at a time, with its weight broadcast
-		// by v_readlane. A split outside the token's span holds m = -inf, l = 0,
-		// o = 0 and adds exact zeros, so a token's result depends only on its own
-		// splits, whatever else the launch covered.
-		template <int HD, int G>
-		__global__ __launch_bounds__(64) void decode_merge_kernel(const decode_params p)
+		// LDS of one merge (256 threads).
+		template <int HD>
+		struct merge_lds
 		{
-			constexpr int PW = HD + 2, E = HD / 64, KB = 32, MS = kDecodeMaxSplits / 64;
-			typedef float fE __attribute__((ext_vector_type(E)));
-			const int kvh = blockIdx.x / G, h = blockIdx.x % G, tok = blockIdx.y;
-			const int n_kv = gridDim.x / G;
-			const int lane = threadIdx.x;
-			const int ns = p.n_split;
-			const size_t sstride = static_cast<size_t>(G) * PW;
-			const float* hp = p.part + ((static_cast<size_t>(tok) * n_kv + kvh) * ns * G + h) * PW; // split s at hp + s * sstride
+			static constexpr int PARTS = 1024 / HD; // 256 threads over HD / 4 float4s of o
+			float m[kDecodeMaxSplits], l[kDecodeMaxSplits];
+			float4 o[PARTS][HD / 4];
+			float ls[PARTS];
+			float wmax[4];
+		};
 
-			float m[MS], l[MS];
-#pragma unroll
-			for (int j = 0; j < MS; ++j)
-			{
-				const int s = lane + 64 * j;
-				m[j] = s < ns ? hp[s * sstride + HD] : -INFINITY;
-				l[j] = s < ns ? hp[s * sstride + HD + 1] : 0.0f;
-			}
-			fE v[KB];
+		// Merges the n_split partials of one (token, query head) and writes
+		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492). 256 threads:
+		// thread t owns elements 4 (t % (HD / 4)) .. + 3 of o for the splits
+		// of part t / (HD / 4), so a work-group's loads are issued together,
+		// 16 per thread at a time. A split belongs to part (its absolute
+		// number, split_base / split_keys + s) % PARTS; o and l are summed in
+		// ascending split order within a part, then the parts in order. A
+		// split outside the token's span holds m = -inf, l = 0, o = 0 and adds
+		// exact zeros, and the parts are fixed by the absolute split grid, so
+		// a token's result depends only on its own splits, whatever else the
+		// launch covered.
+		template <int HD, int G>
+		__device__ __forceinline__ void merge_splits(const decode_params& p, int tok, int qh, merge_lds<HD>& sh)
+		{
+			constexpr int PL = part_pitch<HD>(), Q4 = HD / 4, PARTS = merge_lds<HD>::PARTS, B = 16;
+			const int kvh = qh / G, h = qh % G;
+			const int ns = p.n_split;
+			const int d4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
+			const size_t sstride = static_cast<size_t>(G) * PL;
+			const float* hp = p.part + ((static_cast<size_t>(tok) * p.n_kv + kvh) * ns * G + h) * PL;
+			// This part's splits: s_first, s_first + PARTS, ... below ns.
+			const int a0 = p.split_base / p.split_keys;
+			const int s_first = ((part - a0 % PARTS) + PARTS) % PARTS;
+			const int n_mine = s_first < ns ? (ns - 1 - s_first) / PARTS + 1 : 0;
+
+			// A batch of B of them (indices clamped to a valid split; the ones
+			// past the part's last are not used).
+			float4 o[B];
 			auto load_batch = [&](int b0) __attribute__((always_inline))
 			{
 #pragma unroll
-				for (int u = 0; u < KB; ++u)
-				{
-					const int s = min(b0 + u, ns - 1);
-					v[u] = *reinterpret_cast<const fE*>(hp + s * sstride + E * lane);
-				}
+				for (int u = 0; u < B; ++u)
+					o[u] = *reinterpret_cast<const float4*>(hp + min(s_first + PARTS * (b0 + u), ns - 1) * sstride + 4 * d4);
 			};
 			load_batch(0);
-
-			float mx = m[0];
-#pragma unroll
-			for (int j = 1; j < MS; ++j) mx = fmaxf(mx, m[j]);
-			mx = wave_max_dpp(mx);
-			const float m_use = mx == -INFINITY ? 0.0f : mx;
-			float f[MS];
-#pragma unroll
-			for (int j = 0; j < MS; ++j) f[j] = lane + 64 * j < ns ? fast_exp2(m[j] - m_use) : 0.0f;
-
-			fE acc = fE(0.0f);
-			float L = 0.0f;
-			for (int b0 = 0;; b0 += KB)
+			float mx = -INFINITY;
+			for (int s = threadIdx.x; s < ns; s += 256)
 			{
-				const int g = b0 >> 6; // uniform; KB divides 64
-				float fg = f[0], lg = l[0];
+				const float2 ml = *reinterpret_cast<const float2*>(hp + s * sstride + HD);
+				sh.m[s] = ml.x;
+				sh.l[s] = ml.y;
+				mx = fmaxf(mx, ml.x);
+			}
+			// The maximum over the splits: per wavefront by DPP and lane swaps,
+			// then over the four wavefronts through LDS.
+			mx = wave_max_dpp(mx);
+			if ((threadIdx.x & 63) == 0) sh.wmax[threadIdx.x >> 6] = mx;
+			__syncthreads();
+			mx = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+			const float m_use = mx == -INFINITY ? 0.0f : mx;
+			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+			float L = 0.0f;
+			for (int b0 = 0; b0 < n_mine; b0 += B)
+			{
+				if (b0 > 0) load_batch(b0);
+				float mw[B], lw[B];
 #pragma unroll
-				for (int j = 1; j < MS; ++j)
+				for (int u = 0; u < B; ++u)
 				{
-					fg = g == j ? f[j] : fg;
-					lg = g == j ? l[j] : lg;
+					const int s = min(s_first + PARTS * (b0 + u), ns - 1);
+					mw[u] = sh.m[s];
+					lw[u] = sh.l[s];
 				}
 #pragma unroll
-				for (int u = 0; u < KB; ++u)
+				for (int u = 0; u < B; ++u)
 				{
-					if (b0 + u < ns) // uniform
+					if (b0 + u < n_mine)
 					{
-						const int src = (b0 & 63) + u;
-						const float fw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fg), src));
-						const float lw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lg), src));
-#pragma unroll
-						for (int e = 0; e < E; ++e) acc[e] = fmaf(v[u][e], fw, acc[e]);
-						L = fmaf(lw, fw, L);
+						const float f = fast_exp2(mw[u] - m_use);
+						acc.x = fmaf(o[u].x, f, acc.x);
+						acc.y = fmaf(o[u].y, f, acc.y);
+						acc.z = fmaf(o[u].z, f, acc.z);
+						acc.w = fmaf(o[u].w, f, acc.w);
+						L = fmaf(lw[u], f, L);
 					}
 				}
-				if (b0 + KB >= ns) break;
-				load_batch(b0 + KB);
 			}
-			const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-			const size_t oi = (static_cast<size_t>(tok) * p.n_head + kvh * G + h) * HD + E * lane;
-			fE r;
+			sh.o[part][d4] = acc;
+			if (d4 == 0) sh.ls[part] = L;
+			__syncthreads();
+			if (part == 0)
+			{
+				float4 r = sh.o[0][d4];
+				float lt = sh.ls[0];
 #pragma unroll
-			for (int e = 0; e < E; ++e) r[e] = gated(acc[e] * inv, p.gate, oi + e);
-			*reinterpret_cast<fE*>(p.out + oi) = r;
+				for (int j = 1; j < PARTS; ++j)
+				{
+					const float4 v = sh.o[j][d4];
+					r.x += v.x;
+					r.y += v.y;
+					r.z += v.z;
+					r.w += v.w;
+					lt += sh.ls[j];
+				}
+				const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+				const size_t oi = (static_cast<size_t>(tok) * p.n_head + qh) * HD + 4 * d4;
+				float4 out;
+				out.x = gated(r.x * inv, p.gate, oi);
+				out.y = gated(r.y * inv, p.gate, oi + 1);
+				out.z = gated(r.z * inv, p.gate, oi + 2);
+				out.w = gated(r.w * inv, p.gate, oi + 3);
+				*reinterpret_cast<float4*>(p.out + oi) = out;
+			}
 		}
 
-		template <int HD, int G, bool BF16, int W>
-		__global__ __launch_bounds__(64 * W) void decode_kernel(const decode_params p)
+		// The split merge, launched after the split kernel: one work-group per
+		// (query head, token). (A merge inside the split launch, by extra
+		// work-groups that wait on per-head counts and read the partials with
+		// device-coherent loads, measured slower: 35 vs 32 us per call at 32k
+		// keys, the coherent loads and the polling being slower than the
+		// launch boundary.)
+		template <int HD, int G>
+		__global__ __launch_bounds__(256) void decode_merge_kernel(const decode_params p)
 		{
-			constexpr int kWaves = W, kThreads = 64 * W;
-			using S = decode_shape<HD, BF16>;
+			__shared__ merge_lds<HD> sh;
+			merge_splits<HD, G>(p, blockIdx.y, blockIdx.x, sh);
+		}
+
+		// F32 K/V: scores on MFMA with both operands split into bf16 hi + lo
+		// (near-fp32), P.V on the VALU in fp32.
+		template <int HD, int G>
+		__global__ __launch_bounds__(256) void f32_decode_kernel(const decode_params p)
+		{
+			constexpr int W = 4, kWaves = W, kThreads = 64 * W;
+			using S = f32_shape<HD>;
 			constexpr int CH = S::CH, NT = S::NT, KK = S::KK, VEC = S::VEC, LPK = S::LPK, KPL = S::KPL, NV = S::NV;
-			constexpr int PW = HD + 2;
+			constexpr int PW = part_pitch<HD>();
 
 			__shared__ float s_p[kWaves][CH][16]; // weights: [wave][key][head]
 			__shared__ float s_alpha[kWaves][16];
-			__shared__ float s_wpart[kWaves][G][PW];
+			__shared__ __attribute__((aligned(16))) float s_wpart[kWaves][G][PW];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
@@ -223,7 +307,6 @@ namespace nnchip
 			const int kvh = blockIdx.y;
 			const int split = blockIdx.x;
 			const int tok = blockIdx.z;
-			const int n_kv = gridDim.y;
 
 			int first, last;
 			attn_span(p.causal, p.window, p.pos0 + tok, p.n_seq, first, last);
@@ -249,8 +332,8 @@ namespace nnchip
 			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
 			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
 
-			uint4 kreg[NT][KK][BF16 ? 1 : 2];
-			uint4 vreg[NV];
+			u32x4 kreg[NT][KK][2];
+			u32x4 vreg[NV];
 			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
 			{
 				cbase = sbase + c * CH;
@@ -265,21 +348,12 @@ namespace nnchip
 				{
 					const int k = min(max(cbase + 16 * t + col, clo), chi);
 					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
-					if constexpr (BF16)
-					{
-						const uint16_t* kp = static_cast<const uint16_t*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
+					const float* kp = static_cast<const float*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
 #pragma unroll
-						for (int kk = 0; kk < KK; ++kk) kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
-					}
-					else
+					for (int kk = 0; kk < KK; ++kk)
 					{
-						const float* kp = static_cast<const float*>(p.K) + row * p.kv_dim + head_off + 8 * grp;
-#pragma unroll
-						for (int kk = 0; kk < KK; ++kk)
-						{
-							kreg[t][kk][0] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
-							kreg[t][kk][1] = *reinterpret_cast<const uint4*>(kp + 32 * kk + 4);
-						}
+						kreg[t][kk][0] = load_stream(kp + 32 * kk);
+						kreg[t][kk][1] = load_stream(kp + 32 * kk + 4);
 					}
 				}
 			};
@@ -290,9 +364,7 @@ namespace nnchip
 				{
 					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
 					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
-					const char* vp = static_cast<const char*>(p.V) +
-					                 (row * p.kv_dim + head_off + VEC * (lane % LPK)) * (BF16 ? 2 : 4);
-					vreg[j] = *reinterpret_cast<const uint4*>(vp);
+					vreg[j] = load_stream(static_cast<const float*>(p.V) + row * p.kv_dim + head_off + VEC * (lane % LPK));
 				}
 			};
 
@@ -344,29 +416,18 @@ namespace nnchip
 #pragma unroll
 					for (int kk = 0; kk < KK; ++kk)
 					{
-						if constexpr (BF16)
-						{
-							const bf16x8 a = as_bf16x8(kreg[t][kk][0]);
-							acc[t] = mfma16x16x32(a, qhi[kk], acc[t]);
-							acc[t] = mfma16x16x32(a, qlo[kk], acc[t]);
-						}
-						else
-						{
-							float x[8];
-							const float* f0 = reinterpret_cast<const float*>(&kreg[t][kk][0]);
-							const float* f1 = reinterpret_cast<const float*>(&kreg[t][kk][1]);
+						float x[8];
 #pragma unroll
-							for (int j = 0; j < 4; ++j)
-							{
-								x[j] = f0[j];
-								x[4 + j] = f1[j];
-							}
-							bf16x8 khi, klo;
-							split_bf16x8(x, khi, klo);
-							acc[t] = mfma16x16x32(khi, qhi[kk], acc[t]);
-							acc[t] = mfma16x16x32(khi, qlo[kk], acc[t]);
-							acc[t] = mfma16x16x32(klo, qhi[kk], acc[t]);
+						for (int j = 0; j < 4; ++j)
+						{
+							x[j] = __uint_as_float(kreg[t][kk][0][j]);
+							x[4 + j] = __uint_as_float(kreg[t][kk][1][j]);
 						}
+						bf16x8 khi, klo;
+						split_bf16x8(x, khi, klo);
+						acc[t] = mfma16x16x32(khi, qhi[kk], acc[t]);
+						acc[t] = mfma16x16x32(khi, qlo[kk], acc[t]);
+						acc[t] = mfma16x16x32(klo, qhi[kk], acc[t]);
 					}
 				}
 				if (c_wave + kWaves <= c_last)
@@ -423,22 +484,8 @@ namespace nnchip
 #pragma unroll
 					for (int h = 0; h < G; ++h) w[h] = s_p[wave][kl][h];
 					float v[VEC];
-					if constexpr (BF16)
-					{
-						const uint32_t* d = reinterpret_cast<const uint32_t*>(&vreg[j]);
 #pragma unroll
-						for (int u = 0; u < 4; ++u)
-						{
-							v[2 * u] = bf16_lo(d[u]);
-							v[2 * u + 1] = bf16_hi(d[u]);
-						}
-					}
-					else
-					{
-						const float* f = reinterpret_cast<const float*>(&vreg[j]);
-#pragma unroll
-						for (int u = 0; u < 4; ++u) v[u] = f[u];
-					}
+					for (int u = 0; u < VEC; ++u) v[u] = __uint_as_float(vreg[j][u]);
 #pragma unroll
 					for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -470,7 +517,7 @@ namespace nnchip
 			}
 			__syncthreads();
 
-			write_wg_result<HD, G, G, W>(p, s_wpart, tok, G, split, kvh);
+			write_wg_result<HD, G, W, 1>(p, &s_wpart[0][0][0], G * PW, tok, G, split, kvh);
 		}
 
 		// Chunk sizes of the BF16 kernel: CH keys per wavefront chunk (a chunk's
@@ -506,8 +553,64 @@ namespace nnchip
 			return __builtin_bit_cast(u32x2, v);
 		}
 
+		// K/V rows are read through buffer descriptors over the whole layer
+		// buffer (the host keeps a BF16 buffer under 2 GiB) with the
+		// non-temporal hint. A load past the wavefront's last chunk gets an
+		// offset past every buffer: the range check returns zeros without a
+		// memory access, so loads need no branch around them.
+		constexpr int kBufferFlags = 0x00020000; // descriptor word 3: raw 32-bit data
+		constexpr int kAuxStream = 2; // cache policy bits: nt
+		constexpr uint32_t kDeadOffset = 0x80000000u;
+
+		__device__ __forceinline__ __amdgpu_buffer_rsrc_t layer_rsrc(const void* base, uint32_t bytes)
+		{
+			return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferFlags);
+		}
+
+		__device__ __forceinline__ u32x4 load_rows(__amdgpu_buffer_rsrc_t r, uint32_t off)
+		{
+			return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxStream);
+		}
+
+		// One chunk's K rows (the MFMA A operand) and V rows (as loaded, for
+		// the wavefront's LDS tile).
+		template <int NT, int KK, int NV>
+		struct chunk_regs
+		{
+			u32x4 k[NT][KK];
+			u32x4 v[NV];
+		};
+
+		// The work-group's (head group, split, token group) from its linear
+		// index among nx splits, ny head groups and nz token groups. One
+		// token: the head groups of a
+		// split are adjacent in dispatch order (linear index = head group
+		// fastest), so each split's rows are read as whole runs of
+		// HPW * head_dim elements by neighbouring work-groups. Several token
+		// groups: those of one (split, head group) go to one XCD in
+		// consecutive slots (work-groups are dealt to the XCDs round-robin by
+		// linear index), so they stream the same K/V rows through one L2.
+		__device__ __forceinline__ void wg_coords(int lin, int nx, int ny, int nz, int& hg, int& split, int& zg)
+		{
+			const int nxy = nx * ny;
+			if (nz > 1 && nxy % 8 == 0)
+			{
+				const int xcd = lin % 8, slot = lin / 8;
+				zg = slot % nz;
+				const int pair = 8 * (slot / nz) + xcd;
+				hg = pair % ny;
+				split = pair / ny;
+			}
+			else
+			{
+				zg = lin / nxy;
+				hg = (lin % nxy) % ny;
+				split = (lin % nxy) / ny;
+			}
+		}
+
 		// BF16 K/V: both products on MFMA.
-		//   S^T = K . Q^T     as in decode_kernel (Q split into bf16 hi + lo).
+		//   S^T = K . Q^T     on MFMA, Q split into bf16 hi + lo.
 		//   O^T += V^T . P^T  v_mfma_f32_16x16x32_bf16. P^T comes straight from
 		//                     the registers that hold S^T: two 16-key tiles give
 		//                     a lane the 8 weights it supplies as B operand, keys
@@ -525,41 +628,33 @@ namespace nnchip
 		// column's state bit-for-bit unchanged (its weights are exact zeros and
 		// its rescale factor exactly 1), so a token gets the same bits alone as
 		// in any batch over the same split grid.
-		// Loads run one chunk ahead: a chunk's K registers are reissued as soon
-		// as its scores are done, its V registers as soon as they are in LDS.
-		template <int HD, int G, int W, int CHK, int T>
+		// Loads run DEPTH chunks ahead in DEPTH register sets: a chunk's K
+		// registers are reissued (for the chunk DEPTH ahead) as soon as its
+		// scores are done, its V registers as soon as they are in LDS.
+		template <int HD, int G, int W, int CHK, int T, int HPW>
 		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_kernel(
 			const decode_params p)
 		{
 			using S = bf16_shape<HD, CHK>;
 			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
 			              NV = S::NV, VPITCH = S::VPITCH;
-			constexpr int PW = HD + 2, kWaves = W;
+			constexpr int PW = part_pitch<HD>(), LPH = W / HPW;
 			static_assert(T >= 1 && T * G <= 16, "tokens per work-group");
+			static_assert(HPW >= 1 && W % HPW == 0, "heads per work-group");
+			constexpr int DEPTH = 1; // chunks of K and V in flight per wavefront (register sets; 2 measured slower)
 
 			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
-			__shared__ float s_wpart[W][T * G][PW];
+			__shared__ __attribute__((aligned(16))) float s_wpart[W][T * G][PW];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps chunk control flow scalar
 			const int col = lane & 15;
 			const int grp = lane >> 4;
-			// A batch's token groups of one (split, KV head) pair go to one XCD
-			// in consecutive slots (work-groups are dealt to the XCDs round-robin
-			// by linear index), so they stream the same K/V rows through one L2.
-			int kvh = blockIdx.y, split = blockIdx.x, zg = blockIdx.z;
-			{
-				const int nxy = gridDim.x * gridDim.y, nz = gridDim.z;
-				const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-				if (nz > 1 && nxy % 8 == 0)
-				{
-					const int xcd = lin % 8, slot = lin / 8;
-					zg = slot % nz;
-					const int pair = 8 * (slot / nz) + xcd;
-					split = pair % gridDim.x;
-					kvh = pair / gridDim.x;
-				}
-			}
+			const int hh = wave % HPW, hlane = wave / HPW; // this wavefront's head in the work-group, its lane
+			const int n_hg = p.n_kv / HPW, n_zg = (p.n_tok + T - 1) / T;
+			int hg, split, zg;
+			wg_coords(blockIdx.x, p.n_split, n_hg, n_zg, hg, split, zg);
+			const int kvh = head_of<HPW>(hg, hh, p.n_kv);
 			const int tok0 = zg * T;
 			const int n_tt = min(T, p.n_tok - tok0); // tokens of this work-group
 			const int tt = col / G; // this lane's column: token tok0 + tt, head col % G
@@ -578,6 +673,255 @@ namespace nnchip
 			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
 			const int s0 = max(f0, sbase);
 			const int s1 = min(lL, send);
+			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
+			const __amdgpu_buffer_rsrc_t rk = layer_rsrc(p.K, static_cast<uint32_t>(p.rows) * row_bytes);
+			const __amdgpu_buffer_rsrc_t rv = layer_rsrc(p.V, static_cast<uint32_t>(p.rows) * row_bytes);
+			const uint32_t k_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * grp; // + 64 kk
+			const uint32_t v_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * (lane % LPK);
+			uint16_t* vt = s_v[wave];
+
+			// The head's chunks of the split go to its lanes in turn.
+			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
+			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
+			const int c_wave = c_first + ((hlane - c_first % LPH) + LPH) % LPH;
+			const int n_wchunks = c_wave <= c_last ? (c_last - c_wave) / LPH + 1 : 0; // uniform
+
+			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
+			{
+				cbase = sbase + c * CH;
+				clo = max(s0, cbase);
+				chi = min(s1, cbase + CH - 1);
+				rb = clo % p.rows;
+			};
+			using regs = chunk_regs<NT, KK, NV>;
+			// The i-th chunk of the wavefront (dead past its last one).
+			auto load_k = [&](regs& X, int i) __attribute__((always_inline))
+			{
+				const bool live = i < n_wchunks;
+				int cbase, clo, chi, rb;
+				chunk_bounds(c_wave + i * LPH, cbase, clo, chi, rb);
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+				{
+					const int k = min(max(cbase + 16 * t + col, clo), chi);
+					const uint32_t off = live ? static_cast<uint32_t>(ring_row(k, clo, rb, p.rows)) * row_bytes + k_col
+					                          : kDeadOffset;
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk) X.k[t][kk] = load_rows(rk, off + 64 * kk);
+				}
+			};
+			// Load j: key j * KPL + lane / LPK, elements 8 * (lane % LPK) .. + 8.
+			auto load_v = [&](regs& X, int i) __attribute__((always_inline))
+			{
+				const bool live = i < n_wchunks;
+				int cbase, clo, chi, rb;
+				chunk_bounds(c_wave + i * LPH, cbase, clo, chi, rb);
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+				{
+					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
+					X.v[j] = load_rows(rv, live ? static_cast<uint32_t>(ring_row(k, clo, rb, p.rows)) * row_bytes + v_col
+					                            : kDeadOffset);
+				}
+			};
+
+			// Q first (its loads return before the K/V rows issued after them),
+			// then the first two chunks of K and V, then Q^T as the B operand,
+			// scaled into log2 units and split into bf16 hi + lo.
+			const bool q_ok = tt < n_tt;
+			const float* qp = p.q + (static_cast<size_t>(tok0 + (q_ok ? tt : 0)) * p.n_head + kvh * G + col % G) * HD + 8 * grp;
+			float4 qa[KK], qb[KK];
+#pragma unroll
+			for (int kk = 0; kk < KK; ++kk)
+			{
+				qa[kk] = *reinterpret_cast<const float4*>(qp + 32 * kk);
+				qb[kk] = *reinterpret_cast<const float4*>(qp + 32 * kk + 4);
+			}
+			regs X0, X1;
+			load_k(X0, 0);
+			load_v(X0, 0);
+			if constexpr (DEPTH == 2)
+			{
+				load_k(X1, 1);
+				load_v(X1, 1);
+			}
+			bf16x8 qhi[KK], qlo[KK];
+#pragma unroll
+			for (int kk = 0; kk < KK; ++kk)
+			{
+				const float sq = p.qscale;
+				float x[8] = {qa[kk].x * sq, qa[kk].y * sq, qa[kk].z * sq, qa[kk].w * sq,
+				              qb[kk].x * sq, qb[kk].y * sq, qb[kk].z * sq, qb[kk].w * sq};
+#pragma unroll
+				for (int j = 0; j < 8; ++j) x[j] = q_ok ? x[j] : 0.0f;
+				split_bf16x8(x, qhi[kk], qlo[kk]);
+			}
+
+			float m_run = -INFINITY, l_run = 0.0f;
+			f32x4 acc_o[DB];
+#pragma unroll
+			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+			// The wavefront's i-th chunk from X; X is then reloaded with chunk i + DEPTH.
+			auto chunk = [&](regs& X, int i) __attribute__((always_inline))
+			{
+				int cbase, clo, chi, rb;
+				chunk_bounds(c_wave + i * LPH, cbase, clo, chi, rb);
+
+				f32x4 sc[NT];
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+				{
+					sc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+					for (int kk = 0; kk < KK; ++kk)
+					{
+						const bf16x8 a = as_bf16x8(X.k[t][kk]);
+						sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
+						sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
+					}
+				}
+				const bool reload = i + DEPTH < n_wchunks; // uniform
+				if (reload) load_k(X, i + DEPTH);
+
+				// This chunk's V rows into the wavefront's LDS tile, then the
+				// loads of chunk i + DEPTH into the freed registers.
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = X.v[j];
+				if (reload) load_v(X, i + DEPTH);
+
+				// Online softmax per head (column).
+				float m_loc = -INFINITY;
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int e = 0; e < 4; ++e)
+					{
+						const int k = cbase + 16 * t + 4 * grp + e;
+						const float v = (k >= col_s0 && k <= col_s1) ? sc[t][e] : -INFINITY;
+						sc[t][e] = v;
+						m_loc = fmaxf(m_loc, v);
+					}
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
+				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
+				const float m_new = fmaxf(m_run, m_loc);
+				const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+				const float alpha = fast_exp2(m_run - m_use);
+				m_run = m_new;
+				float lsum = 0.0f;
+				bf16x8 phi[NC], plo[NC];
+#pragma unroll
+				for (int c = 0; c < NC; ++c)
+				{
+					float w[8];
+#pragma unroll
+					for (int e = 0; e < 4; ++e)
+					{
+						w[e] = fast_exp2(sc[2 * c][e] - m_use);
+						w[4 + e] = fast_exp2(sc[2 * c + 1][e] - m_use);
+					}
+#pragma unroll
+					for (int e = 0; e < 8; ++e) lsum += w[e];
+					split_bf16x8(w, phi[c], plo[c]);
+				}
+				l_run = l_run * alpha + lsum;
+#pragma unroll
+				for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
+
+				wave_sync();
+#pragma unroll
+				for (int c = 0; c < NC; ++c)
+#pragma unroll
+					for (int db = 0; db < DB; ++db)
+					{
+						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
+						const u32x2 lo = vt_read(r0);
+						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
+						const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+						acc_o[db] = mfma16x16x32(a, phi[c], acc_o[db]);
+						acc_o[db] = mfma16x16x32(a, plo[c], acc_o[db]);
+					}
+				wave_sync(); // V is read before the next chunk overwrites it
+			};
+			int i = 0;
+			if constexpr (DEPTH == 2)
+				for (; i + 1 < n_wchunks; i += 2)
+				{
+					chunk(X0, i);
+					chunk(X1, i + 1);
+				}
+			for (; i < n_wchunks; ++i) chunk(X0, i);
+
+			// Wavefront partial: each (head, d) of O^T has one owner lane.
+			l_run += __shfl_xor(l_run, 16);
+			l_run += __shfl_xor(l_run, 32);
+			if (tt < n_tt) // col < n_tt * G <= T * G
+			{
+#pragma unroll
+				for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(&s_wpart[wave][col][16 * db + 4 * grp]) = acc_o[db];
+				if (grp == 0)
+				{
+					s_wpart[wave][col][HD] = m_run;
+					s_wpart[wave][col][HD + 1] = l_run;
+				}
+			}
+			__syncthreads();
+			write_wg_result<HD, G, W, HPW>(p, &s_wpart[0][0][0], T * G * PW, tok0, n_tt * G, split, hg);
+		}
+
+		// The BF16 kernel for a session batch: NTL tiles of 16 MFMA columns,
+		// 16 * NTL / G tokens per work-group, so a 16-token batch streams each
+		// K and V row once. Q (hi and lo) sits in LDS; per chunk the scores of
+		// every tile come from the same K registers and the V^T tile is read
+		// back once per tile. Each column goes through exactly the operations
+		// of decode_bf16_kernel (same products, same order), so a token gets
+		// the bits of its one-token call here too.
+		template <int HD, int G, int W, int CHK, int NTL, int HPW>
+		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_multi_kernel(
+			const decode_params p)
+		{
+			using S = bf16_shape<HD, CHK>;
+			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
+			              NV = S::NV, VPITCH = S::VPITCH;
+			constexpr int PW = part_pitch<HD>(), T = 16 * NTL / G, LPH = W / HPW;
+			static_assert(NTL >= 2 && (16 * NTL) % G == 0, "tiles per work-group");
+
+			// Each wavefront's partials go into its own V tile after its last chunk.
+			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
+			__shared__ __attribute__((aligned(16))) u32x4 s_q[HPW][NTL][KK][2][64]; // B operands, hi and lo, per head
+			static_assert(16 * PW * 4 <= CH * VPITCH * 2, "partials fit a V tile");
+			constexpr int kTileFloats = CH * VPITCH / 2;
+
+			const int lane = threadIdx.x & 63;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+			const int col = lane & 15;
+			const int grp = lane >> 4;
+			const int hh = wave % HPW, hlane = wave / HPW; // this wavefront's head in the work-group, its lane
+			const int n_hg = p.n_kv / HPW, n_zg = (p.n_tok + T - 1) / T;
+			int hg, split, zg;
+			wg_coords(blockIdx.x, p.n_split, n_hg, n_zg, hg, split, zg);
+			const int kvh = head_of<HPW>(hg, hh, p.n_kv);
+			const int tok0 = zg * T;
+			const int n_tt = min(T, p.n_tok - tok0);
+
+			const int sbase = p.split_base + split * p.split_keys;
+			const int send = sbase + p.split_keys - 1;
+			int col_s0[NTL], col_s1[NTL];
+#pragma unroll
+			for (int tl = 0; tl < NTL; ++tl)
+			{
+				const int tt = (16 * tl + col) / G;
+				int first, last;
+				attn_span(p.causal, p.window, p.pos0 + tok0 + tt, p.n_seq, first, last);
+				col_s0[tl] = tt < n_tt ? max(first, sbase) : 1;
+				col_s1[tl] = tt < n_tt ? min(last, send) : 0;
+			}
+			int f0, l0, fL, lL;
+			attn_span(p.causal, p.window, p.pos0 + tok0, p.n_seq, f0, l0);
+			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
+			const int s0 = max(f0, sbase);
+			const int s1 = min(lL, send);
 			const size_t head_off = static_cast<size_t>(kvh) * HD;
 			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
 			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
@@ -585,12 +929,12 @@ namespace nnchip
 
 			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
 			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
-			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
-			const bool has_chunk = c_wave <= c_last; // uniform over the wavefront
-			const int n_wchunks = has_chunk ? (c_last - c_wave) / kWaves + 1 : 0;
-			const int c_wlast = c_wave + (n_wchunks - 1) * kWaves;
+			int c_wave = c_first + ((hlane - c_first % LPH) + LPH) % LPH;
+			const bool has_chunk = c_wave <= c_last;
+			const int n_wchunks = has_chunk ? (c_last - c_wave) / LPH + 1 : 0;
+			const int c_wlast = c_wave + (n_wchunks - 1) * LPH;
 
-			u32x4 kreg[NT][KK]; // the chunk in flight
+			u32x4 kreg[NT][KK];
 			u32x4 vreg[NV];
 			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
 			{
@@ -637,253 +981,18 @@ namespace nnchip
 				load_v(c_wave);
 			}
 
-			// (The first K and V rows are in flight while Q is prepared.) Q^T as
-			// the B operand, scaled into log2 units and split into bf16 hi + lo.
-			bf16x8 qhi[KK], qlo[KK];
-#pragma unroll
-			for (int kk = 0; kk < KK; ++kk)
+			// Q^T of every tile of each head into LDS as the B operands, scaled
+			// into log2 units and split into bf16 hi + lo (entry (head, tl, kk, l)
+			// is lane l's 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
+			for (int i = threadIdx.x; i < HPW * NTL * KK * 64; i += 64 * W)
 			{
-				float x[8];
-				if (tt < n_tt)
-				{
-					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + kvh * G + col % G) * HD + 32 * kk +
-					                  8 * grp;
-					const float4 a = *reinterpret_cast<const float4*>(qp);
-					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
-					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-					x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-#pragma unroll
-					for (int j = 0; j < 8; ++j) x[j] *= p.qscale;
-				}
-				else
-				{
-#pragma unroll
-					for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-				}
-				split_bf16x8(x, qhi[kk], qlo[kk]);
-			}
-
-			float m_run = -INFINITY, l_run = 0.0f;
-			f32x4 acc_o[DB];
-#pragma unroll
-			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-			// One chunk from (kreg, vreg); the wavefront's next chunk is loaded
-			// into them as soon as they are consumed.
-			auto chunk = [&](int cw) __attribute__((always_inline))
-			{
-				int cbase, clo, chi, rb;
-				chunk_bounds(cw, cbase, clo, chi, rb);
-
-				f32x4 sc[NT];
-#pragma unroll
-				for (int t = 0; t < NT; ++t)
-				{
-					sc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-					for (int kk = 0; kk < KK; ++kk)
-					{
-						const bf16x8 a = as_bf16x8(kreg[t][kk]);
-						sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
-						sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
-					}
-				}
-				load_k(cw + kWaves);
-
-				// This chunk's V rows into the wavefront's LDS tile, then the next
-				// chunk's V loads into the freed registers.
-#pragma unroll
-				for (int j = 0; j < NV; ++j)
-					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
-				load_v(cw + kWaves);
-
-				// Online softmax per head (column).
-				float m_loc = -INFINITY;
-#pragma unroll
-				for (int t = 0; t < NT; ++t)
-#pragma unroll
-					for (int i = 0; i < 4; ++i)
-					{
-						const int k = cbase + 16 * t + 4 * grp + i;
-						const float v = (k >= col_s0 && k <= col_s1) ? sc[t][i] : -INFINITY;
-						sc[t][i] = v;
-						m_loc = fmaxf(m_loc, v);
-					}
-				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
-				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
-				const float m_new = fmaxf(m_run, m_loc);
-				const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-				const float alpha = fast_exp2(m_run - m_use);
-				m_run = m_new;
-				float lsum = 0.0f;
-				bf16x8 phi[NC], plo[NC];
-#pragma unroll
-				for (int c = 0; c < NC; ++c)
-				{
-					float w[8];
-#pragma unroll
-					for (int i = 0; i < 4; ++i)
-					{
-						w[i] = fast_exp2(sc[2 * c][i] - m_use);
-						w[4 + i] = fast_exp2(sc[2 * c + 1][i] - m_use);
-					}
-#pragma unroll
-					for (int i = 0; i < 8; ++i) lsum += w[i];
-					split_bf16x8(w, phi[c], plo[c]);
-				}
-				l_run = l_run * alpha + lsum;
-#pragma unroll
-				for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
-
-				wave_sync();
-#pragma unroll
-				for (int c = 0; c < NC; ++c)
-#pragma unroll
-					for (int db = 0; db < DB; ++db)
-					{
-						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
-						const u32x2 lo = vt_read(r0);
-						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-						const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-						acc_o[db] = mfma16x16x32(a, phi[c], acc_o[db]);
-						acc_o[db] = mfma16x16x32(a, plo[c], acc_o[db]);
-					}
-				wave_sync(); // V is read before the next chunk overwrites it
-			};
-			for (int i = 0; i < n_wchunks; ++i, c_wave += kWaves) chunk(c_wave);
-
-			// Wavefront partial: each (head, d) of O^T has one owner lane.
-			l_run += __shfl_xor(l_run, 16);
-			l_run += __shfl_xor(l_run, 32);
-			if (tt < n_tt) // col < n_tt * G <= T * G
-			{
-#pragma unroll
-				for (int db = 0; db < DB; ++db)
-#pragma unroll
-					for (int i = 0; i < 4; ++i) s_wpart[wave][col][16 * db + 4 * grp + i] = acc_o[db][i];
-				if (grp == 0)
-				{
-					s_wpart[wave][col][HD] = m_run;
-					s_wpart[wave][col][HD + 1] = l_run;
-				}
-			}
-			__syncthreads();
-			write_wg_result<HD, G, T * G, W>(p, s_wpart, tok0, n_tt * G, split, kvh);
-		}
-
-		// The BF16 kernel for a session batch: NTL tiles of 16 MFMA columns,
-		// 16 * NTL / G tokens per work-group, so a 16-token batch streams each
-		// K and V row once. Q (hi and lo) sits in LDS; per chunk the scores of
-		// every tile come from the same K registers and the V^T tile is read
-		// back once per tile. Each column goes through exactly the operations
-		// of decode_bf16_kernel (same products, same order), so a token gets
-		// the bits of its one-token call here too.
-		template <int HD, int G, int W, int CHK, int NTL>
-		__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_bf16_multi_kernel(
-			const decode_params p)
-		{
-			using S = bf16_shape<HD, CHK>;
-			constexpr int CH = S::CH, NT = S::NT, NC = S::NC, KK = S::KK, DB = S::DB, LPK = S::LPK, KPL = S::KPL,
-			              NV = S::NV, VPITCH = S::VPITCH;
-			constexpr int PW = HD + 2, kWaves = W, T = 16 * NTL / G;
-			static_assert(NTL >= 2 && (16 * NTL) % G == 0, "tiles per work-group");
-
-			__shared__ __attribute__((aligned(16))) uint16_t s_v[W][CH * VPITCH];
-			__shared__ float s_wpart[W][16][PW];
-			__shared__ __attribute__((aligned(16))) u32x4 s_q[NTL][KK][2][64]; // B operands, hi and lo
-
-			const int lane = threadIdx.x & 63;
-			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-			const int col = lane & 15;
-			const int grp = lane >> 4;
-			const int kvh = blockIdx.y;
-			const int split = blockIdx.x;
-			const int tok0 = blockIdx.z * T;
-			const int n_tt = min(T, p.n_tok - tok0);
-
-			const int sbase = p.split_base + split * p.split_keys;
-			const int send = sbase + p.split_keys - 1;
-			int col_s0[NTL], col_s1[NTL];
-#pragma unroll
-			for (int tl = 0; tl < NTL; ++tl)
-			{
-				const int tt = (16 * tl + col) / G;
-				int first, last;
-				attn_span(p.causal, p.window, p.pos0 + tok0 + tt, p.n_seq, first, last);
-				col_s0[tl] = tt < n_tt ? max(first, sbase) : 1;
-				col_s1[tl] = tt < n_tt ? min(last, send) : 0;
-			}
-			int f0, l0, fL, lL;
-			attn_span(p.causal, p.window, p.pos0 + tok0, p.n_seq, f0, l0);
-			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
-			const int s0 = max(f0, sbase);
-			const int s1 = min(lL, send);
-			const size_t head_off = static_cast<size_t>(kvh) * HD;
-			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
-			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
-			uint16_t* vt = s_v[wave];
-
-			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
-			const int c_last = s0 <= s1 ? (s1 - sbase) / CH : -1;
-			int c_wave = c_first + ((wave - c_first % kWaves) + kWaves) % kWaves;
-			const bool has_chunk = c_wave <= c_last;
-			const int n_wchunks = has_chunk ? (c_last - c_wave) / kWaves + 1 : 0;
-			const int c_wlast = c_wave + (n_wchunks - 1) * kWaves;
-
-			u32x4 kreg[NT][KK];
-			u32x4 vreg[NV];
-			auto chunk_bounds = [&](int c, int& cbase, int& clo, int& chi, int& rb) __attribute__((always_inline))
-			{
-				cbase = sbase + c * CH;
-				clo = max(s0, cbase);
-				chi = min(s1, cbase + CH - 1);
-				rb = clo % p.rows;
-			};
-			auto load_k = [&](int c) __attribute__((always_inline))
-			{
-				int cbase, clo, chi, rb;
-				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
-#pragma unroll
-				for (int t = 0; t < NT; ++t)
-				{
-					const int k = min(max(cbase + 16 * t + col, clo), chi);
-					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
-					const uint16_t* kp = Kg + row * p.kv_dim + 8 * grp;
-#pragma unroll
-					for (int kk = 0; kk < KK; ++kk) kreg[t][kk] = *reinterpret_cast<const u32x4*>(kp + 32 * kk);
-				}
-			};
-			auto load_v = [&](int c) __attribute__((always_inline))
-			{
-				int cbase, clo, chi, rb;
-				chunk_bounds(min(c, c_wlast), cbase, clo, chi, rb);
-#pragma unroll
-				for (int j = 0; j < NV; ++j)
-				{
-					const int k = min(max(cbase + j * KPL + lane / LPK, clo), chi);
-					const size_t row = static_cast<size_t>(ring_row(k, clo, rb, p.rows));
-					vreg[j] = *reinterpret_cast<const u32x4*>(Vg + row * p.kv_dim + 8 * (lane % LPK));
-				}
-			};
-
-			if (has_chunk)
-			{
-				load_k(c_wave);
-				load_v(c_wave);
-			}
-
-			// Q^T of every tile into LDS as the B operands, scaled into log2
-			// units and split into bf16 hi + lo (entry (tl, kk, l) is lane l's
-			// 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
-			for (int i = threadIdx.x; i < NTL * KK * 64; i += 64 * W)
-			{
-				const int l = i & 63, kk = (i >> 6) % KK, tl = (i >> 6) / KK;
+				const int l = i & 63, kk = (i >> 6) % KK, tl = ((i >> 6) / KK) % NTL, qh = (i >> 6) / (KK * NTL);
 				const int gc = 16 * tl + (l & 15), tt = gc / G;
 				float x[8];
 				if (tt < n_tt)
 				{
-					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + kvh * G + gc % G) * HD + 32 * kk +
-					                  8 * (l >> 4);
+					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + head_of<HPW>(hg, qh, p.n_kv) * G + gc % G) * HD +
+					                  32 * kk + 8 * (l >> 4);
 					const float4 a = *reinterpret_cast<const float4*>(qp);
 					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
 					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
@@ -898,8 +1007,8 @@ namespace nnchip
 				}
 				bf16x8 hi, lo;
 				split_bf16x8(x, hi, lo);
-				s_q[tl][kk][0][l] = __builtin_bit_cast(u32x4, hi);
-				s_q[tl][kk][1][l] = __builtin_bit_cast(u32x4, lo);
+				s_q[qh][tl][kk][0][l] = __builtin_bit_cast(u32x4, hi);
+				s_q[qh][tl][kk][1][l] = __builtin_bit_cast(u32x4, lo);
 			}
 			__syncthreads();
 
@@ -929,8 +1038,8 @@ namespace nnchip
 #pragma unroll
 					for (int kk = 0; kk < KK; ++kk)
 					{
-						const bf16x8 qh = __builtin_bit_cast(bf16x8, s_q[tl][kk][0][lane]);
-						const bf16x8 ql = __builtin_bit_cast(bf16x8, s_q[tl][kk][1][lane]);
+						const bf16x8 qh = __builtin_bit_cast(bf16x8, s_q[hh][tl][kk][0][lane]);
+						const bf16x8 ql = __builtin_bit_cast(bf16x8, s_q[hh][tl][kk][1][lane]);
 #pragma unroll
 						for (int t = 0; t < NT; ++t)
 						{
@@ -939,12 +1048,12 @@ namespace nnchip
 							sc[tl][t] = mfma16x16x32(a, ql, sc[tl][t]);
 						}
 					}
-				load_k(cw + kWaves);
+				load_k(cw + LPH);
 
 #pragma unroll
 				for (int j = 0; j < NV; ++j)
 					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
-				load_v(cw + kWaves);
+				load_v(cw + LPH);
 				wave_sync();
 
 #pragma unroll
@@ -1001,9 +1110,12 @@ namespace nnchip
 				}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			for (int i = 0; i < n_wchunks; ++i, c_wave += kWaves) chunk(c_wave);
+			for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(c_wave);
 
-			// One tile at a time through the wavefront merge.
+			// One tile at a time through the wavefront merge; a wavefront's
+			// partials go into its own V tile (read by it only until here).
+			float* s_wpart = reinterpret_cast<float*>(&s_v[0][0]);
+			float* wpart = s_wpart + wave * kTileFloats;
 #pragma unroll
 			for (int tl = 0; tl < NTL; ++tl)
 			{
@@ -1014,17 +1126,15 @@ namespace nnchip
 				if (col < n_cols)
 				{
 #pragma unroll
-					for (int db = 0; db < DB; ++db)
-#pragma unroll
-						for (int i = 0; i < 4; ++i) s_wpart[wave][col][16 * db + 4 * grp + i] = acc_o[tl][db][i];
+					for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(&wpart[col * PW + 16 * db + 4 * grp]) = acc_o[tl][db];
 					if (grp == 0)
 					{
-						s_wpart[wave][col][HD] = m_run[tl];
-						s_wpart[wave][col][HD + 1] = lr;
+						wpart[col * PW + HD] = m_run[tl];
+						wpart[col * PW + HD + 1] = lr;
 					}
 				}
 				__syncthreads();
-				if (n_cols > 0) write_wg_result<HD, G, 16, W>(p, s_wpart, tok0 + 16 * tl / G, n_cols, split, kvh);
+				if (n_cols > 0) write_wg_result<HD, G, W, HPW>(p, s_wpart, kTileFloats, tok0 + 16 * tl / G, n_cols, split, hg);
 				__syncthreads(); // the partials are read before the next tile overwrites them
 			}
 		}
@@ -1034,107 +1144,87 @@ namespace nnchip
 		// SIMD) run 2% slower.
 		constexpr int bf16_chunk(int head_dim) { return head_dim == 256 ? 32 : 64; }
 
-		int bf16_wg_keys(int head_dim) { return 4 * bf16_chunk(head_dim); }
-
-		// NNC_HIP_DECODE_KERNEL=valu runs BF16 caches through the VALU P.V
-		// kernel instead of the MFMA one (for comparison).
-		bool decode_valu_pv()
-		{
-			static const bool v = []
-			{
-				const char* e = std::getenv("NNC_HIP_DECODE_KERNEL");
-				return e && e[0] == 'v';
-			}();
-			return v;
-		}
 
 		template <int HD, int G, bool BF16>
-		void launch_g(const decode_params& p, int n_kv, int n_tok, int waves, hipStream_t stream)
+		void launch_g(const decode_params& p, int n_tok, hipStream_t stream)
 		{
-			const dim3 grid(p.n_split, n_kv, n_tok);
-			if (BF16 && !decode_valu_pv())
+			if constexpr (BF16)
 			{
 				// One token: the one-token instance (less LDS for partials);
-				// batches: 16 / G tokens per work-group. Both compute a token's
-				// column with the same operations.
+				// batches: 16 / G tokens per work-group, or four tiles of them.
+				// All compute a token's column with the same operations.
 				constexpr int T = 16 / G, TM = 64 / G; // tokens per work-group: one tile, four tiles
-				if (n_tok == 1)
-					decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1><<<grid, 256, 0, stream>>>(p);
-				else
+				auto go = [&](auto hpw_tag)
 				{
-					bool multi = false;
-					if constexpr (HD <= 128) // (at head_dim 256 four tiles do not fit the registers)
+					constexpr int HPW = decltype(hpw_tag)::value;
+					const int n_hg = p.n_kv / HPW;
+					if (n_tok == 1)
+						decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1, HPW><<<p.n_split * n_hg, 256, 0, stream>>>(p);
+					else
 					{
-						if (n_tok > T)
+						bool multi = false;
+						if constexpr (HD <= 128) // (at head_dim 256 four tiles do not fit the registers)
 						{
-							multi = true;
-							decode_bf16_multi_kernel<HD, G, 4, bf16_chunk(HD), 4>
-								<<<dim3(p.n_split, n_kv, (n_tok + TM - 1) / TM), 256, 0, stream>>>(p);
+							if (n_tok > T)
+							{
+								multi = true;
+								decode_bf16_multi_kernel<HD, G, 4, bf16_chunk(HD), 4, HPW>
+									<<<p.n_split * n_hg * ((n_tok + TM - 1) / TM), 256, 0, stream>>>(p);
+							}
 						}
+						if (!multi)
+							decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), T, HPW>
+								<<<p.n_split * n_hg * ((n_tok + T - 1) / T), 256, 0, stream>>>(p);
 					}
-					if (!multi)
-						decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), T>
-							<<<dim3(p.n_split, n_kv, (n_tok + T - 1) / T), 256, 0, stream>>>(p);
-				}
+				};
+				if (bf16_heads_per_wg(p.n_kv) == 2)
+					go(std::integral_constant<int, 2>{});
+				else
+					go(std::integral_constant<int, 1>{});
 			}
-			else if (waves == 8)
-				decode_kernel<HD, G, BF16, 8><<<grid, 512, 0, stream>>>(p);
 			else
-				decode_kernel<HD, G, BF16, 4><<<grid, 256, 0, stream>>>(p);
-			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(n_kv * G, n_tok), 64, 0, stream>>>(p);
+				f32_decode_kernel<HD, G><<<dim3(p.n_split, p.n_kv, n_tok), 256, 0, stream>>>(p);
+			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(p.n_kv * G, n_tok), 256, 0, stream>>>(p);
 		}
 
 		template <int HD, bool BF16>
-		bool launch_hd(const decode_params& p, int n_kv, int n_tok, int group, int waves, hipStream_t stream)
+		bool launch_hd(const decode_params& p, int n_tok, int group, hipStream_t stream)
 		{
 			switch (group)
 			{
-			case 1: launch_g<HD, 1, BF16>(p, n_kv, n_tok, waves, stream); return true;
-			case 2: launch_g<HD, 2, BF16>(p, n_kv, n_tok, waves, stream); return true;
-			case 4: launch_g<HD, 4, BF16>(p, n_kv, n_tok, waves, stream); return true;
-			case 8: launch_g<HD, 8, BF16>(p, n_kv, n_tok, waves, stream); return true;
+			case 1: launch_g<HD, 1, BF16>(p, n_tok, stream); return true;
+			case 2: launch_g<HD, 2, BF16>(p, n_tok, stream); return true;
+			case 4: launch_g<HD, 4, BF16>(p, n_tok, stream); return true;
+			case 8: launch_g<HD, 8, BF16>(p, n_tok, stream); return true;
 			default: return false;
 			}
 		}
-
 	}
 
-	int decode_waves()
+	int decode_wg_keys(int head_dim, bool bf16, int n_kv)
 	{
-		static const int w = []
-		{
-			const char* e = std::getenv("NNC_HIP_DECODE_WAVES"); // 4 or 8, for tuning
-			return (e && std::atoi(e) == 8) ? 8 : 4;
-		}();
-		return w;
-	}
-
-	int decode_wg_keys(int head_dim, bool bf16)
-	{
+		const int lanes = bf16 ? 4 / bf16_heads_per_wg(n_kv) : 4; // wavefronts per KV head
 		switch (head_dim)
 		{
-		case 64: return (bf16 && !decode_valu_pv()) ? bf16_wg_keys(64) : (bf16 ? decode_shape<64, true>::CH : decode_shape<64, false>::CH) * decode_waves();
-		case 128: return (bf16 && !decode_valu_pv()) ? bf16_wg_keys(128) : (bf16 ? decode_shape<128, true>::CH : decode_shape<128, false>::CH) * decode_waves();
-		case 256: return (bf16 && !decode_valu_pv()) ? bf16_wg_keys(256) : (bf16 ? decode_shape<256, true>::CH : decode_shape<256, false>::CH) * decode_waves();
+		case 64: return lanes * (bf16 ? bf16_chunk(64) : f32_shape<64>::CH);
+		case 128: return lanes * (bf16 ? bf16_chunk(128) : f32_shape<128>::CH);
+		case 256: return lanes * (bf16 ? bf16_chunk(256) : f32_shape<256>::CH);
 		default: return 0;
 		}
 	}
 
-	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
-	                   hipStream_t stream)
+	int decode_groups(int n_kv, bool bf16) { return bf16 ? n_kv / bf16_heads_per_wg(n_kv) : n_kv; }
+
+	bool launch_decode(const decode_params& p, int n_tok, int head_dim, int group, bool bf16, hipStream_t stream)
 	{
-		const int w = decode_waves();
 		switch (head_dim)
 		{
 		case 64:
-			return bf16 ? launch_hd<64, true>(p, n_kv, n_tok, group, w, stream)
-			            : launch_hd<64, false>(p, n_kv, n_tok, group, w, stream);
+			return bf16 ? launch_hd<64, true>(p, n_tok, group, stream) : launch_hd<64, false>(p, n_tok, group, stream);
 		case 128:
-			return bf16 ? launch_hd<128, true>(p, n_kv, n_tok, group, w, stream)
-			            : launch_hd<128, false>(p, n_kv, n_tok, group, w, stream);
+			return bf16 ? launch_hd<128, true>(p, n_tok, group, stream) : launch_hd<128, false>(p, n_tok, group, stream);
 		case 256:
-			return bf16 ? launch_hd<256, true>(p, n_kv, n_tok, group, w, stream)
-			            : launch_hd<256, false>(p, n_kv, n_tok, group, w, stream);
+			return bf16 ? launch_hd<256, true>(p, n_tok, group, stream) : launch_hd<256, false>(p, n_tok, group, stream);
 		default: return false;
 		}
 	}

@@ -17,8 +17,8 @@ namespace nnchip
 		const void* K; // [rows][kv_dim], BF16 bits or F32
 		const void* V;
 		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
-		float* part; // [n_tok][n_kv][n_split][group][head_dim + 2]: o, then m (log2 units), then l
-		int rows, kv_dim, n_head;
+		float* part; // [n_tok][n_kv][n_split][group][head_dim + 4]: o, then m (log2 units), then l
+		int rows, kv_dim, n_head, n_kv;
 		int pos0, n_seq, window, causal; // token t sits at pos0 + t
 		int n_tok; // tokens in this launch
 		int split_base; // first key of split 0, a multiple of split_keys
@@ -29,17 +29,26 @@ namespace nnchip
 
 	constexpr int kDecodeMaxSplits = 256;
 
-	// Keys one decode work-group consumes per iteration, for a head size and
-	// element type; split_keys must be a multiple of it.
-	int decode_wg_keys(int head_dim, bool bf16);
+	// KV heads per work-group of the BF16 kernels: two when n_kv is even (a
+	// work-group then reads runs of 2 * head_dim elements of each row, two
+	// wavefronts per head), else one (four wavefronts per head). Every BF16
+	// kernel splits a head's keys among its wavefronts the same way, which is
+	// what keeps a token's bits independent of the kernel that computes it.
+	inline int bf16_heads_per_wg(int n_kv) { return n_kv % 2 == 0 ? 2 : 1; }
 
-	// Launches the decode kernel over an (n_split, n_kv, token groups) grid,
-	// then (n_split > 1) the split merge over (n_kv * group, n_tok); returns
-	// false when (head_dim, group, bf16) has no instantiation. A token's
-	// result depends only on its own span and the split grid (split_keys and
-	// the absolute split boundaries), not on the other tokens of the launch.
-	bool launch_decode(const decode_params& p, int n_kv, int n_tok, int head_dim, int group, bool bf16,
-	                   hipStream_t stream);
+	// Work-groups per split (head groups) and the keys one work-group
+	// consumes per iteration, for a head size, element type and n_kv;
+	// split_keys must be a multiple of the latter.
+	int decode_groups(int n_kv, bool bf16);
+	int decode_wg_keys(int head_dim, bool bf16, int n_kv);
+
+	// Launches the decode kernel over an (n_split, head groups, token groups)
+	// grid, then (n_split > 1) the split merge over (n_kv * group, n_tok);
+	// returns false when (head_dim, group, bf16) has no instantiation. A
+	// token's result depends only on its own span and the split grid
+	// (split_keys and the absolute split boundaries), not on the other tokens
+	// of the launch.
+	bool launch_decode(const decode_params& p, int n_tok, int head_dim, int group, bool bf16, hipStream_t stream);
 
 	// Tiled MFMA attention for a batch of query tokens.
 	struct prefill_params

@@ -195,16 +195,14 @@ namespace
 	}
 
 	// Keys per decode work-group for the span [kmin, kmax] shared out over
-	// `pairs` (token, KV head) pairs: about one work-group per CU, a multiple
-	// of what one work-group iteration consumes, at most kDecodeMaxSplits
-	// splits.
+	// `pairs` (token, head group) pairs: about one work-group per CU, a
+	// multiple of what one work-group iteration consumes, at most
+	// kDecodeMaxSplits splits.
 	int split_keys_for(const nnc_hip_kv* kv, int kmin, int kmax, long long pairs, int wgk)
 	{
 		const int span = std::max(1, kmax - kmin + 1);
 		const long long want = std::max<long long>(1, 1LL * kv->n_cu / std::max<long long>(pairs, 1));
 		long long sk = (span + want - 1) / want;
-		if (const char* e = std::getenv("NNC_HIP_DECODE_SPLIT")) // keys per work-group, for tuning
-			if (std::atoll(e) > 0) sk = std::atoll(e);
 		sk = std::max<long long>(wgk, (sk + wgk - 1) / wgk * wgk);
 		while ((kmax / sk) - (kmin / sk) + 1 > nnchip::kDecodeMaxSplits) sk += wgk;
 		return static_cast<int>(sk);
@@ -227,8 +225,7 @@ namespace
 		const int n_split = kmax / split_keys - kmin / split_keys + 1;
 		if (n_split > nnchip::kDecodeMaxSplits)
 			return fail(NNC_ERR_IO, "decode split grid of %d splits (at most %d)", n_split, nnchip::kDecodeMaxSplits);
-		const long long pairs = static_cast<long long>(n_tok) * n_kv;
-		const size_t part_floats = static_cast<size_t>(pairs) * n_split * group * (head_dim + 2);
+		const size_t part_floats = static_cast<size_t>(n_tok) * n_kv * n_split * group * (head_dim + 4);
 		if (nnc_status s = reserve(kv, kv->part, part_floats * sizeof(float), "decode scratch")) return s;
 
 		nnchip::decode_params p{};
@@ -241,6 +238,7 @@ namespace
 		p.rows = b.rows;
 		p.kv_dim = b.kv_dim;
 		p.n_head = n_head;
+		p.n_kv = n_kv;
 		p.pos0 = pos0;
 		p.n_seq = n_seq;
 		p.window = window;
@@ -250,7 +248,7 @@ namespace
 		p.split_keys = split_keys;
 		p.n_split = n_split;
 		p.qscale = scale * 1.4426950408889634f;
-		if (!nnchip::launch_decode(p, n_kv, n_tok, head_dim, group, kv->bf16, kv->stream))
+		if (!nnchip::launch_decode(p, n_tok, head_dim, group, kv->bf16, kv->stream))
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no decode kernel for head_dim %d, group %d", head_dim, group);
 		NNC_HIP_TRY(hipGetLastError(), "decode launch");
 		return NNC_OK;
@@ -265,14 +263,15 @@ namespace
 	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
 	                         int32_t head_dim, float scale)
 	{
-		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16);
+		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv);
+		const int groups = nnchip::decode_groups(n_kv, kv->bf16);
 		auto span_of = [&](int32_t t, int& first, int& last)
 		{ nnchip::attn_span(causal ? 1 : 0, window, pos0 + t, n_seq, first, last); };
 		auto own_split = [&](int32_t t)
 		{
 			int first, last;
 			span_of(t, first, last);
-			return split_keys_for(kv, first, last, n_kv, wgk);
+			return split_keys_for(kv, first, last, groups, wgk);
 		};
 		const size_t tok_floats = static_cast<size_t>(n_head) * head_dim;
 		for (int32_t t = 0; t < n_tok;)
@@ -355,8 +354,8 @@ namespace
 			int kmin, kmax, unused;
 			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0, n_seq, kmin, unused);
 			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
-			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * n_kv,
-			                              nnchip::decode_wg_keys(head_dim, bf16));
+			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, bf16),
+			                              nnchip::decode_wg_keys(head_dim, bf16, n_kv));
 			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, nt, pos0 + t0, n_seq, window, causal, n_head,
 			                                 n_kv, head_dim, scale, sk))
 				return s;
@@ -387,9 +386,9 @@ namespace
 			            group);
 		if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
 			return fail(NNC_ERR_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
-		// The BF16 batch kernel addresses a buffer with 32-bit byte offsets.
-		if (n_tok > kSessionBatch && kv->bf16 && static_cast<uint64_t>(b.rows) * b.kv_dim * 2 > 0x7fffffffu)
-			return fail(NNC_ERR_UNSUPPORTED_MODEL, "a %d x %d BF16 buffer is too large for the batch kernel (2 GiB)",
+		// The BF16 kernels address a buffer with 32-bit byte offsets.
+		if (kv->bf16 && static_cast<uint64_t>(b.rows) * b.kv_dim * 2 > 0x7fffffffu)
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "a %d x %d BF16 buffer is too large for the GPU kernels (2 GiB)",
 			            b.rows, b.kv_dim);
 		// Every key the batch reads must still be in the buffer: the newest
 		// position written is n_seq - 1, and the buffer keeps the last `rows`.
