@@ -185,6 +185,28 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
                                  int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
                                  int32_t n_kv, int32_t head_dim, float scale);
 
+/* Bytes of the fixed per-device decode scratch of
+ * nnc_hip_attend_device_noalloc. */
+#define NNC_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* As nnc_hip_attend_device, for callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. No counterpart in the reference. The call allocates nothing
+ * (no hipMalloc, hipFree or allocating library routine): the decode kernels'
+ * partials go to a fixed array of NNC_HIP_NOALLOC_SCRATCH_BYTES in each
+ * device's memory, which the library holds until the process ends. Every
+ * call on a GPU shares that GPU's array, so calls that overlap on one GPU
+ * (caches driven from different threads at once) race on it; calls on one
+ * cache are ordered on its stream and do not. The first call on a device
+ * looks up the array's device address (no allocation).
+ * NNC_ERR_INVALID_ARGUMENT: as nnc_hip_attend_device, and when the call's
+ * partials would exceed the array (the message gives both sizes); one
+ * decode token of Qwen3-4B at 32k context needs about 1 MiB, a 16-token
+ * session batch about 16 MiB. */
+nnc_status nnc_hip_attend_device_noalloc(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok,
+                                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
+                                         int32_t n_kv, int32_t head_dim, float scale);
+
 /* As nnc_hip_attend / nnc_hip_attend_device, then Qwen3.5's output gate:
  * out[i] *= 1 / (1 + exp(-gate[i])), with gate [n_tok][n_head * head_dim]
  * F32 in the same memory as q (reference model.cpp:1759-1760,

@@ -18,9 +18,16 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
+
+// The decode partials of nnc_hip_attend_device_noalloc: a fixed array in
+// every device's global memory, held until the process ends. In host code
+// this name is only a stand-in for the symbol; its device address comes from
+// hipGetSymbolAddress, once per device (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[NNC_HIP_NOALLOC_SCRATCH_BYTES];
 
 namespace
 {
@@ -75,6 +82,20 @@ namespace
 		void* ptr = nullptr;
 		size_t bytes = 0;
 	};
+
+	// Where a call's decode partials go: a fixed array of `bytes` bytes, or
+	// (ptr null) the cache's grow-only scratch.
+	struct part_source
+	{
+		float* ptr = nullptr;
+		size_t bytes = 0;
+	};
+
+	// The device address of `scratch` on each device, looked up on the
+	// device's first no-alloc call with that device current.
+	constexpr int kMaxDevices = 64;
+	std::mutex g_scratch_mu;
+	void* g_scratch_ptr[kMaxDevices] = {};
 
 	constexpr int kAttnBlock = 256; // reference model.h:229
 	constexpr int32_t kDecodeChunk = 1024; // tokens per split-K launch
@@ -212,7 +233,7 @@ namespace
 	// on the absolute split grid of split_keys keys.
 	nnc_status decode_launch(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
 	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
-	                         int32_t head_dim, float scale, int split_keys)
+	                         int32_t head_dim, float scale, int split_keys, const part_source& src)
 	{
 		const int group = n_head / n_kv;
 		int kmin, kmax, unused;
@@ -225,8 +246,20 @@ namespace
 		const int n_split = kmax / split_keys - kmin / split_keys + 1;
 		if (n_split > nnchip::kDecodeMaxSplits)
 			return fail(NNC_ERR_IO, "decode split grid of %d splits (at most %d)", n_split, nnchip::kDecodeMaxSplits);
-		const size_t part_floats = static_cast<size_t>(n_tok) * n_kv * n_split * group * (head_dim + 4);
-		if (nnc_status s = reserve(kv, kv->part, part_floats * sizeof(float), "decode scratch")) return s;
+		const size_t part_bytes = static_cast<size_t>(n_tok) * n_kv * n_split * group * (head_dim + 4) * sizeof(float);
+		float* part = src.ptr;
+		if (part)
+		{
+			if (n_split > 1 && part_bytes > src.bytes) // (one split writes no partials)
+				return fail(NNC_ERR_INVALID_ARGUMENT,
+				            "%d tokens over %d splits need %zu bytes of decode partials; the fixed scratch holds %zu",
+				            n_tok, n_split, part_bytes, src.bytes);
+		}
+		else
+		{
+			if (nnc_status s = reserve(kv, kv->part, part_bytes, "decode scratch")) return s;
+			part = static_cast<float*>(kv->part.ptr);
+		}
 
 		nnchip::decode_params p{};
 		p.q = q;
@@ -234,7 +267,7 @@ namespace
 		p.gate = gate;
 		p.K = b.k;
 		p.V = b.v;
-		p.part = static_cast<float*>(kv->part.ptr);
+		p.part = part;
 		p.rows = b.rows;
 		p.kv_dim = b.kv_dim;
 		p.n_head = n_head;
@@ -261,7 +294,7 @@ namespace
 	// bit for bit.
 	nnc_status decode_tokens(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
 	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
-	                         int32_t head_dim, float scale)
+	                         int32_t head_dim, float scale, const part_source& src)
 	{
 		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv);
 		const int groups = nnchip::decode_groups(n_kv, kv->bf16);
@@ -288,7 +321,7 @@ namespace
 			}
 			if (nnc_status s = decode_launch(kv, b, q + t * tok_floats, out + t * tok_floats,
 			                                 gate ? gate + t * tok_floats : nullptr, u - t, pos0 + t, n_seq,
-			                                 window, causal, n_head, n_kv, head_dim, scale, sk))
+			                                 window, causal, n_head, n_kv, head_dim, scale, sk, src))
 				return s;
 			t = u;
 		}
@@ -297,7 +330,7 @@ namespace
 
 	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, const float* gate, int32_t n_tok, int32_t pos0,
 	                       int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
-	                       float scale)
+	                       float scale, const part_source& src = part_source{})
 	{
 		const kv_buffer& b = kv->bufs[buf];
 		const int group = n_head / n_kv;
@@ -317,7 +350,7 @@ namespace
 		// split-K kernel over the batch's span for F32 (exact fp32 products
 		// against F32 K/V).
 		if (n_tok <= kSessionBatch)
-			return decode_tokens(kv, b, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+			return decode_tokens(kv, b, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale, src);
 		if (bf16)
 		{
 			nnchip::prefill_params p{};
@@ -357,7 +390,7 @@ namespace
 			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, bf16),
 			                              nnchip::decode_wg_keys(head_dim, bf16, n_kv));
 			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, nt, pos0 + t0, n_seq, window, causal, n_head,
-			                                 n_kv, head_dim, scale, sk))
+			                                 n_kv, head_dim, scale, sk, src))
 				return s;
 		}
 		return NNC_OK;
@@ -628,6 +661,46 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
 	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
 		return s;
 	return attend_impl(kv, buf, q, out, nullptr, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
+}
+
+namespace
+{
+	// The device address of `scratch` on the cache's device: looked up once
+	// per device, on its first no-alloc call, with that device current.
+	nnc_status noalloc_scratch(const nnc_hip_kv* kv, void** out)
+	{
+		if (kv->device < 0 || kv->device >= kMaxDevices)
+			return fail(NNC_ERR_UNSUPPORTED_CPU, "device %d is past the library's %d-device table", kv->device, kMaxDevices);
+		std::lock_guard<std::mutex> lock(g_scratch_mu);
+		if (!g_scratch_ptr[kv->device])
+		{
+			int cur = 0;
+			NNC_HIP_TRY(hipGetDevice(&cur), "scratch lookup");
+			if (cur != kv->device) NNC_HIP_TRY(hipSetDevice(kv->device), "scratch lookup");
+			void* ptr = nullptr;
+			const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+			if (cur != kv->device) (void)hipSetDevice(cur);
+			if (e != hipSuccess) return hip_fail(e, "scratch lookup");
+			if (!ptr) return fail(NNC_ERR_IO, "scratch lookup: no device address");
+			g_scratch_ptr[kv->device] = ptr;
+		}
+		*out = g_scratch_ptr[kv->device];
+		return NNC_OK;
+	}
+}
+
+nnc_status nnc_hip_attend_device_noalloc(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok,
+                                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
+                                         int32_t n_kv, int32_t head_dim, float scale)
+{
+	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
+		return s;
+	void* ptr = nullptr;
+	if (nnc_status s = noalloc_scratch(kv, &ptr)) return s;
+	part_source src;
+	src.ptr = static_cast<float*>(ptr);
+	src.bytes = NNC_HIP_NOALLOC_SCRATCH_BYTES;
+	return attend_impl(kv, buf, q, out, nullptr, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale, src);
 }
 
 nnc_status nnc_hip_attend_gated(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out,

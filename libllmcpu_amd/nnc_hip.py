@@ -81,6 +81,7 @@ SIGNATURES = {
     "nnc_hip_kv_read": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_attend": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_device": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
+    "nnc_hip_attend_device_noalloc": (C.c_int, [_P, _I, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_gated": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_attend_gated_device": (C.c_int, [_P, _I, _P, _P, _P, _I, _I, _I, _I, _B, _I, _I, _I, _F]),
     "nnc_hip_gemv_bf16": (C.c_int, [_P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
@@ -270,6 +271,16 @@ class KVCache:
             n_seq = pos0 + n_tok
         _check(self._lib.nnc_hip_attend_device(self.handle, buf, q_dev, out_dev, n_tok, pos0, n_seq, window,
                                                bool(causal), n_head, n_kv, head_dim, float(scale)))
+
+    def attend_device_noalloc(self, buf: int, q_dev: int, out_dev: int, *, n_tok: int, pos0: int,
+                              n_seq: int | None = None, window: int = 0, causal: bool = True, n_head: int,
+                              n_kv: int, head_dim: int, scale: float) -> None:
+        """attend_device through nnc_hip_attend_device_noalloc: no device
+        allocation, the decode partials in the library's fixed per-device array."""
+        if n_seq is None:
+            n_seq = pos0 + n_tok
+        _check(self._lib.nnc_hip_attend_device_noalloc(self.handle, buf, q_dev, out_dev, n_tok, pos0, n_seq, window,
+                                                       bool(causal), n_head, n_kv, head_dim, float(scale)))
 
     def prep_append_device(self, buf: int, q_dev: int, k_dev: int, v_dev: int, *, pos0: int, n_tok: int,
                            prep: NncHipPrep) -> None:
