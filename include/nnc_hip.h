@@ -67,10 +67,11 @@ typedef struct nnc_hip_kv nnc_hip_kv;
  * stream. Mirrors model_kv_init's buffer allocation (reference
  * model.cpp:1908-1957; rows come from the same rule: n_ctx, or a ring of
  * round_up(window + n_batch, 256) rows for a sliding layer). A BF16 cache
- * also keeps an fp16 copy of every buffer, written by every append, for the
- * prefill kernel (twice the device memory; NNC_HIP_F16_SHADOW=0 in the
- * environment at creation leaves it out, and prefill then runs about 13 %
- * slower). The nnc-visible buffers stay BF16 in nnc's layout.
+ * also keeps an fp16 copy of every V buffer, written by every append, for the
+ * prefill kernel, which uses it while every value in it fits fp16 (1.5 times
+ * the device memory of K and V alone; NNC_HIP_F16_SHADOW=0 in the environment
+ * at creation leaves it out, and prefill then runs slower). The nnc-visible
+ * buffers stay BF16 in nnc's layout.
  * NNC_ERR_INVALID_ARGUMENT: n_buf <= 0, a NULL pointer, rows or kv_dim <= 0.
  * NNC_ERR_OUT_OF_MEMORY: the device allocation failed.
  * NNC_ERR_UNSUPPORTED_CPU: no usable HIP device (the nearest existing status:
@@ -84,6 +85,21 @@ void nnc_hip_kv_free(nnc_hip_kv* kv);
 /* Total device bytes held by the K/V buffers, fp16 copies included
  * (reference model.h:325, bytes). */
 uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv);
+
+/* How the cache's attend calls compute batches of more than 16 tokens.
+ * exact = false (the default): a BF16 batch runs the prefill kernel, within
+ * the parity bound of nnc's CPU result but not bit-identical to the same
+ * tokens' one-token calls. exact = true: every batch runs the split-K decode
+ * kernels with each token on the split grid of its one-token call, so a
+ * token's result has the same bits whatever batch computes it, the promise
+ * nnc's CPU path keeps (reference model.cpp:1724-1729, docs/design.md:417-419)
+ * for its n_batch-sized chunks and model_embed; prompt-sized batches then
+ * cost several times more. Batches of up to 16 tokens (every batch of a
+ * session, MTP verification included) take the exact path either way.
+ * No counterpart in the reference, whose CPU path has only the exact mode;
+ * for callers that need its bits on long batches.
+ * NNC_ERR_INVALID_ARGUMENT: kv is NULL. */
+nnc_status nnc_hip_kv_set_exact_batches(nnc_hip_kv* kv, bool exact);
 
 /* Writes n_tok rows for positions pos0 .. pos0 + n_tok - 1 into buffer
  * `buf`, position p to row p % rows, from host memory already in the cache's

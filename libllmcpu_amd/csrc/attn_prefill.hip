@@ -14,29 +14,34 @@
 //
 // The work-group first stages its Q rows through LDS (each thread loads one
 // eighth of a row once, pre-scaled into log2 units and split into bf16 hi +
-// lo); every wavefront then keeps both halves of its B operand in registers
-// (at head_dim 256 it reads them from LDS). Per step, a wavefront's 32 K rows and 32 V rows
-// arrive in its own LDS tiles by LDS-DMA (buffer_load ... lds, 16 bytes per
-// lane, rows XOR-swizzled in 16-byte slots so the reads below are
-// conflict-free), issued during the previous step:
-//   S^T = K . Q^T      v_mfma_f32_32x32x16_bf16, K rows as the A operand and
-//                      Q^T as B, hi and lo, so the product against the exact
-//                      bf16 K is near-fp32. The accumulator starts at -m (the
-//                      row's running offset), so the scores come out already
-//                      shifted. Meanwhile the VALU reads V^T back transposed
-//                      (ds_read_b64_tr_b16) and converts it to fp16 (exact up
-//                      to 65504; larger magnitudes saturate there); then both
-//                      tiles are free and the next step's loads go out;
+// lo, so two MFMAs against the exact bf16 K give near-fp32 scores); every
+// wavefront then keeps both halves of its B operand in registers (at
+// head_dim 256 it reads them from LDS). V comes from one of two copies:
+//   - an fp16 copy (exact copies of the bf16 values, kept beside the cache
+//     and used while every value in it fits fp16): P goes in fp16 rounded to
+//     nearest, one MFMA per product;
+//   - the bf16 V itself (no copy, or a value past fp16's range in it): P is
+//     split into bf16 hi + lo, two MFMAs per product, near-fp32.
+// Per step, a wavefront's 32 K rows and 32 V rows arrive in its own LDS
+// tiles by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled
+// in 16-byte slots so the reads below are conflict-free), issued during the
+// previous step:
+//   S^T = K . Q^T      v_mfma_f32_32x32x16, K rows as the A operand and Q^T
+//                      as B. The accumulator starts at -m (the row's running
+//                      offset), so the scores come out already shifted.
+//                      Meanwhile V^T is read back transposed
+//                      (ds_read_b64_tr_b16); then both tiles are free and the
+//                      next step's loads go out;
 //   softmax            in fp32 and log2 units. The offset m is raised only
 //                      when a row's scores exceed it by more than 8, so
 //                      weights stay in (0, 256] and the O rescale is rare; the
 //                      two halves of a row's 32 scores meet through
 //                      v_permlane32_swap;
-//   O^T += V^T . P^T   v_mfma_f32_32x32x16_f16 with P (fp16, rounded to
-//                      nearest) as the B operand straight from the score
-//                      registers (key order permuted to match). The row sums
-//                      l come from the same rounded P through v_dot2_f32_f16,
-//                      so numerator and denominator see identical weights.
+//   O^T += V^T . P^T   P as the B operand straight from the score registers
+//                      (key order permuted to match). In fp16 the row sums l
+//                      come from the same rounded P through v_dot2_f32_f16, so
+//                      numerator and denominator see identical weights; in
+//                      bf16 they are fp32 sums of the unrounded weights.
 // K/V are read through buffer descriptors whose range check returns zeros
 // for rows past the key range without touching memory; a range that wraps a
 // ring buffer is walked as two contiguous segments. Masking is applied only
@@ -170,13 +175,6 @@ namespace nnchip
 			__builtin_amdgcn_sched_barrier(0);
 		}
 
-		// Eight bf16 -> eight fp16, exact up to 65504.
-		__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& b)
-		{
-			return u32x4{pack_f16x2_rtz(bf16_lo(b.x), bf16_hi(b.x)), pack_f16x2_rtz(bf16_lo(b.y), bf16_hi(b.y)),
-			             pack_f16x2_rtz(bf16_lo(b.z), bf16_hi(b.z)), pack_f16x2_rtz(bf16_lo(b.w), bf16_hi(b.w))};
-		}
-
 		template <int HD, int G>
 		__global__ __launch_bounds__(64 * kWaves)
 			__attribute__((amdgpu_waves_per_eu(prefill_shape<HD>::WPE, prefill_shape<HD>::WPE))) void prefill_kernel(
@@ -236,11 +234,11 @@ namespace nnchip
 			// Byte offsets are 32-bit (the host keeps a buffer under 2 GiB).
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
-			// The fp16 shadow when the buffer has one and every value in it is
-			// exact (Q then goes in fp16 too, if it fits; see below).
-			const bool shadow = p.K16 != nullptr && __builtin_amdgcn_readfirstlane(*p.range) == 0;
-			const char* kbase = static_cast<const char*>(shadow ? p.K16 : p.K) + head_bytes;
-			const char* vbase = static_cast<const char*>(shadow ? p.V16 : p.V) + head_bytes;
+			// V's fp16 copy when the buffer has one and every value now in it
+			// fits fp16; else the bf16 V itself.
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
+			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
+			const char* vbase = static_cast<const char*>(use16 ? p.V16 : p.V) + head_bytes;
 
 			// Step i of the wavefront: its first key and the last key of its
 			// segment; its descriptors are based at the block's first row and in
@@ -304,73 +302,37 @@ namespace nnchip
 			// The first step's tiles go out before Q is read, so the latencies overlap.
 			if (n_steps > 0) load_tiles(0);
 
-			// Q, pre-scaled into log2 units, in LDS in the K tiles' layout (row r,
-			// 16-byte slot s at s ^ kswz(r)): thread t converts the eighth t % 8
-			// of row t / 8. With the shadow, Q goes in fp16 (one MFMA per product
-			// against the exact fp16 K) unless some value of the work-group's Q
-			// is past fp16's range; otherwise as bf16 hi + lo (two MFMAs against
-			// the exact bf16 K).
+			// Q, pre-scaled into log2 units and split into bf16 hi + lo (two
+			// MFMAs against the exact bf16 K give near-fp32 scores), in LDS in
+			// the K tiles' layout (row r, 16-byte slot s at s ^ kswz(r)): thread
+			// t converts the eighth t % 8 of row t / 8.
 			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kQlo);
 			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + S::kQhi);
-			constexpr int E = HD / 8; // elements per thread
-			const int qr = threadIdx.x >> 3, qseg = threadIdx.x & 7;
-			float xq[E];
-			bool q_big = false;
 			{
+				constexpr int E = HD / 8; // elements per thread
+				const int qr = threadIdx.x >> 3, qseg = threadIdx.x & 7;
 				const int grow = row0 + qr;
 				const bool ok = grow < n_rows;
 				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
 				                                  static_cast<size_t>(kvh * G + grow % G) * HD + qseg * E
 				                            : 0);
 #pragma unroll
-				for (int c = 0; c < E / 4; ++c)
+				for (int c = 0; c < E / 8; ++c)
 				{
-					const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 4 * c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-					xq[4 * c] = a.x * p.qscale;
-					xq[4 * c + 1] = a.y * p.qscale;
-					xq[4 * c + 2] = a.z * p.qscale;
-					xq[4 * c + 3] = a.w * p.qscale;
-				}
+					float xq[8];
 #pragma unroll
-				for (int e = 0; e < E; ++e) q_big |= !(fabsf(xq[e]) <= 65504.0f);
-			}
-			// Whether any thread of the work-group holds such a value: one word
-			// per wavefront in the Q lo region (written below only after every
-			// thread has read the words).
-			bool any_big = false;
-			if (shadow) // uniform over the work-group
-			{
-				uint32_t* words = reinterpret_cast<uint32_t*>(s_raw + S::kQlo);
-				const bool wave_big = __builtin_amdgcn_ballot_w64(q_big) != 0;
-				if (lane == 0) words[wave] = wave_big ? 1u : 0u;
-				__syncthreads();
-#pragma unroll
-				for (int w = 0; w < kWaves; ++w) any_big |= words[w] != 0;
-				__syncthreads();
-			}
-			const bool use16 = shadow && !any_big;
-			if (shadow && !use16)
-			{
-				// Rare: the first tiles came from the shadow; fetch the bf16 ones.
-				dma_done();
-				kbase = static_cast<const char*>(p.K) + head_bytes;
-				vbase = static_cast<const char*>(p.V) + head_bytes;
-				if (n_steps > 0) load_tiles(0);
-			}
-#pragma unroll
-			for (int c = 0; c < E / 8; ++c)
-			{
-				const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
-				if (use16)
-				{
-					const u32x4 h16 = {pack_f16x2(xq[8 * c], xq[8 * c + 1]), pack_f16x2(xq[8 * c + 2], xq[8 * c + 3]),
-					                   pack_f16x2(xq[8 * c + 4], xq[8 * c + 5]), pack_f16x2(xq[8 * c + 6], xq[8 * c + 7])};
-					*reinterpret_cast<u32x4*>(s_qhi + off) = h16;
-				}
-				else
-				{
+					for (int u = 0; u < 2; ++u)
+					{
+						const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 8 * c + 4 * u)
+						                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+						xq[4 * u] = a.x * p.qscale;
+						xq[4 * u + 1] = a.y * p.qscale;
+						xq[4 * u + 2] = a.z * p.qscale;
+						xq[4 * u + 3] = a.w * p.qscale;
+					}
+					const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
 					bf16x8 hi, lo;
-					split_bf16x8(xq + 8 * c, hi, lo);
+					split_bf16x8(xq, hi, lo);
 					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
 					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
 				}
@@ -407,8 +369,8 @@ namespace nnchip
 			const int tq = (lane >> 4) & 1, ti = lane & 15;
 			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-			// The key loop, in one of two instantiations: fp16 K, V and Q (the
-			// shadow), or bf16 K and V with Q as hi + lo.
+			// The key loop, in one of two instantiations: V in fp16 (the copy)
+			// with P in fp16, or V in bf16 with P as bf16 hi + lo.
 			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
 			{
 				constexpr bool F16 = decltype(f16_tag)::value;
@@ -418,14 +380,14 @@ namespace nnchip
 					const int kw0 = step_key(i, seg_last);
 					dma_done(); // this step's tiles have landed
 
-					// S^T - m (32 keys x 32 rows), while V^T converts to fp16: keys
+					// S^T - m (32 keys x 32 rows), while V^T is read back: keys
 					// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
 					// A wavefront in one of its MFMA phases raises its issue priority,
 					// so the other wavefront of the SIMD fills the matrix core's shadow
 					// with its softmax (measured: 4.6 % faster per prefill step).
 					__builtin_amdgcn_s_setprio(1);
 					f32x16 sc = c_init;
-					f16x8 vta[2][DBK];
+					u32x4 vta[2][DBK]; // fp16 (shadow) or bf16 elements
 					// V^T as read: lane (g, c) of a transposing read holds keys
 					// 16 c' + 4 h + g .. of the tile rows below (both halves).
 					auto vt_pair = [&](int c, int b) __attribute__((always_inline)) -> u32x4
@@ -436,64 +398,26 @@ namespace nnchip
 						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + hf);
 						return u32x4{lo.x, lo.y, hi.x, hi.y};
 					};
-					if constexpr (F16)
+					// bf16 K, Q as hi + lo: two MFMAs per 16 elements of d.
+	#pragma unroll
+					for (int t = 0; t < KT; ++t)
 					{
-						// fp16 K and Q: one MFMA per 16 elements of d; V^T is already fp16.
-					// (MFMA, two LDS reads, two VALU at a time: measured 1 % faster.)
-	#pragma unroll
-						for (int t = 0; t < KT; ++t)
+						const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
+						if constexpr (S::QREG)
 						{
-							const f16x8 a = *reinterpret_cast<const f16x8*>(kt + q_slot(t));
-							if constexpr (S::QREG)
-								sc = mfma32x32x16(a, __builtin_bit_cast(f16x8, qhi[t]), sc);
-							else
-								sc = mfma32x32x16(a, *reinterpret_cast<const f16x8*>(s_qhi + q_slot(t)), sc);
+							sc = mfma32x32x16(a, qhi[t], sc);
+							sc = mfma32x32x16(a, qlo[t], sc);
 						}
-	#pragma unroll
-						for (int c = 0; c < 2; ++c)
-	#pragma unroll
-							for (int b = 0; b < DBK; ++b) vta[c][b] = as_f16x8(vt_pair(c, b));
-	#pragma unroll
-						for (int z = 0; z < KT; ++z)
+						else
 						{
-							__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-							__builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-							__builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+							sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
+							sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
 						}
 					}
-					else
-					{
-						// bf16 K, Q as hi + lo: two MFMAs; V^T converted to fp16.
 	#pragma unroll
-						for (int t = 0; t < KT; ++t)
-						{
-							const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
-							if constexpr (S::QREG)
-							{
-								sc = mfma32x32x16(a, qhi[t], sc);
-								sc = mfma32x32x16(a, qlo[t], sc);
-							}
-							else
-							{
-								sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
-								sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
-							}
-						}
+					for (int c = 0; c < 2; ++c)
 	#pragma unroll
-						for (int c = 0; c < 2; ++c)
-	#pragma unroll
-							for (int b = 0; b < DBK; ++b) vta[c][b] = as_f16x8(bf16x8_to_f16x8(vt_pair(c, b)));
-						// One MFMA, one LDS read, five VALU instructions at a time
-						// through the QK phase (measured: 1 % faster than the
-						// compiler's order).
-	#pragma unroll
-						for (int z = 0; z < 2 * KT; ++z)
-						{
-							__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-							__builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-							__builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-						}
-					}
+						for (int b = 0; b < DBK; ++b) vta[c][b] = vt_pair(c, b);
 					__builtin_amdgcn_s_setprio(0);
 					// Both tiles are read: the next step's rows. A DMA's LDS write is
 					// not ordered after earlier LDS reads still in flight, so those
@@ -537,26 +461,51 @@ namespace nnchip
 					}
 
 					// P^T as the B operand, per 16-key half c (k-slot j holds key
-					// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row sums
-					// from the same fp16 weights.
+					// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row
+					// sums. fp16: P rounded to fp16, the sums from the same rounded
+					// weights. bf16: P split into bf16 hi + lo against the exact
+					// bf16 V^T (no fp16 range limit on V), the sums in fp32.
 	#pragma unroll
 					for (int c = 0; c < 2; ++c)
 					{
-						u32x4 pw;
-	#pragma unroll
-						for (int q = 0; q < 4; ++q)
+						if constexpr (F16)
 						{
-							// (a scalar copy: clang's bit_cast of a vector element
-							// reads element 0 whatever the index)
-							const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
-							pw[q] = w2;
-							l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
-						}
-						const f16x8 pb = as_f16x8(pw);
-						__builtin_amdgcn_s_setprio(1);
+							u32x4 pw;
 	#pragma unroll
-						for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(vta[c][b], pb, acc_o[b]);
-						__builtin_amdgcn_s_setprio(0);
+							for (int q = 0; q < 4; ++q)
+							{
+								// (a scalar copy: clang's bit_cast of a vector element
+								// reads element 0 whatever the index)
+								const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
+								pw[q] = w2;
+								l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
+							}
+							const f16x8 pb = as_f16x8(pw);
+							__builtin_amdgcn_s_setprio(1);
+	#pragma unroll
+							for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(as_f16x8(vta[c][b]), pb, acc_o[b]);
+							__builtin_amdgcn_s_setprio(0);
+						}
+						else
+						{
+							float w[8];
+	#pragma unroll
+							for (int q = 0; q < 8; ++q)
+							{
+								w[q] = fast_exp2(sc[8 * c + q]);
+								l_acc += w[q];
+							}
+							bf16x8 phi, plo;
+							split_bf16x8(w, phi, plo);
+							__builtin_amdgcn_s_setprio(1);
+	#pragma unroll
+							for (int b = 0; b < DBK; ++b)
+							{
+								acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), phi, acc_o[b]);
+								acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), plo, acc_o[b]);
+							}
+							__builtin_amdgcn_s_setprio(0);
+						}
 					}
 				}
 

@@ -104,15 +104,6 @@ namespace nnchip
 		return __builtin_bit_cast(uint32_t, h);
 	}
 
-	// Two bf16 values (as fp32) -> packed fp16 with round-toward-zero: exact
-	// for magnitudes in fp16's normal range (a bf16 significand has 8 bits,
-	// fp16's 11); larger magnitudes saturate at +-65504 instead of becoming
-	// infinities, and magnitudes below 2^-14 keep 2^-24 absolute precision.
-	__device__ __forceinline__ uint32_t pack_f16x2_rtz(float lo, float hi)
-	{
-		return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-	}
-
 	// nnc's BF16 contract (reference runtime.h:97-113): widen by a 16-bit
 	// shift, narrow with round-to-nearest-even on the bit pattern.
 	__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
@@ -175,12 +166,24 @@ namespace nnchip
 
 	// The fp16 copy of a BF16 K/V element kept for the prefill kernel (RNE;
 	// exact for every finite bf16 up to 65504 in magnitude down to 2^-14, and
-	// within 2^-25 below). Sets `bad` for a finite value past fp16's range.
-	__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint32_t b, bool& bad)
+	// within 2^-25 below). A finite value past fp16's range is stored as
+	// kF16Bad, a NaN pattern that no conversion of a bf16 value produces (its
+	// lowest mantissa bit is set, where bf16's 7 mantissa bits fill only fp16's
+	// top 7), so the copy itself records which of its elements are unusable.
+	constexpr uint16_t kF16Bad = 0x7e01;
+
+	__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint32_t b)
 	{
 		const float f = bf16_bits_to_f32(b);
-		bad |= fabsf(f) > 65504.0f && fabsf(f) < INFINITY;
+		if (fabsf(f) > 65504.0f && fabsf(f) < INFINITY) return kF16Bad;
 		return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+	}
+
+	// The change in a buffer's count of kF16Bad elements when `was` is
+	// overwritten by `now`.
+	__device__ __forceinline__ int bad_delta(uint16_t was, uint16_t now)
+	{
+		return (now == kF16Bad ? 1 : 0) - (was == kF16Bad ? 1 : 0);
 	}
 
 	// Qwen3.5's output gate on one attention output (reference

@@ -58,9 +58,8 @@ namespace nnchip
 		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		const void* K; // [rows][kv_dim]
 		const void* V;
-		const void* K16; // fp16 shadow of K and V, or null
-		const void* V16;
-		const int* range; // nonzero: some shadow value is out of fp16 range (use K and V)
+		const void* V16; // fp16 copy of V, or null
+		const int* n_bad; // elements of the copy past fp16's range (kF16Bad); not 0: use V
 		int rows, kv_dim, n_head, n_kv;
 		int n_tok, pos0, n_seq, window;
 		int causal;
@@ -81,9 +80,8 @@ namespace nnchip
 		const float* v; // [n_tok][kv_dim]
 		void* K; // the layer's buffers: [rows][kv_dim], BF16 bits or F32
 		void* V;
-		void* K16; // their fp16 shadow (BF16 buffers), or null
-		void* V16;
-		int* range; // set when a value does not fit fp16
+		void* V16; // V's fp16 copy (BF16 buffers), or null
+		int* n_bad; // the copy's count of elements past fp16's range
 		const float* q_gamma; // head_dim floats, or null: no Q norm
 		const float* k_gamma; // head_dim floats, or null: no K norm
 		const float* freq_factors; // n_rot / 2 floats, or null
@@ -99,14 +97,15 @@ namespace nnchip
 	// head rows; false for a head_dim or n_rot outside the supported range.
 	bool launch_prep(const prep_params& p, int n_tok, hipStream_t stream);
 
-	// K16, V16, range: the buffer's fp16 shadow and its out-of-range flag, or
-	// null (no shadow).
+	// V16, n_bad: the buffer's fp16 copy of V and its count of elements past
+	// fp16's range (kept up to date as elements are replaced), or null (no
+	// copy).
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
-	                       int n_tok, bool bf16, hipStream_t stream, void* K16, void* V16, int* range);
+	                       int n_tok, bool bf16, hipStream_t stream, void* V16, int* n_bad);
 
-	// The fp16 shadow of BF16 rows pos0 .. pos0 + n_tok - 1 (mod rows).
-	bool launch_shadow_rows(const void* K, const void* V, void* K16, void* V16, int* range, int rows, int kv_dim,
-	                        int pos0, int n_tok, hipStream_t stream);
+	// The fp16 copy of BF16 V rows pos0 .. pos0 + n_tok - 1 (mod rows).
+	bool launch_shadow_rows(const void* V, void* V16, int* n_bad, int rows, int kv_dim, int pos0, int n_tok,
+	                        hipStream_t stream);
 
 	bool launch_fill_normal(void* dst, uint64_t n, uint64_t seed, int norm_dim, bool bf16, hipStream_t stream);
 

@@ -11,14 +11,15 @@ namespace nnchip
 		// The KV append of reference model.cpp:1668-1691: position pos0 + t goes
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
-		// With a shadow (K16, V16 not null) the fp16 copies of the same rows
-		// are written too, and `range` is set when a value does not fit fp16.
+		// With a shadow (V16 not null) the fp16 copy of the same V rows is
+		// written too, and `n_bad` (the copy's count of elements that do not
+		// fit fp16) follows the elements replaced and written.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
-		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* K16, uint16_t* V16,
-		                                   int* range)
+		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* V16,
+		                                   int* n_bad)
 		{
 			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
-			bool bad = false;
+			int delta = 0;
 			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
 			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
 			{
@@ -28,32 +29,34 @@ namespace nnchip
 				const uint32_t kb = f32_to_bf16_bits(k_rows[i]), vb = f32_to_bf16_bits(v_rows[i]);
 				K[dst] = static_cast<uint16_t>(kb);
 				V[dst] = static_cast<uint16_t>(vb);
-				if (K16)
+				if (V16)
 				{
-					K16[dst] = bf16_to_f16_bits(kb, bad);
-					V16[dst] = bf16_to_f16_bits(vb, bad);
+					const uint16_t v16 = bf16_to_f16_bits(vb);
+					delta += bad_delta(V16[dst], v16);
+					V16[dst] = v16;
 				}
 			}
-			if (bad) *range = 1;
+			if (delta != 0) atomicAdd(n_bad, delta);
 		}
 
-		// The fp16 copies of rows pos0 .. pos0 + n_tok - 1 (mod rows) of BF16
-		// buffers written by a plain copy.
-		__global__ void shadow_rows_kernel(const uint16_t* K, const uint16_t* V, uint16_t* K16, uint16_t* V16,
-		                                   int* range, int rows, int kv_dim, int pos0, int n_tok)
+		// The fp16 copy of V rows pos0 .. pos0 + n_tok - 1 (mod rows) of a BF16
+		// buffer written by a plain copy; `n_bad` as above.
+		__global__ void shadow_rows_kernel(const uint16_t* V, uint16_t* V16,
+		                                   int* n_bad, int rows, int kv_dim, int pos0, int n_tok)
 		{
 			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
-			bool bad = false;
+			int delta = 0;
 			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
 			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
 			{
 				const int t = static_cast<int>(i / kv_dim);
 				const int c = static_cast<int>(i % kv_dim);
 				const size_t dst = static_cast<size_t>((pos0 + t) % rows) * kv_dim + c;
-				K16[dst] = bf16_to_f16_bits(K[dst], bad);
-				V16[dst] = bf16_to_f16_bits(V[dst], bad);
+				const uint16_t v16 = bf16_to_f16_bits(V[dst]);
+				delta += bad_delta(V16[dst], v16);
+				V16[dst] = v16;
 			}
-			if (bad) *range = 1;
+			if (delta != 0) atomicAdd(n_bad, delta);
 		}
 
 		__global__ void append_f32_kernel(float* K, float* V, const float* k_rows, const float* v_rows, int rows,
@@ -148,13 +151,13 @@ namespace nnchip
 	}
 
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
-	                       int n_tok, bool bf16, hipStream_t stream, void* K16, void* V16, int* range)
+	                       int n_tok, bool bf16, hipStream_t stream, void* V16, int* n_bad)
 	{
 		const size_t n = static_cast<size_t>(n_tok) * kv_dim;
 		if (bf16)
 			append_bf16_kernel<<<grid_for(n, 256), 256, 0, stream>>>(
 				static_cast<uint16_t*>(K), static_cast<uint16_t*>(V), k_rows, v_rows, rows, kv_dim, pos0, n_tok,
-				static_cast<uint16_t*>(K16), static_cast<uint16_t*>(V16), range);
+				static_cast<uint16_t*>(V16), n_bad);
 		else
 			append_f32_kernel<<<grid_for(n, 256), 256, 0, stream>>>(static_cast<float*>(K), static_cast<float*>(V), k_rows,
 			                                                         v_rows, rows, kv_dim, pos0, n_tok);
@@ -173,13 +176,13 @@ namespace nnchip
 		return true;
 	}
 
-	bool launch_shadow_rows(const void* K, const void* V, void* K16, void* V16, int* range, int rows, int kv_dim,
-	                        int pos0, int n_tok, hipStream_t stream)
+	bool launch_shadow_rows(const void* V, void* V16, int* n_bad, int rows, int kv_dim, int pos0, int n_tok,
+	                        hipStream_t stream)
 	{
 		const size_t n = static_cast<size_t>(n_tok) * kv_dim;
-		shadow_rows_kernel<<<grid_for(n, 256), 256, 0, stream>>>(
-			static_cast<const uint16_t*>(K), static_cast<const uint16_t*>(V), static_cast<uint16_t*>(K16),
-			static_cast<uint16_t*>(V16), range, rows, kv_dim, pos0, n_tok);
+		shadow_rows_kernel<<<grid_for(n, 256), 256, 0, stream>>>(static_cast<const uint16_t*>(V),
+		                                                         static_cast<uint16_t*>(V16), n_bad, rows, kv_dim,
+		                                                         pos0, n_tok);
 		return true;
 	}
 

@@ -286,18 +286,23 @@ namespace nnchip
 							static_cast<float*>(base)[off + i] = xr[j];
 					}
 				}
-				if (p.bf16 && p.K16)
+				if (p.bf16 && p.V16 && kind == 2)
 				{
-					// The fp16 shadow of the same row (from its BF16 value).
-					uint16_t* sh = static_cast<uint16_t*>(kind == 1 ? p.K16 : p.V16) + off;
-					bool bad = false;
+					// V's fp16 copy of the same row (from its BF16 value).
+					uint16_t* sh = static_cast<uint16_t*>(p.V16) + off;
+					int delta = 0;
 #pragma unroll
 					for (int j = 0; j < NJ; ++j)
 					{
 						const int i = pos(j);
-						if (i < hd) sh[i] = bf16_to_f16_bits(f32_to_bf16_bits(xr[j]), bad);
+						if (i < hd)
+						{
+							const uint16_t s16 = bf16_to_f16_bits(f32_to_bf16_bits(xr[j]));
+							delta += bad_delta(sh[i], s16);
+							sh[i] = s16;
+						}
 					}
-					if (bad) *p.range = 1;
+					if (delta != 0) atomicAdd(p.n_bad, delta);
 				}
 			}
 		}

@@ -67,10 +67,9 @@ namespace
 	{
 		void* k = nullptr;
 		void* v = nullptr;
-		// BF16 caches: fp16 copies of k and v for the prefill kernel, kept by
-		// every append (its MFMAs then take Q in fp16 and need no conversion
-		// of V); null when disabled (NNC_HIP_F16_SHADOW=0).
-		void* k16 = nullptr;
+		// BF16 caches: an fp16 copy of v for the prefill kernel, kept by every
+		// append (its P . V products then take P in fp16, one MFMA each); null
+		// when disabled (NNC_HIP_F16_SHADOW=0).
 		void* v16 = nullptr;
 		int32_t rows = 0;
 		int32_t kv_dim = 0;
@@ -120,6 +119,7 @@ struct nnc_hip_kv
 	int device = 0;
 	int n_cu = 256;
 	bool bf16 = true;
+	bool exact_batches = false; // batches over kSessionBatch tokens on the split-K path too
 	hipStream_t stream = nullptr;
 	std::vector<kv_buffer> bufs;
 	uint64_t bytes = 0;
@@ -128,7 +128,7 @@ struct nnc_hip_kv
 	dev_scratch out;
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
-	int* range = nullptr; // per buffer: nonzero once a value outside fp16's range was appended (device)
+	int* n_bad = nullptr; // per buffer: elements of the fp16 shadow now past fp16's range (device)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 };
@@ -141,10 +141,10 @@ namespace
 		if (kv->stream) (void)hipStreamSynchronize(kv->stream);
 		for (auto& b : kv->bufs)
 		{
-			for (void* ptr : {b.k, b.v, b.k16, b.v16})
+			for (void* ptr : {b.k, b.v, b.v16})
 				if (ptr) (void)hipFree(ptr);
 		}
-		if (kv->range) (void)hipFree(kv->range);
+		if (kv->n_bad) (void)hipFree(kv->n_bad);
 		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
@@ -206,9 +206,9 @@ namespace
 			            "K/V append");
 			done += n;
 		}
-		if (b.k16)
+		if (b.v16)
 		{
-			nnchip::launch_shadow_rows(b.k, b.v, b.k16, b.v16, kv->range + buf, b.rows, b.kv_dim, pos0, n_tok,
+			nnchip::launch_shadow_rows(b.v, b.v16, kv->n_bad + buf, b.rows, b.kv_dim, pos0, n_tok,
 			                           kv->stream);
 			NNC_HIP_TRY(hipGetLastError(), "K/V append");
 		}
@@ -313,7 +313,7 @@ namespace
 			int f0, l0;
 			span_of(t, f0, l0);
 			int32_t u = t + 1;
-			for (; u < n_tok && own_split(u) == sk; ++u)
+			for (; u < n_tok && u - t < kDecodeChunk && own_split(u) == sk; ++u)
 			{
 				int fu, lu;
 				span_of(u, fu, lu);
@@ -345,11 +345,11 @@ namespace
 		const int kmin = first0, kmax = last1;
 		if (kmax < kmin) return nnchip::launch_zero(out, q_floats, kv->stream) ? NNC_OK : NNC_ERR_IO;
 
-		// Decode and session-sized batches: the split-K kernel, each token on
-		// its own split grid. Larger batches: the prefill kernel for BF16, the
-		// split-K kernel over the batch's span for F32 (exact fp32 products
-		// against F32 K/V).
-		if (n_tok <= kSessionBatch)
+		// Decode and session-sized batches (and every batch in exact mode):
+		// the split-K kernel, each token on its own split grid. Larger
+		// batches: the prefill kernel for BF16, the split-K kernel over the
+		// batch's span for F32 (exact fp32 products against F32 K/V).
+		if (n_tok <= kSessionBatch || kv->exact_batches)
 			return decode_tokens(kv, b, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale, src);
 		if (bf16)
 		{
@@ -359,9 +359,8 @@ namespace
 			p.gate = gate;
 			p.K = b.k;
 			p.V = b.v;
-			p.K16 = b.k16;
 			p.V16 = b.v16;
-			p.range = b.k16 ? kv->range + buf : nullptr;
+			p.n_bad = b.v16 ? kv->n_bad + buf : nullptr;
 			p.rows = b.rows;
 			p.kv_dim = b.kv_dim;
 			p.n_head = n_head;
@@ -466,8 +465,8 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 	kv->bufs.resize(static_cast<size_t>(n_buf));
 	if (shadow)
 	{
-		e = hipMalloc(&kv->range, sizeof(int) * static_cast<size_t>(n_buf));
-		if (e == hipSuccess) e = hipMemsetAsync(kv->range, 0, sizeof(int) * static_cast<size_t>(n_buf), kv->stream);
+		e = hipMalloc(&kv->n_bad, sizeof(int) * static_cast<size_t>(n_buf));
+		if (e == hipSuccess) e = hipMemsetAsync(kv->n_bad, 0, sizeof(int) * static_cast<size_t>(n_buf), kv->stream);
 		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 	}
 	for (int32_t i = 0; i < n_buf; ++i)
@@ -482,11 +481,9 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 		if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, n, kv->stream);
 		if (shadow)
 		{
-			if (e == hipSuccess) e = hipMalloc(&b.k16, n);
 			if (e == hipSuccess) e = hipMalloc(&b.v16, n);
-			if (e == hipSuccess) e = hipMemsetAsync(b.k16, 0, n, kv->stream);
 			if (e == hipSuccess) e = hipMemsetAsync(b.v16, 0, n, kv->stream);
-			kv->bytes += 2 * n;
+			kv->bytes += n;
 		}
 		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 		kv->bytes += 2 * n;
@@ -500,6 +497,13 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 void nnc_hip_kv_free(nnc_hip_kv* kv) { release(kv); }
 
 uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv) { return kv ? kv->bytes : 0; }
+
+nnc_status nnc_hip_kv_set_exact_batches(nnc_hip_kv* kv, bool exact)
+{
+	if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL cache");
+	kv->exact_batches = exact;
+	return NNC_OK;
+}
 
 nnc_status nnc_hip_kv_append(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const void* k_rows,
                              const void* v_rows)
@@ -532,8 +536,8 @@ nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos
 {
 	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
 	const kv_buffer& b = kv->bufs[buf];
-	nnchip::launch_append_f32(b.k, b.v, k_rows, v_rows, b.rows, b.kv_dim, pos0, n_tok, kv->bf16, kv->stream, b.k16,
-	                          b.v16, b.k16 ? kv->range + buf : nullptr);
+	nnchip::launch_append_f32(b.k, b.v, k_rows, v_rows, b.rows, b.kv_dim, pos0, n_tok, kv->bf16, kv->stream, b.v16,
+	                          b.v16 ? kv->n_bad + buf : nullptr);
 	NNC_HIP_TRY(hipGetLastError(), "K/V append");
 	return NNC_OK;
 }
@@ -566,9 +570,8 @@ nnc_status nnc_hip_kv_prep_append_device(nnc_hip_kv* kv, int32_t buf, int32_t po
 	p.v = v;
 	p.K = b.k;
 	p.V = b.v;
-	p.K16 = b.k16;
 	p.V16 = b.v16;
-	p.range = b.k16 ? kv->range + buf : nullptr;
+	p.n_bad = b.v16 ? kv->n_bad + buf : nullptr;
 	p.q_gamma = pr.q_gamma;
 	p.k_gamma = pr.k_gamma;
 	p.freq_factors = pr.freq_factors;

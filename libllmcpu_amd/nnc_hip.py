@@ -74,6 +74,7 @@ SIGNATURES = {
     "nnc_hip_kv_create": (C.c_int, [_I, C.POINTER(_I), C.POINTER(_I), _B, C.POINTER(_P)]),
     "nnc_hip_kv_free": (None, [_P]),
     "nnc_hip_kv_bytes": (_U64, [_P]),
+    "nnc_hip_kv_set_exact_batches": (C.c_int, [_P, _B]),
     "nnc_hip_kv_append": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_kv_append_f32": (C.c_int, [_P, _I, _I, _I, _P, _P]),
     "nnc_hip_kv_append_f32_device": (C.c_int, [_P, _I, _I, _I, _P, _P]),
@@ -214,6 +215,11 @@ class KVCache:
     @property
     def stream(self) -> int:
         return int(self._lib.nnc_hip_kv_stream(self.handle) or 0)
+
+    def set_exact_batches(self, exact: bool) -> None:
+        """Batches over 16 tokens on the split-K path too, each token with the
+        bits of its one-token call (default False: the prefill kernel)."""
+        _check(self._lib.nnc_hip_kv_set_exact_batches(self.handle, bool(exact)))
 
     def append(self, buf: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
         """Rows already in the cache's element type: uint16 BF16 bits, or float32."""

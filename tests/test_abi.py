@@ -90,6 +90,7 @@ def test_calls_on_a_null_cache_are_refused(lib):
     assert lib.nnc_hip_kv_sync(None) == nh.NncStatus.INVALID_ARGUMENT
     assert lib.nnc_hip_kv_bytes(None) == 0
     assert lib.nnc_hip_kv_stream(None) is None
+    assert lib.nnc_hip_kv_set_exact_batches(None, True) == nh.NncStatus.INVALID_ARGUMENT
     lib.nnc_hip_kv_free(None)  # a no-op
     assert lib.nnc_hip_fill_normal(None, 10, 1, 0, False, None) == nh.NncStatus.INVALID_ARGUMENT
     assert lib.nnc_hip_fill_normal(q.ctypes.data, 10, 1, 3, False, None) == nh.NncStatus.INVALID_ARGUMENT

@@ -58,3 +58,42 @@ def test_batch_matches_one_token_calls_bitwise(orc, cfg, layer, pos0, n):
     err = float(np.abs(batch.astype(np.float64) - want).max())
     print(f"  bitwise equal; max-abs vs oracle {err:.3e}", flush=True)
     assert err <= cfg.tol
+
+
+EXACT_CASES = [
+    # (config, layer, first position, batch): batches past 16 tokens in exact mode
+    (synth.CONFIGS["D"], 0, 3584, 512),  # Qwen3-4B: the last 512-token chunk of a 4096 prompt
+    (synth.CONFIGS["C"], 0, 5000, 300),  # Gemma-3-1B local layer: ring, window 512
+    (synth.CONFIGS["E"], 5, 2000, 64),  # Gemma-3-4B global layer, hd 256, group 2
+    (synth.CONFIGS["A"], 0, 1000, 40),  # F32 K/V
+]
+
+
+@pytest.mark.parametrize("cfg,layer,pos0,n", EXACT_CASES, ids=[f"{c.name}-{l}-{p}+{n}" for c, l, p, n in EXACT_CASES])
+def test_exact_mode_long_batch_matches_one_token_calls_bitwise(orc, cfg, layer, pos0, n):
+    """With nnc_hip_kv_set_exact_batches, a chunk of n_batch tokens (nnc's
+    prompt chunks, reference tests.cpp:2607) gives every token the bits of its
+    one-token call, as nnc's CPU path does (model.cpp:1724-1729); the default
+    mode's prefill kernel stays within the parity bound instead."""
+    n_seq = pos0 + n
+    window = cfg.layer_window(layer)
+    rows = cfg.layer_rows(layer, n_seq, n)
+    K, V = synth.cache_buffer(cfg, layer, rows, n_seq)
+    q = synth.qk_rows(cfg, layer, 0, np.arange(pos0, n_seq), cfg.n_head)
+    kw = dict(window=window, causal=True, n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim,
+              scale=cfg.attn_scale)
+    print(f"case exact mode {cfg.name} layer {layer}: tokens {pos0}+{n}, rows {rows}, window {window}", flush=True)
+    with nh.KVCache([rows], [cfg.kv_dim], bf16=cfg.kv_bf16) as kv:
+        kv.append(0, 0, K, V)
+        fast = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+        kv.set_exact_batches(True)
+        batch = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+        single = np.stack([kv.attend(0, q[t:t + 1], pos0=pos0 + t, n_seq=pos0 + t + 1, **kw)[0]
+                           for t in range(n)])
+    differ = [t for t in range(n) if not np.array_equal(batch[t].view(np.uint32), single[t].view(np.uint32))]
+    assert not differ, f"tokens whose batch bits differ from their one-token call: {differ[:20]}"
+    want = orc.attend_layer(q, K, V, kv_bf16=cfg.kv_bf16, rows=rows, pos0=pos0, n_seq=n_seq, **kw)
+    err = float(np.abs(batch.astype(np.float64) - want).max())
+    err_fast = float(np.abs(fast.astype(np.float64) - want).max())
+    print(f"  bitwise equal; max-abs vs oracle {err:.3e} (default mode {err_fast:.3e})", flush=True)
+    assert err <= cfg.tol and err_fast <= cfg.tol
