@@ -65,10 +65,25 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+BOX_CPU_SHARE = 16  # host CPUs one GPU's jobs may use on the GPU boxes
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(kv, target_s: float) -> dict:
     """nnc's CPU attention on this host: one Qwen3-4B layer at 32768 keys,
-    repeated for about target_s seconds (threads = min(8, nproc), the
-    reference default)."""
+    repeated for about target_s seconds per setting, at the reference's two
+    thread settings: min(8, nproc) (its default, reference nn_ops.cpp:865-879)
+    and nproc capped at 64 (nn_ops.cpp:786), the latter also held to the
+    CPUs this process may use. The first is the reported value."""
     import oracle
 
     K, V = kv.read(0, 0, CTX)
@@ -76,29 +91,39 @@ def cpu_baseline(kv, target_s: float) -> dict:
     q = rng.standard_normal((1, N_HEAD * HD)).astype(np.float32)
     q /= np.sqrt((q.reshape(N_HEAD, HD) ** 2).mean(axis=1)).repeat(HD)[None, :]
     nproc = os.cpu_count() or 1
-    threads = min(8, nproc)
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
     kw = dict(kv_bf16=True, rows=CTX, pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
-    if oracle.reference_available():
-        lib = oracle.Reference()
-        lib.set_threads(threads)
-        kind = "reference"
-        run = lambda: lib.attend_layer(q, K, V, **kw)  # noqa: E731
-    else:
-        lib = oracle.Oracle()
-        kind = "port"
-        run = lambda: lib.attend_layer(q, K, V, threads=threads, **kw)  # noqa: E731
-    run()
-    n, t0 = 0, time.perf_counter()
-    best = float("inf")
-    while time.perf_counter() - t0 < target_s:
-        t = time.perf_counter()
+    ref = oracle.reference_available()
+    lib = oracle.Reference() if ref else oracle.Oracle()
+    kind = "reference" if ref else "port"
+
+    def timed_run(threads):
+        if ref:
+            lib.set_threads(threads)
+            run = lambda: lib.attend_layer(q, K, V, **kw)  # noqa: E731
+        else:
+            run = lambda: lib.attend_layer(q, K, V, threads=threads, **kw)  # noqa: E731
         run()
-        best = min(best, time.perf_counter() - t)
-        n += 1
-    gbs = decode_bytes(CTX) / best / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+        n, t0 = 0, time.perf_counter()
+        best = float("inf")
+        while time.perf_counter() - t0 < target_s:
+            t = time.perf_counter()
+            run()
+            best = min(best, time.perf_counter() - t)
+            n += 1
+        return decode_bytes(CTX) / best / 1e9, n
+
+    t_default = min(8, nproc)
+    t_all = min(64, nproc, usable, BOX_CPU_SHARE)
+    gbs, n = timed_run(t_default)
+    gbs_all, n_all = timed_run(t_all)
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": t_default, "kind": kind,
             "sample": f"decode of one Qwen3-4B layer at {CTX} keys, best of {n} runs over {target_s:.0f} s "
-                      f"(nproc {nproc}; the reference's kernels and worker pool)"}
+                      f"(the reference's kernels and worker pool)",
+            "cpu": cpu_model(), "nproc": nproc, "usable_cpus": usable,
+            "all_cores": {"value": round(gbs_all, 2), "cores": t_all, "runs": n_all,
+                          "threads_rule": f"min(64, nproc) held to the usable CPUs and the box's "
+                                          f"{BOX_CPU_SHARE}-CPU share per GPU"}}
 
 
 def pmc_summary(fetch_csv: str, write_csv: str) -> dict:
@@ -216,18 +241,175 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
             "kernels": "gemv_vec_kernel (one vector), gemv_kernel + gemv_reduce_kernel (batches)", **res}
 
 
+def decode_layer_bytes(span: int, n_kv: int, hd: int, n_head: int, esize: int) -> int:
+    """Algorithmic bytes of one decode call: K and V over the span, q in and out."""
+    return 2 * span * n_kv * hd * esize + 2 * n_head * hd * 4
+
+
+def layer_spans(cfg, layer: int, pos0: int, n_tok: int) -> np.ndarray:
+    """Keys each query of a causal batch sees (a window caps local layers)."""
+    pos = np.arange(pos0, pos0 + n_tok, dtype=np.int64)
+    w = cfg.layer_window(layer)
+    return np.minimum(pos + 1, w) if w > 0 else pos + 1
+
+
+def configs_bench(nh, hip_rt, synth) -> dict:
+    """The benchmark's other configurations (A, B, C, D at 4096, E), each
+    step replayed from a HIP graph of its attend calls so the small layers are
+    timed by the GPU rather than by Python's launch rate. Inputs come from
+    the device generator (K RMS-normed per head where the model normalises
+    it); every layer's buffer holds the positions the step reads (a sliding
+    layer's ring the last `rows` of them). A replay is checked bit for bit
+    against an eager run of the same calls. Algorithmic work per the
+    decode-bytes and prefill-flops formulas of the headline line."""
+    import ctypes as C
+
+    lib = nh.load_library()
+    out = {}
+
+    def build(cfg, n_ctx, n_batch):
+        rows = [cfg.layer_rows(li, n_ctx, n_batch) for li in range(cfg.n_layer)]
+        kv = nh.KVCache(rows, [cfg.kv_dim] * cfg.n_layer, bf16=cfg.kv_bf16)
+        st = kv.stream
+        n_max = max(rows) * cfg.kv_dim
+        k_dev, v_dev = hip_rt.malloc(4 * n_max), hip_rt.malloc(4 * n_max)
+        for li, r in enumerate(rows):
+            seed = (synth.BASE_SEED + 1000 * cfg.index + li) * 256
+            nh.fill_normal(k_dev, r * cfg.kv_dim, seed + 1, cfg.head_dim if cfg.qk_norm else 0, False, st)
+            nh.fill_normal(v_dev, r * cfg.kv_dim, seed + 2, 0, False, st)
+            first = n_ctx - r  # the ring keeps the newest rows
+            status = lib.nnc_hip_kv_append_f32_device(kv.handle, li, first, r, C.c_void_p(k_dev), C.c_void_p(v_dev))
+            if status:
+                raise nh.NncError(status, lib.nnc_hip_last_error().decode())
+        kv.sync()
+        hip_rt.free(k_dev)
+        hip_rt.free(v_dev)
+        return kv
+
+    def measure(kv, calls, n_tok_max, n_out, cfg, reps):
+        """calls: (layer, out slot, pos0, n_tok) tuples of one step."""
+        st = kv.stream
+        width = cfg.n_head * cfg.head_dim
+        q = hip_rt.malloc(4 * n_tok_max * width)
+        o = hip_rt.malloc(4 * n_out * n_tok_max * width)
+        nh.fill_normal(q, n_tok_max * width, 4242 + cfg.index, cfg.head_dim if cfg.qk_norm else 0, False, st)
+
+        def step():
+            for li, slot, pos0, n in calls:
+                kv.attend_device(li, q, o + 4 * slot * n_tok_max * width, n_tok=n, pos0=pos0,
+                                 window=cfg.layer_window(li), n_head=cfg.n_head, n_kv=cfg.n_kv,
+                                 head_dim=cfg.head_dim, scale=cfg.attn_scale)
+
+        step()  # eager: scratch grows here, never inside the capture
+        kv.sync()
+        eager = hip_rt.to_host(np.empty(n_out * n_tok_max * width, np.float32), o)
+        graph = hip_rt.Graph(st, step)
+        graph.launch(st)
+        kv.sync()
+        e0, e1 = hip_rt.Event(), hip_rt.Event()
+        e0.record(st)
+        for _ in range(reps):
+            graph.launch(st)
+        e1.record(st)
+        e1.synchronize()
+        ms = e1.ms_since(e0) / reps
+        replay = hip_rt.to_host(np.empty_like(eager), o)
+        graph.close()
+        same = bool(np.array_equal(eager.view(np.uint32), replay.view(np.uint32)))
+        hip_rt.free(q)
+        hip_rt.free(o)
+        return ms, same
+
+    def decode_entry(cfg, label, kv, ctx, reps=20):
+        calls = [(li, li, ctx - 1, 1) for li in range(cfg.n_layer)]
+        ms, same = measure(kv, calls, 1, cfg.n_layer, cfg, reps)
+        esize = 2 if cfg.kv_bf16 else 4
+        nbytes = sum(decode_layer_bytes(int(layer_spans(cfg, li, ctx - 1, 1)[0]), cfg.n_kv, cfg.head_dim, cfg.n_head,
+                                        esize) for li in range(cfg.n_layer))
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[label] = {"workload": f"{cfg.name}: one decode token at {ctx} keys through {cfg.n_layer} layers",
+                      "ms_per_step": round(ms, 4), "bytes_per_step": nbytes, "value": round(gbs, 1), "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "replay_equals_eager": same}
+        log(f"[bench] {label}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s")
+
+    def prefill_entry(cfg, label, kv, n_prompt, chunk, reps=3):
+        calls = [(li, c, c * chunk, chunk) for li in range(cfg.n_layer) for c in range(n_prompt // chunk)]
+        ms, same = measure(kv, calls, chunk, n_prompt // chunk, cfg, reps)
+        flops = sum(int(4 * cfg.head_dim * cfg.n_head * layer_spans(cfg, li, 0, n_prompt).sum())
+                    for li in range(cfg.n_layer))
+        tf = flops / (ms * 1e-3) / 1e12
+        out[label] = {"workload": f"{cfg.name}: a {n_prompt}-token prompt in {chunk}-token chunks through "
+                                  f"{cfg.n_layer} layers", "ms_per_step": round(ms, 3), "flops_per_step": flops,
+                      "value": round(tf, 1), "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                      "replay_equals_eager": same}
+        log(f"[bench] {label}: {ms:.3f} ms/step, {tf:.0f} TFLOP/s")
+
+    A, B, Cc, E = (synth.CONFIGS[k] for k in "ABCE")
+    kv = build(A, 1024, 1)
+    decode_entry(A, "A_decode_1024", kv, 1024, reps=50)
+    out["A_decode_1024"]["note"] = "18 x 2 MB of K/V stay in the 256 MB Infinity Cache: not an HBM rate"
+    kv.close()
+    kv = build(B, 16384, 1)
+    for ctx in (512, 4096, 16384):
+        decode_entry(B, f"B_decode_{ctx}", kv, ctx)
+    kv.close()
+    kv = build(Cc, 8192, 2048)
+    decode_entry(Cc, "C_decode_8192", kv, 8192)
+    prefill_entry(Cc, "C_prefill_8192", kv, 8192, 2048)
+    kv.close()
+    n_ctx = 16384 + 256
+    kv = build(E, n_ctx, 1024)
+    prefill_entry(E, "E_prefill_16384", kv, 16384, 1024, reps=2)
+    # 256 decode steps after the prompt, one graph
+    calls = [(li, li, p, 1) for p in range(16384, n_ctx) for li in range(E.n_layer)]
+    ms, same = measure(kv, calls, 1, E.n_layer, E, 2)
+    nbytes = sum(decode_layer_bytes(int(layer_spans(E, li, p, 1)[0]), E.n_kv, E.head_dim, E.n_head, 2)
+                 for p in range(16384, n_ctx) for li in range(E.n_layer))
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out["E_decode_256"] = {"workload": f"{E.name}: 256 decode steps after a 16384-token prompt, {E.n_layer} layers",
+                           "ms_per_step": round(ms / 256, 4), "bytes_per_step": nbytes // 256, "value": round(gbs, 1),
+                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "replay_equals_eager": same}
+    log(f"[bench] E_decode_256: {ms / 256 * 1e3:.1f} us/step, {gbs:.0f} GB/s")
+    kv.close()
+    return out
+
+
+def host_path_bench(nh, kv) -> dict:
+    """One decode layer through nnc_hip_attend (q and out in host memory, the
+    call synchronous), as a drop-in caller at reference model.cpp:1693-1757
+    would make it; wall time per call, ctypes overhead included."""
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, N_HEAD * HD)).astype(np.float32)
+    kw = dict(pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+    for li in range(N_LAYER):
+        kv.attend(li, q, **kw)
+    n = 0
+    t0 = time.perf_counter()
+    for _ in range(5):
+        for li in range(N_LAYER):
+            kv.attend(li, q, **kw)
+            n += 1
+    us = (time.perf_counter() - t0) * 1e6 / n
+    return {"what": "one Qwen3-4B decode layer at 32768 keys through nnc_hip_attend: q staged through pinned "
+                    "memory, out copied back, the call synchronous (Python ctypes call included)",
+            "us_per_call": round(us, 2), "gbs": round(decode_bytes(CTX) / (us * 1e-6) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--prefill-steps", type=int, default=3)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "batch", "gemv"], default=None,
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations (A, B, C, E)")
+    ap.add_argument("--only", choices=["decode", "prefill", "batch", "gemv", "configs"], default=None,
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
                     help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
+    ap.add_argument("--prefill-traffic", default=str(ROOT / "profiles" / "prefill_counters.json"),
+                    help="rocprofv3 --pmc summary giving HBM bytes per prefill launch")
     ap.add_argument("--calibrate", action="store_true",
                     help=f"start with a {CALIBRATE_MIB} MiB copy kernel (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -324,6 +506,12 @@ def main() -> int:
     if args.only == "gemv":
         log(f"[bench] gemv {json.dumps(gemv_bench(nh, hip_rt, kv, stream, timed))}")
         return 0
+    if args.only == "configs":
+        kv.close()
+        from libllmcpu_amd import synth
+
+        log(f"[bench] configs {json.dumps(configs_bench(nh, hip_rt, synth))}")
+        return 0
     if args.only == "batch":
         batch_step()
         hip_rt.sync()
@@ -403,18 +591,34 @@ def main() -> int:
     gemv_res = gemv_bench(nh, hip_rt, kv, stream, timed)
     log(f"[bench] gemv {json.dumps(gemv_res)}")
 
-    traffic = None
-    tp = Path(args.traffic)
-    if tp.exists():
-        try:
-            traffic = json.loads(tp.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, AttributeError):
-            traffic = None
+    def traffic_of(path):
+        tp = Path(path)
+        if tp.exists():
+            try:
+                return json.loads(tp.read_text()).get("hbm_bytes_per_launch")
+            except (ValueError, AttributeError):
+                return None
+        return None
+
+    traffic = traffic_of(args.traffic)
+    pre_traffic = traffic_of(args.prefill_traffic)
+
+    log("[bench] host-buffer decode path")
+    host_res = host_path_bench(nh, kv)
+    log(f"[bench] host path {host_res['us_per_call']} us/call")
 
     cpu = None
     if not args.no_cpu:
-        log(f"[bench] cpu baseline ~{args.cpu_seconds:.0f} s")
+        log(f"[bench] cpu baseline ~{args.cpu_seconds:.0f} s per setting")
         cpu = cpu_baseline(kv, args.cpu_seconds)
+    kv.close()
+
+    configs = None
+    if not args.no_configs:
+        from libllmcpu_amd import synth
+
+        log("[bench] other configurations")
+        configs = configs_bench(nh, hip_rt, synth)
 
     line = {
         "metric": METRIC,
@@ -441,7 +645,7 @@ def main() -> int:
                     "workload": f"qwen3-4b prefill of {PROMPT} tokens in {CHUNK}-token chunks, 36 layers",
                     "roofline": {"bound": "mfma", "achieved": round(pre_launch_tflops, 1),
                                  "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                 "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                                 "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": pre_traffic,
                                  "kernel": "prefill_kernel<128,4> (bf16 hi+lo QK, fp16 PV MFMA, fp32 accumulate)",
                                  "avg_launch_us": round(pre_launch_us, 3)}},
         "session_batch": {"what": f"one {SESSION_BATCH}-token forward pass of an nnc session (its batch size, "
@@ -455,12 +659,13 @@ def main() -> int:
                               "unit": "GB/s", "frac": round(prep_res["chunk"]["gbs"] / HBM_PEAK_GBS, 4),
                               "kernel": "prep_kernel (512-token chunk)"}},
         "gemv": gemv_res,
+        "host_path": host_res,
+        "configs": configs,
         "cpu_baseline": cpu,
         "device": {"cu": n_cu, "clock_mhz": clock_mhz},
         "wall_ms": {"decode": round(dec_wall, 2), "prefill": round(pre_wall, 2)},
     }
     print(json.dumps(line), flush=True)
-    kv.close()
     for p in (q_dec, o_dec, q_pre, o_pre):
         hip_rt.free(p)
     return 0

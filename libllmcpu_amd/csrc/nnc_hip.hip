@@ -82,6 +82,17 @@ namespace
 		size_t bytes = 0;
 	};
 
+	// Pinned host memory (hipHostMalloc) through which the host-buffer entry
+	// points move rows, so every copy is a DMA from page-locked memory and the
+	// caller's buffers are free on return. `free` is recorded after the last
+	// copy that reads the buffer; the host waits on it before writing again.
+	struct host_staging
+	{
+		void* ptr = nullptr;
+		size_t bytes = 0;
+		hipEvent_t free = nullptr;
+	};
+
 	// Where a call's decode partials go: a fixed array of `bytes` bytes, or
 	// (ptr null) the cache's grow-only scratch.
 	struct part_source
@@ -124,13 +135,14 @@ struct nnc_hip_kv
 	std::vector<kv_buffer> bufs;
 	uint64_t bytes = 0;
 	dev_scratch part; // decode partials
-	dev_scratch q; // staging of host q / out / append rows
+	dev_scratch q; // device copies of host q / gate / out and append rows
 	dev_scratch out;
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
-	int* n_bad = nullptr; // per buffer: elements of the fp16 shadow now past fp16's range (device)
+	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now past fp16's range (device)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
+	host_staging pinned; // host rows in and out (q, gate, out; K/V appends)
 };
 
 namespace
@@ -147,6 +159,8 @@ namespace
 		if (kv->n_bad) (void)hipFree(kv->n_bad);
 		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v})
 			if (s->ptr) (void)hipFree(s->ptr);
+		if (kv->pinned.ptr) (void)hipHostFree(kv->pinned.ptr);
+		if (kv->pinned.free) (void)hipEventDestroy(kv->pinned.free);
 		if (kv->stream) (void)hipStreamDestroy(kv->stream);
 		delete kv;
 	}
@@ -163,6 +177,33 @@ namespace
 		const size_t n = (std::max<size_t>(bytes, 256) + 255) & ~static_cast<size_t>(255);
 		NNC_HIP_TRY(hipMalloc(&s.ptr, n), what);
 		s.bytes = n;
+		return NNC_OK;
+	}
+
+	// Makes the pinned staging at least `bytes` long and free to write (every
+	// earlier copy out of it has completed).
+	nnc_status reserve_pinned(nnc_hip_kv* kv, size_t bytes, const char* what)
+	{
+		host_staging& h = kv->pinned;
+		if (h.free) NNC_HIP_TRY(hipEventSynchronize(h.free), what);
+		if (h.bytes >= bytes) return NNC_OK;
+		if (h.ptr) NNC_HIP_TRY(hipHostFree(h.ptr), what);
+		h.ptr = nullptr;
+		h.bytes = 0;
+		const size_t n = (std::max<size_t>(bytes, 64 << 10) + 4095) & ~static_cast<size_t>(4095);
+		NNC_HIP_TRY(hipHostMalloc(&h.ptr, n, hipHostMallocDefault), what);
+		h.bytes = n;
+		return NNC_OK;
+	}
+
+	// Host rows -> device memory through the pinned staging (asynchronous on
+	// the cache's stream; the host rows are free on return).
+	nnc_status upload(nnc_hip_kv* kv, void* dst, const void* src, size_t bytes, const char* what)
+	{
+		if (nnc_status s = reserve_pinned(kv, bytes, what)) return s;
+		std::memcpy(kv->pinned.ptr, src, bytes);
+		NNC_HIP_TRY(hipMemcpyAsync(dst, kv->pinned.ptr, bytes, hipMemcpyHostToDevice, kv->stream), what);
+		NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), what);
 		return NNC_OK;
 	}
 
@@ -459,6 +500,7 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 	hipError_t e = hipGetDevice(&kv->device);
 	if (e == hipSuccess) e = hipDeviceGetAttribute(&kv->n_cu, hipDeviceAttributeMultiprocessorCount, kv->device);
 	if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking);
+	if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->pinned.free, hipEventDisableTiming);
 	if (e != hipSuccess) return bail(hip_fail(e, "device setup"));
 	const size_t esize = bf16 ? 2 : 4;
 	const bool shadow = bf16 && f16_shadow_enabled();
@@ -509,13 +551,16 @@ nnc_status nnc_hip_kv_append(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t 
                              const void* v_rows)
 {
 	if (nnc_status s = check_append(kv, buf, pos0, n_tok, k_rows, v_rows)) return s;
-	// Stage through device scratch so the host rows are free on return.
+	// Through the pinned staging, straight into the buffer's rows, so the
+	// host rows are free on return.
 	const size_t bytes = static_cast<size_t>(n_tok) * kv->bufs[buf].kv_dim * (kv->bf16 ? 2 : 4);
-	if (nnc_status s = reserve(kv, kv->rows_k, bytes, "append staging")) return s;
-	if (nnc_status s = reserve(kv, kv->rows_v, bytes, "append staging")) return s;
-	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_k.ptr, k_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
-	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_v.ptr, v_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
-	return append_raw(kv, buf, pos0, n_tok, kv->rows_k.ptr, kv->rows_v.ptr, hipMemcpyDeviceToDevice);
+	if (nnc_status s = reserve_pinned(kv, 2 * bytes, "append staging")) return s;
+	char* pk = static_cast<char*>(kv->pinned.ptr);
+	std::memcpy(pk, k_rows, bytes);
+	std::memcpy(pk + bytes, v_rows, bytes);
+	if (nnc_status s = append_raw(kv, buf, pos0, n_tok, pk, pk + bytes, hipMemcpyHostToDevice)) return s;
+	NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), "K/V append");
+	return NNC_OK;
 }
 
 nnc_status nnc_hip_kv_append_f32(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int32_t n_tok, const float* k_rows,
@@ -525,8 +570,13 @@ nnc_status nnc_hip_kv_append_f32(nnc_hip_kv* kv, int32_t buf, int32_t pos0, int3
 	const size_t bytes = static_cast<size_t>(n_tok) * kv->bufs[buf].kv_dim * sizeof(float);
 	if (nnc_status s = reserve(kv, kv->rows_k, bytes, "append staging")) return s;
 	if (nnc_status s = reserve(kv, kv->rows_v, bytes, "append staging")) return s;
-	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_k.ptr, k_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
-	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_v.ptr, v_rows, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	if (nnc_status s = reserve_pinned(kv, 2 * bytes, "append staging")) return s;
+	char* pk = static_cast<char*>(kv->pinned.ptr);
+	std::memcpy(pk, k_rows, bytes);
+	std::memcpy(pk + bytes, v_rows, bytes);
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_k.ptr, pk, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	NNC_HIP_TRY(hipMemcpyAsync(kv->rows_v.ptr, pk + bytes, bytes, hipMemcpyHostToDevice, kv->stream), "K/V append");
+	NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), "K/V append");
 	return nnc_hip_kv_append_f32_device(kv, buf, pos0, n_tok, static_cast<const float*>(kv->rows_k.ptr),
 	                                    static_cast<const float*>(kv->rows_v.ptr));
 }
@@ -622,8 +672,9 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
 
 namespace
 {
-	// The host-buffer form of the op: q (and gate) staged to the device, out
-	// downloaded, the call synchronous with respect to out.
+	// The host-buffer form of the op: q (and gate) staged to the device
+	// through pinned memory, out downloaded through it, the call synchronous
+	// with respect to out.
 	nnc_status attend_host(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out, int32_t n_tok,
 	                       int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
 	                       int32_t head_dim, float scale)
@@ -638,14 +689,26 @@ namespace
 		if (nnc_status s = reserve(kv, kv->out, bytes, "out staging")) return s;
 		if (gate)
 			if (nnc_status s = reserve(kv, kv->gate, bytes, "gate staging")) return s;
-		NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, q, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
-		if (gate) NNC_HIP_TRY(hipMemcpyAsync(kv->gate.ptr, gate, bytes, hipMemcpyHostToDevice, kv->stream), "gate upload");
+		// pinned: q, then gate; out comes back over q once the call is done
+		if (nnc_status s = reserve_pinned(kv, gate ? 2 * bytes : bytes, "q staging")) return s;
+		char* pq = static_cast<char*>(kv->pinned.ptr);
+		std::memcpy(pq, q, bytes);
+		NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, pq, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
+		if (gate)
+		{
+			std::memcpy(pq + bytes, gate, bytes);
+			NNC_HIP_TRY(hipMemcpyAsync(kv->gate.ptr, pq + bytes, bytes, hipMemcpyHostToDevice, kv->stream), "gate upload");
+		}
 		if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), static_cast<float*>(kv->out.ptr),
 		                               gate ? static_cast<const float*>(kv->gate.ptr) : nullptr, n_tok, pos0, n_seq,
 		                               window, causal, n_head, n_kv, head_dim, scale))
+		{
+			(void)hipStreamSynchronize(kv->stream); // the staging is read until the uploads finish
 			return s;
-		NNC_HIP_TRY(hipMemcpyAsync(out, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
+		}
+		NNC_HIP_TRY(hipMemcpyAsync(pq, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
 		NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "attention");
+		std::memcpy(out, pq, bytes);
 		return NNC_OK;
 	}
 }

@@ -1,5 +1,6 @@
-"""A few HIP runtime calls through ctypes (device memory, copies, events),
-for the benchmark and the tests; the attention op itself is in libnnc_hip.so."""
+"""A few HIP runtime calls through ctypes (device memory, copies, events,
+graphs), for the benchmark and the tests; the attention op itself is in
+libnnc_hip.so."""
 from __future__ import annotations
 
 import ctypes as C
@@ -23,6 +24,13 @@ def hip() -> C.CDLL:
         h.hipEventDestroy.argtypes = [C.c_void_p]
         h.hipGetErrorString.restype = C.c_char_p
         h.hipDeviceGetAttribute.argtypes = [C.POINTER(C.c_int), C.c_int, C.c_int]
+        h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        h.hipGraphDestroy.argtypes = [C.c_void_p]
+        h.hipStreamSynchronize.argtypes = [C.c_void_p]
         _hip = h
     return _hip
 
@@ -89,5 +97,42 @@ class Event:
     def __del__(self):
         try:
             hip().hipEventDestroy(self.e)
+        except Exception:
+            pass
+
+
+class Graph:
+    """The kernel launches `fn()` issues on `stream`, captured once into a HIP
+    graph (thread-local capture: any allocation or synchronisation inside
+    fn() fails the capture) and replayed with launch(). fn() must not record
+    memset nodes."""
+
+    def __init__(self, stream: int, fn):
+        h = hip()
+        check(h.hipStreamBeginCapture(stream, 1), "hipStreamBeginCapture")
+        g = C.c_void_p()
+        try:
+            fn()
+        finally:
+            err = h.hipStreamEndCapture(stream, C.byref(g))
+        check(err, "hipStreamEndCapture")
+        self.graph = g
+        self.exec = C.c_void_p()
+        check(h.hipGraphInstantiate(C.byref(self.exec), g, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self, stream: int) -> None:
+        check(hip().hipGraphLaunch(self.exec, stream), "hipGraphLaunch")
+
+    def close(self) -> None:
+        if self.exec:
+            hip().hipGraphExecDestroy(self.exec)
+            self.exec = C.c_void_p()
+        if self.graph:
+            hip().hipGraphDestroy(self.graph)
+            self.graph = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
