@@ -4,13 +4,16 @@
 //
 // Rows of the problem are (token, query head) pairs of one KV head, token
 // major, so the heads of a GQA group sit in adjacent rows and share every key
-// the work-group reads. Grid: n_kv * n_qtiles work-groups of 4 wavefronts; a
-// work-group owns 32 rows and walks its key range in steps of 128 keys,
-// wavefront w taking keys 32w .. 32w + 31 of each step for all 32 rows, so
-// every product is one 32 x 32 tile (v_mfma_f32_32x32x16, which one
-// wavefront keeps near the matrix peak). Each wavefront therefore reads a
-// disjoint quarter of the keys, keeps its own online softmax, and the four
-// partial results merge once, in LDS, at the end.
+// the work-group reads. Grid: n_kv * n_qtiles work-groups. A work-group owns
+// RG row groups of 32 rows (RG = 2 at head_dim 64 and 128: 64 rows, eight
+// wavefronts, one work-group per CU; RG = 1 at head_dim 256: 32 rows, four
+// wavefronts) and walks its key range in steps of 128 keys. Wavefront
+// (g, r) takes keys 32 g .. 32 g + 31 of each step for the 32 rows of row
+// group r, so every product is one 32 x 32 tile (v_mfma_f32_32x32x16, which
+// one wavefront keeps near the matrix peak); the row groups share each key
+// group's K and V tiles, which halves the bytes loaded per product. Each
+// wavefront keeps its own online softmax, and the four key groups of a row
+// group merge once, in LDS, at the end.
 //
 // The work-group first stages its Q rows through LDS (each thread loads one
 // eighth of a row once, pre-scaled into log2 units and split into bf16 hi +
@@ -22,16 +25,16 @@
 //     nearest, one MFMA per product;
 //   - the bf16 V itself (no copy, or a value past fp16's range in it): P is
 //     split into bf16 hi + lo, two MFMAs per product, near-fp32.
-// Per step, a wavefront's 32 K rows and 32 V rows arrive in its own LDS
-// tiles by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled
-// in 16-byte slots so the reads below are conflict-free), issued during the
-// previous step:
+// Per step, a key group's 32 K rows and 32 V rows arrive in its LDS tiles
+// by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled in
+// 16-byte slots so the reads below are conflict-free), issued during the
+// previous step (RG = 2: two stages, the DMAs split between the row groups,
+// one barrier per step; RG = 1: each wavefront's own tiles, one stage):
 //   S^T = K . Q^T      v_mfma_f32_32x32x16, K rows as the A operand and Q^T
 //                      as B. The accumulator starts at -m (the row's running
 //                      offset), so the scores come out already shifted.
 //                      Meanwhile V^T is read back transposed
-//                      (ds_read_b64_tr_b16); then both tiles are free and the
-//                      next step's loads go out;
+//                      (ds_read_b64_tr_b16) into registers;
 //   softmax            in fp32 and log2 units. The offset m is raised only
 //                      when a row's scores exceed it by more than 8, so
 //                      weights stay in (0, 256] and the O rescale is rare; the
@@ -53,25 +56,32 @@
 
 #include <type_traits>
 
+
+
 namespace nnchip
 {
 	namespace
 	{
-		constexpr int kWaves = 4; // wavefronts per work-group (key quarters of a step)
+		constexpr int kKG = 4; // key groups: the key quarters of a step
 		constexpr int kWK = 32; // keys per wavefront per step (one MFMA tile)
-		constexpr int kStep = kWaves * kWK; // keys per work-group step
-		constexpr int kRows = 32; // rows per work-group
+		constexpr int kStep = kKG * kWK; // keys per work-group step
 		constexpr float kLazy = 8.0f; // max growth of a row's scores over its offset, log2 units
 		constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3: raw 32-bit data
 
-		// LDS: the wavefronts' K and V tiles, Q's lo half, Q's hi half (staged
-		// once, then the merge's row statistics); the merge buffer reuses the
-		// tiles and the lo half. At head_dim 128 this is 80 KiB, so two
-		// work-groups (two wavefronts per SIMD) share a CU.
-		template <int HD>
+		// A work-group is RG row groups of 32 rows times kKG key groups, one
+		// wavefront each; the row groups of a key group share its K and V
+		// tiles. LDS: the K and V tiles (RG = 2: two stages, double-buffered),
+		// Q's lo half, Q's hi half (staged once); the merge buffer reuses the
+		// tiles and Q, and the merge's row statistics sit at kStats. RG = 1 at
+		// head_dim 128 is 80 KiB, so two work-groups (two wavefronts per SIMD)
+		// share a CU; RG = 2 is 160 KiB, one work-group of eight wavefronts.
+		template <int HD, int RG>
 		struct prefill_shape
 		{
-			static constexpr int WPE = HD == 256 ? 1 : 2; // wavefronts per SIMD
+			static constexpr int WAVES = kKG * RG;
+			static constexpr int ROWS = 32 * RG; // rows per work-group
+			static constexpr int STAGES = RG == 1 ? 1 : 2;
+			// wavefronts per SIMD: HD == 256 ? 1 : 2 (in the kernel's attributes)
 			// Q's B operand (hi and lo halves) held in registers; at head_dim 256
 			// it would not fit beside the accumulators, and is read from LDS.
 			static constexpr bool QREG = HD != 256;
@@ -82,15 +92,19 @@ namespace nnchip
 			static constexpr int NV = kWK / KPL; // DMAs per tile per step
 			static constexpr int OPITCH = HD + 4; // floats per row in the final merge
 			static constexpr int kTile = kWK * HD * 2; // bytes of one K (or V) tile
-			static constexpr int kTiles = kWaves * 2 * kTile;
-			static constexpr int kQ = kRows * HD * 2; // bytes of one bf16 half of Q
+			static constexpr int kStage = kKG * 2 * kTile; // the tiles of one step
+			static constexpr int kTiles = STAGES * kStage;
+			static constexpr int kQ = ROWS * HD * 2; // bytes of one bf16 half of Q
 			static constexpr int kQlo = kTiles; // offsets
 			static constexpr int kQhi = kTiles + kQ;
 			static constexpr int kLds = kTiles + 2 * kQ;
-			static constexpr int kOBytes = kWaves * kRows * OPITCH * 4;
-			static_assert(NV >= 1 && KPL * NV == kWK, "unsupported prefill shape");
-			static_assert(kOBytes <= kQhi && 2 * kWaves * kRows * 4 <= kQ, "merge buffer layout");
+			static constexpr int kStatBytes = 2 * WAVES * 32 * 4;
+			static constexpr int kStats = RG == 1 ? kQhi : kLds - kStatBytes;
+			static constexpr int kOBytes = WAVES * 32 * OPITCH * 4;
+			static_assert(NV >= 1 && KPL * NV == kWK && NV % RG == 0, "unsupported prefill shape");
+			static_assert(kOBytes <= kStats && kStats + kStatBytes <= kLds, "merge buffer layout");
 			static_assert(kLds <= 160 * 1024, "prefill LDS budget");
+			static_assert(RG == 1 || QREG, "two row groups need Q in registers (the Q region is reused)");
 		};
 
 		// Two 16-bit halves of one row of O^T's A operand: lane (g, c) of the
@@ -175,18 +189,20 @@ namespace nnchip
 			__builtin_amdgcn_sched_barrier(0);
 		}
 
-		template <int HD, int G>
-		__global__ __launch_bounds__(64 * kWaves)
-			__attribute__((amdgpu_waves_per_eu(prefill_shape<HD>::WPE, prefill_shape<HD>::WPE))) void prefill_kernel(
+		template <int HD, int G, int RG>
+		__global__ __launch_bounds__(64 * kKG * RG)
+			__attribute__((amdgpu_waves_per_eu(HD == 256 ? 1 : 2, HD == 256 ? 1 : 2))) void prefill_kernel(
 				const prefill_params p)
 		{
-			using S = prefill_shape<HD>;
+			using S = prefill_shape<HD, RG>;
 			constexpr int KT = S::KT, DBK = S::DBK, LPK = S::LPK, KPL = S::KPL, NV = S::NV, OPITCH = S::OPITCH;
+			constexpr int kWaves = S::WAVES, kRows = S::ROWS;
 
 			__shared__ __attribute__((aligned(16))) unsigned char s_raw[S::kLds];
 
 			const int lane = threadIdx.x & 63;
 			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: keeps step control scalar
+			const int kg = wave % kKG, rg = wave / kKG; // this wavefront's key group and row group
 			const int r32 = lane & 31; // this lane's row of the tile (and key, as an A-operand row)
 			const int h = lane >> 5; // which half of an MFMA's k range this lane holds
 
@@ -216,7 +232,7 @@ namespace nnchip
 				attn_span(p.causal, p.window, p.pos0 + t1, p.n_seq, first_hi, kmax);
 			}
 			// This lane's row and its span.
-			const int my_row = row0 + r32;
+			const int my_row = row0 + 32 * rg + r32;
 			int rfirst = 1, rlast = 0; // no key
 			if (my_row < n_rows) attn_span(p.causal, p.window, p.pos0 + my_row / G, p.n_seq, rfirst, rlast);
 
@@ -247,7 +263,7 @@ namespace nnchip
 			{
 				const bool second = i >= n1;
 				seg_last = second ? kmax : wrap_key - 1;
-				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + wave * kWK;
+				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + kg * kWK;
 			};
 			// In bytes from the buffer's start: the wavefront's block at step i
 			// is at seg_off + i * step_bytes (seg_off per segment: the block of
@@ -255,8 +271,8 @@ namespace nnchip
 			// at seg_end (its last row's head slice included). Everything stays
 			// below 2^32 since a buffer is under 2 GiB.
 			const uint32_t step_bytes = static_cast<uint32_t>(kStep) * row_bytes;
-			const uint32_t seg1_off = static_cast<uint32_t>(rb0 + wave * kWK) * row_bytes;
-			const uint32_t seg2_off = static_cast<uint32_t>(wave * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
+			const uint32_t seg1_off = static_cast<uint32_t>(rb0 + kg * kWK) * row_bytes;
+			const uint32_t seg2_off = static_cast<uint32_t>(kg * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
 			const uint32_t seg1_end = static_cast<uint32_t>(rb0 + len1 - 1) * row_bytes + HD * 2;
 			const uint32_t seg2_end = static_cast<uint32_t>(kmax - wrap_key) * row_bytes + HD * 2; // used when len2 > 0
 			auto step_rsrc = [&](int i, const char* base) __attribute__((always_inline))
@@ -274,31 +290,40 @@ namespace nnchip
 			// Tile layout: DMA j fills tile rows j KPL .. + KPL, lane l the 16
 			// bytes at l * 16, i.e. row j KPL + l / LPK, slot l % LPK, which holds
 			// the row's 16-byte segment (l % LPK) ^ swizzle(row).
+			// The row groups of a key group split its DMAs: row group rg issues
+			// DMAs rg NV / RG .. of each tile.
 			const int t_row = lane / LPK;
-			uint16_t* kt = reinterpret_cast<uint16_t*>(s_raw) + wave * 2 * kWK * HD;
-			uint16_t* vt = kt + kWK * HD;
-			auto load_tiles = [&](int i) __attribute__((always_inline))
+			auto k_tile = [&](int i) __attribute__((always_inline)) -> uint16_t*
+			{
+				return reinterpret_cast<uint16_t*>(s_raw + (S::STAGES == 2 ? (i & 1) : 0) * S::kStage) +
+				       kg * 2 * kWK * HD;
+			};
+			// DMAs e0 .. e1 - 1 of this wavefront's 2 ND for step i: its K DMAs,
+			// then its V DMAs (so a step's loads can be spread over the step).
+			constexpr int ND = NV / RG;
+			auto load_part = [&](int i, int e0, int e1) __attribute__((always_inline))
 			{
 				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
 				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
+				uint16_t* kt = k_tile(i);
+				uint16_t* vt = kt + kWK * HD;
 				// Each group of four DMAs shares one LDS base (the instruction
 				// offset moves the LDS and buffer addresses alike), so the K tile,
 				// then the V tile, needs one LDS base per 4 KiB.
 #pragma unroll
-				for (int jj = 0; jj < NV; ++jj)
+				for (int e = e0; e < e1; ++e)
 				{
+					const bool is_v = e >= ND;
+					const int jj = rg * ND + (is_v ? e - ND : e);
 					const int row = jj * KPL + t_row;
 					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
-				}
-#pragma unroll
-				for (int jj = 0; jj < NV; ++jj)
-				{
-					const int row = jj * KPL + t_row;
-					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
+					if (is_v)
+						load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
+					else
+						load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
 				}
 			};
+			auto load_tiles = [&](int i) __attribute__((always_inline)) { load_part(i, 0, 2 * ND); };
 			// The first step's tiles go out before Q is read, so the latencies overlap.
 			if (n_steps > 0) load_tiles(0);
 
@@ -349,8 +374,8 @@ namespace nnchip
 #pragma unroll
 				for (int t = 0; t < KT; ++t)
 				{
-					qhi[t] = *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t));
-					qlo[t] = *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t));
+					qhi[t] = *reinterpret_cast<const bf16x8*>(s_qhi + 32 * rg * HD + q_slot(t));
+					qlo[t] = *reinterpret_cast<const bf16x8*>(s_qlo + 32 * rg * HD + q_slot(t));
 				}
 			}
 
@@ -369,146 +394,181 @@ namespace nnchip
 			const int tq = (lane >> 4) & 1, ti = lane & 15;
 			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-			// The key loop, in one of two instantiations: V in fp16 (the copy)
-			// with P in fp16, or V in bf16 with P as bf16 hi + lo.
-			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
+			// V^T as read: lane (g, c) of a transposing read holds keys
+			// 16 c' + 4 h + g .. of the tile rows below (both halves).
+			auto vt_pair = [&](const uint16_t* vt, int c, int b) __attribute__((always_inline)) -> u32x4
+			{
+				const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), hf = 4 * (ti & 1);
+				const int ra = 16 * c + 4 * h + (ti >> 2), rb = ra + 8;
+				const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + hf);
+				const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + hf);
+				return u32x4{lo.x, lo.y, hi.x, hi.y};
+			};
+
+			// S^T - m (32 keys x 32 rows) of step i, and its V^T read back: keys
+			// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j. A
+			// wavefront in one of its MFMA phases raises its issue priority, so
+			// the other wavefront of the SIMD fills the matrix core's shadow with
+			// its softmax (measured: 4.6 % faster per prefill step).
+			auto qk_phase = [&](int i, f32x16& sc, u32x4 (&vta)[2][DBK]) __attribute__((always_inline))
+			{
+				const uint16_t* kt = k_tile(i);
+				const uint16_t* vt = kt + kWK * HD;
+				__builtin_amdgcn_s_setprio(1);
+				sc = c_init;
+				// bf16 K, Q as hi + lo: two MFMAs per 16 elements of d.
+#pragma unroll
+				for (int t = 0; t < KT; ++t)
+				{
+					const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
+					if constexpr (S::QREG)
+					{
+						sc = mfma32x32x16(a, qhi[t], sc);
+						sc = mfma32x32x16(a, qlo[t], sc);
+					}
+					else
+					{
+						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + 32 * rg * HD + q_slot(t)), sc);
+						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + 32 * rg * HD + q_slot(t)), sc);
+					}
+				}
+#pragma unroll
+				for (int c = 0; c < 2; ++c)
+#pragma unroll
+					for (int b = 0; b < DBK; ++b) vta[c][b] = vt_pair(vt, c, b);
+				__builtin_amdgcn_s_setprio(0);
+			};
+
+			// Masking, the online softmax and O^T += V^T . P^T of one step whose
+			// scores and V^T are in registers.
+			auto soft_phase = [&](auto f16_tag, int kw0, int seg_last, f32x16 sc, const u32x4 (&vta)[2][DBK])
+				__attribute__((always_inline))
 			{
 				constexpr bool F16 = decltype(f16_tag)::value;
+				// Mask keys outside the row's span or past the segment (only on
+				// steps that cross an edge).
+				if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
+				{
+					const int hi_key = min(rlast, seg_last);
+#pragma unroll
+					for (int e = 0; e < 16; ++e)
+					{
+						const int k = kw0 + 8 * (e / 4) + 4 * h + (e % 4);
+						if (k < rfirst || k > hi_key) sc[e] = -INFINITY;
+					}
+				}
+
+				// Raise the row's offset when its scores outgrow it by more than
+				// kLazy (or on its first visible key): rare, and O's rescale with it.
+				float mx = sc[0];
+#pragma unroll
+				for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+				mx = max_with_other_half(mx);
+				const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
+				if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
+				{
+					const bool fresh = m_off == -INFINITY;
+					const float d = grow ? mx : 0.0f;
+					const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
+					if (grow) m_off = (fresh ? 0.0f : m_off) + d;
+					const float ci = m_off == -INFINITY ? 0.0f : -m_off;
+#pragma unroll
+					for (int e = 0; e < 16; ++e) c_init[e] = ci;
+#pragma unroll
+					for (int b = 0; b < DBK; ++b) acc_o[b] *= alpha;
+					l_acc *= alpha;
+					sc -= d;
+				}
+
+				// P^T as the B operand, per 16-key half c (k-slot j holds key
+				// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row
+				// sums. fp16: P rounded to fp16, the sums from the same rounded
+				// weights. bf16: P split into bf16 hi + lo against the exact
+				// bf16 V^T (no fp16 range limit on V), the sums in fp32.
+#pragma unroll
+				for (int c = 0; c < 2; ++c)
+				{
+					if constexpr (F16)
+					{
+						u32x4 pw;
+#pragma unroll
+						for (int q = 0; q < 4; ++q)
+						{
+							// (a scalar copy: clang's bit_cast of a vector element
+							// reads element 0 whatever the index)
+							const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
+							pw[q] = w2;
+							l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
+						}
+						const f16x8 pb = as_f16x8(pw);
+						__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+						for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(as_f16x8(vta[c][b]), pb, acc_o[b]);
+						__builtin_amdgcn_s_setprio(0);
+					}
+					else
+					{
+						float w[8];
+#pragma unroll
+						for (int q = 0; q < 8; ++q)
+						{
+							w[q] = fast_exp2(sc[8 * c + q]);
+							l_acc += w[q];
+						}
+						bf16x8 phi, plo;
+						split_bf16x8(w, phi, plo);
+						__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+						for (int b = 0; b < DBK; ++b)
+						{
+							acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), phi, acc_o[b]);
+							acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), plo, acc_o[b]);
+						}
+						__builtin_amdgcn_s_setprio(0);
+					}
+				}
+			};
+
+			// The key loop, in one of two instantiations: V in fp16 (the copy)
+			// with P in fp16, or V in bf16 with P as bf16 hi + lo. With two row
+			// groups the next step's K DMAs go out right after the step's
+			// barrier and its V DMAs after the QK phase, so the address unit's
+			// work is spread over the step (placements from all at the barrier
+			// to all after the QK phase measured within 2 % of each other).
+			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
+			{
 				for (int i = 0; i < n_steps; ++i)
 				{
 					int seg_last;
 					const int kw0 = step_key(i, seg_last);
-					dma_done(); // this step's tiles have landed
-
-					// S^T - m (32 keys x 32 rows), while V^T is read back: keys
-					// 16 c + 4 h + j and 16 c + 8 + 4 h + j in k-slots j and 4 + j.
-					// A wavefront in one of its MFMA phases raises its issue priority,
-					// so the other wavefront of the SIMD fills the matrix core's shadow
-					// with its softmax (measured: 4.6 % faster per prefill step).
-					__builtin_amdgcn_s_setprio(1);
-					f32x16 sc = c_init;
-					u32x4 vta[2][DBK]; // fp16 (shadow) or bf16 elements
-					// V^T as read: lane (g, c) of a transposing read holds keys
-					// 16 c' + 4 h + g .. of the tile rows below (both halves).
-					auto vt_pair = [&](int c, int b) __attribute__((always_inline)) -> u32x4
+					dma_done(); // this step's tiles (this wavefront's DMAs) have landed
+					if constexpr (RG > 1)
 					{
-						const int slot = 4 * b + 2 * tq + ((ti & 3) >> 1), hf = 4 * (ti & 1);
-						const int ra = 16 * c + 4 * h + (ti >> 2), rb = ra + 8;
-						const u32x2 lo = tr_read(vt + ra * HD + 8 * (slot ^ vswz<HD>(ra)) + hf);
-						const u32x2 hi = tr_read(vt + rb * HD + 8 * (slot ^ vswz<HD>(rb)) + hf);
-						return u32x4{lo.x, lo.y, hi.x, hi.y};
-					};
-					// bf16 K, Q as hi + lo: two MFMAs per 16 elements of d.
-	#pragma unroll
-					for (int t = 0; t < KT; ++t)
+						// Every wavefront's DMAs of this step have landed, and every
+						// wavefront is done with the other stage (read in the last
+						// step): the next step's loads go there.
+						lds_reads_done();
+						__syncthreads();
+						if (i + 1 < n_steps) load_part(i + 1, 0, ND);
+					}
+					f32x16 sc;
+					u32x4 vta[2][DBK]; // fp16 (the copy) or bf16 elements
+					qk_phase(i, sc, vta);
+					if (i + 1 < n_steps)
 					{
-						const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + q_slot(t));
-						if constexpr (S::QREG)
-						{
-							sc = mfma32x32x16(a, qhi[t], sc);
-							sc = mfma32x32x16(a, qlo[t], sc);
-						}
+						if constexpr (RG > 1)
+							load_part(i + 1, ND, 2 * ND);
 						else
 						{
-							sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qhi + q_slot(t)), sc);
-							sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + q_slot(t)), sc);
+							// Both tiles are read: the next step's rows. A DMA's LDS
+							// write is not ordered after earlier LDS reads still in
+							// flight, so those complete first.
+							lds_reads_done();
+							load_tiles(i + 1);
 						}
 					}
-	#pragma unroll
-					for (int c = 0; c < 2; ++c)
-	#pragma unroll
-						for (int b = 0; b < DBK; ++b) vta[c][b] = vt_pair(c, b);
-					__builtin_amdgcn_s_setprio(0);
-					// Both tiles are read: the next step's rows. A DMA's LDS write is
-					// not ordered after earlier LDS reads still in flight, so those
-					// complete first.
-					lds_reads_done();
-					if (i + 1 < n_steps) load_tiles(i + 1);
-
-					// Mask keys outside the row's span or past the segment (only on
-					// steps that cross an edge).
-					if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
-					{
-						const int hi_key = min(rlast, seg_last);
-	#pragma unroll
-						for (int e = 0; e < 16; ++e)
-						{
-							const int k = kw0 + 8 * (e / 4) + 4 * h + (e % 4);
-							if (k < rfirst || k > hi_key) sc[e] = -INFINITY;
-						}
-					}
-
-					// Raise the row's offset when its scores outgrow it by more than
-					// kLazy (or on its first visible key): rare, and O's rescale with it.
-					float mx = sc[0];
-	#pragma unroll
-					for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
-					mx = max_with_other_half(mx);
-					const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
-					if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
-					{
-						const bool fresh = m_off == -INFINITY;
-						const float d = grow ? mx : 0.0f;
-						const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
-						if (grow) m_off = (fresh ? 0.0f : m_off) + d;
-						const float ci = m_off == -INFINITY ? 0.0f : -m_off;
-	#pragma unroll
-						for (int e = 0; e < 16; ++e) c_init[e] = ci;
-	#pragma unroll
-						for (int b = 0; b < DBK; ++b) acc_o[b] *= alpha;
-						l_acc *= alpha;
-						sc -= d;
-					}
-
-					// P^T as the B operand, per 16-key half c (k-slot j holds key
-					// 16 c + 8 (j / 4) + 4 h + j % 4, as in V^T above), and the row
-					// sums. fp16: P rounded to fp16, the sums from the same rounded
-					// weights. bf16: P split into bf16 hi + lo against the exact
-					// bf16 V^T (no fp16 range limit on V), the sums in fp32.
-	#pragma unroll
-					for (int c = 0; c < 2; ++c)
-					{
-						if constexpr (F16)
-						{
-							u32x4 pw;
-	#pragma unroll
-							for (int q = 0; q < 4; ++q)
-							{
-								// (a scalar copy: clang's bit_cast of a vector element
-								// reads element 0 whatever the index)
-								const uint32_t w2 = pack_f16x2(fast_exp2(sc[8 * c + 2 * q]), fast_exp2(sc[8 * c + 2 * q + 1]));
-								pw[q] = w2;
-								l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
-							}
-							const f16x8 pb = as_f16x8(pw);
-							__builtin_amdgcn_s_setprio(1);
-	#pragma unroll
-							for (int b = 0; b < DBK; ++b) acc_o[b] = mfma32x32x16(as_f16x8(vta[c][b]), pb, acc_o[b]);
-							__builtin_amdgcn_s_setprio(0);
-						}
-						else
-						{
-							float w[8];
-	#pragma unroll
-							for (int q = 0; q < 8; ++q)
-							{
-								w[q] = fast_exp2(sc[8 * c + q]);
-								l_acc += w[q];
-							}
-							bf16x8 phi, plo;
-							split_bf16x8(w, phi, plo);
-							__builtin_amdgcn_s_setprio(1);
-	#pragma unroll
-							for (int b = 0; b < DBK; ++b)
-							{
-								acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), phi, acc_o[b]);
-								acc_o[b] = mfma32x32x16(as_bf16x8(vta[c][b]), plo, acc_o[b]);
-							}
-							__builtin_amdgcn_s_setprio(0);
-						}
-					}
+					soft_phase(f16_tag, kw0, seg_last, sc, vta);
 				}
-
 			};
 			if (use16)
 				key_loop(std::true_type{});
@@ -519,34 +579,37 @@ namespace nnchip
 			// 0 when no key was seen (reference nn_ops.cpp:492). The row
 			// statistics take the place of Q's hi half, the partial results that
 			// of the tiles.
-			float* s_m = reinterpret_cast<float*>(s_raw + S::kQhi); // [kWaves][kRows]
-			float* s_l = s_m + kWaves * kRows;
+			float* s_m = reinterpret_cast<float*>(s_raw + S::kStats); // [kWaves][32]
+			float* s_l = s_m + kWaves * 32;
 			const float l_row = add_with_other_half(l_acc);
 			// Every wavefront has left the key loop: the tiles are read (no DMA
 			// is left: the last step issues none) and so is Q's hi half.
 			__syncthreads();
 			if (h == 0)
 			{
-				s_m[wave * kRows + r32] = m_off;
-				s_l[wave * kRows + r32] = l_row;
+				s_m[wave * 32 + r32] = m_off;
+				s_l[wave * 32 + r32] = l_row;
 			}
 			__syncthreads();
 			float* s_o = reinterpret_cast<float*>(s_raw);
 			{
-				float M = s_m[r32];
+				// the key groups of this wavefront's row group: wavefronts rg kKG + w
+				const float* sm = s_m + rg * kKG * 32 + r32;
+				const float* sl = s_l + rg * kKG * 32 + r32;
+				float M = sm[0];
 #pragma unroll
-				for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w * kRows + r32]);
+				for (int w = 1; w < kKG; ++w) M = fmaxf(M, sm[w * 32]);
 				float L = 0.0f, f_own = 0.0f;
 #pragma unroll
-				for (int w = 0; w < kWaves; ++w)
+				for (int w = 0; w < kKG; ++w)
 				{
-					const float mw = s_m[w * kRows + r32];
+					const float mw = sm[w * 32];
 					const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
-					L = fmaf(s_l[w * kRows + r32], f, L);
-					if (w == wave) f_own = f;
+					L = fmaf(sl[w * 32], f, L);
+					if (w == kg) f_own = f;
 				}
 				const float sc_own = L > 0.0f ? f_own / L : 0.0f;
-				float* orow = s_o + (wave * kRows + r32) * OPITCH + 4 * h;
+				float* orow = s_o + (wave * 32 + r32) * OPITCH + 4 * h;
 #pragma unroll
 				for (int b = 0; b < DBK; ++b)
 #pragma unroll
@@ -562,11 +625,13 @@ namespace nnchip
 				const int r = idx / Q4, d4 = idx % Q4;
 				const int gr = row0 + r;
 				if (gr >= n_rows) continue;
-				float4 acc = *reinterpret_cast<const float4*>(s_o + r * OPITCH + 4 * d4);
+				// row r is row r % 32 of row group r / 32, kept by its kKG wavefronts
+				const float* o0 = s_o + ((r / 32) * kKG * 32 + r % 32) * OPITCH + 4 * d4;
+				float4 acc = *reinterpret_cast<const float4*>(o0);
 #pragma unroll
-				for (int w = 1; w < kWaves; ++w)
+				for (int w = 1; w < kKG; ++w)
 				{
-					const float4 v = *reinterpret_cast<const float4*>(s_o + (w * kRows + r) * OPITCH + 4 * d4);
+					const float4 v = *reinterpret_cast<const float4*>(o0 + w * 32 * OPITCH);
 					acc.x += v.x;
 					acc.y += v.y;
 					acc.z += v.z;
@@ -584,16 +649,18 @@ namespace nnchip
 			}
 		}
 
-		template <int HD>
-		bool launch_hd(const prefill_params& p, int group, hipStream_t stream)
+		template <int HD, int RG>
+		bool launch_hd(prefill_params p, int group, hipStream_t stream)
 		{
-			const dim3 grid(p.n_qtiles * p.n_kv), block(64 * kWaves);
+			using S = prefill_shape<HD, RG>;
+			p.n_qtiles = (p.n_tok * group + S::ROWS - 1) / S::ROWS;
+			const dim3 grid(p.n_qtiles * p.n_kv), block(64 * S::WAVES);
 			switch (group)
 			{
-			case 1: prefill_kernel<HD, 1><<<grid, block, 0, stream>>>(p); return true;
-			case 2: prefill_kernel<HD, 2><<<grid, block, 0, stream>>>(p); return true;
-			case 4: prefill_kernel<HD, 4><<<grid, block, 0, stream>>>(p); return true;
-			case 8: prefill_kernel<HD, 8><<<grid, block, 0, stream>>>(p); return true;
+			case 1: prefill_kernel<HD, 1, RG><<<grid, block, 0, stream>>>(p); return true;
+			case 2: prefill_kernel<HD, 2, RG><<<grid, block, 0, stream>>>(p); return true;
+			case 4: prefill_kernel<HD, 4, RG><<<grid, block, 0, stream>>>(p); return true;
+			case 8: prefill_kernel<HD, 8, RG><<<grid, block, 0, stream>>>(p); return true;
 			default: return false;
 			}
 		}
@@ -602,12 +669,11 @@ namespace nnchip
 	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream)
 	{
 		if (!bf16) return false;
-		p.n_qtiles = (p.n_tok * group + kRows - 1) / kRows;
 		switch (head_dim)
 		{
-		case 64: return launch_hd<64>(p, group, stream);
-		case 128: return launch_hd<128>(p, group, stream);
-		case 256: return launch_hd<256>(p, group, stream);
+		case 64: return launch_hd<64, 2>(p, group, stream);
+		case 128: return launch_hd<128, 2>(p, group, stream);
+		case 256: return launch_hd<256, 1>(p, group, stream);
 		default: return false;
 		}
 	}
