@@ -63,14 +63,24 @@ namespace
 		if (e_ != hipSuccess) return hip_fail(e_, what);                                                             \
 	} while (0)
 
+	// V starts kVOffset bytes into its allocation, so a K row and its V row
+	// do not start on the same HBM channel. Measured on Qwen3-4B decode at
+	// 32 768 keys (one box, fresh processes): 28.83 us per layer with K and V
+	// aligned alike, 28.55 with V 256 bytes in, 28.75 with 512, 28.54 with
+	// 768; a bare stream of the same head slices: the slices at bytes 256 and
+	// 1280 of each row finish 15 % after the others when aligned alike.
+	constexpr size_t kVOffset = 256;
+
 	struct kv_buffer
 	{
 		void* k = nullptr;
-		void* v = nullptr;
+		void* v = nullptr; // v_alloc + kVOffset
 		// BF16 caches: an fp16 copy of v for the prefill kernel, kept by every
 		// append (its P . V products then take P in fp16, one MFMA each); null
-		// when disabled (NNC_HIP_F16_SHADOW=0).
+		// when disabled (NNC_HIP_F16_SHADOW=0). v16_alloc + kVOffset.
 		void* v16 = nullptr;
+		void* v_alloc = nullptr;
+		void* v16_alloc = nullptr;
 		int32_t rows = 0;
 		int32_t kv_dim = 0;
 	};
@@ -153,7 +163,7 @@ namespace
 		if (kv->stream) (void)hipStreamSynchronize(kv->stream);
 		for (auto& b : kv->bufs)
 		{
-			for (void* ptr : {b.k, b.v, b.v16})
+			for (void* ptr : {b.k, b.v_alloc, b.v16_alloc})
 				if (ptr) (void)hipFree(ptr);
 		}
 		if (kv->n_bad) (void)hipFree(kv->n_bad);
@@ -518,12 +528,14 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 		b.kv_dim = kv_dim[i];
 		const size_t n = static_cast<size_t>(rows[i]) * kv_dim[i] * esize;
 		e = hipMalloc(&b.k, n);
-		if (e == hipSuccess) e = hipMalloc(&b.v, n);
+		if (e == hipSuccess) e = hipMalloc(&b.v_alloc, n + kVOffset);
+		if (e == hipSuccess) b.v = static_cast<char*>(b.v_alloc) + kVOffset;
 		if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, n, kv->stream);
 		if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, n, kv->stream);
 		if (shadow)
 		{
-			if (e == hipSuccess) e = hipMalloc(&b.v16, n);
+			if (e == hipSuccess) e = hipMalloc(&b.v16_alloc, n + kVOffset);
+			if (e == hipSuccess) b.v16 = static_cast<char*>(b.v16_alloc) + kVOffset;
 			if (e == hipSuccess) e = hipMemsetAsync(b.v16, 0, n, kv->stream);
 			kv->bytes += n;
 		}
