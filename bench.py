@@ -126,12 +126,15 @@ def cpu_baseline(kv, target_s: float) -> dict:
                                           f"{BOX_CPU_SHARE}-CPU share per GPU"}}
 
 
-def pmc_summary(fetch_csv: str, write_csv: str) -> dict:
-    """HBM bytes per decode call from two `rocprofv3 --pmc` runs of
-    `bench.py --only decode --calibrate` (FETCH_SIZE, then WRITE_SIZE, both
-    in KiB per dispatch). The copy of CALIBRATE_MIB MiB that such a run
+def pmc_summary(fetch_csv: str, write_csv: str, kind: str = "decode") -> dict:
+    """HBM bytes per attend call from two `rocprofv3 --pmc` runs of
+    `bench.py --only decode|prefill --calibrate` (FETCH_SIZE, then WRITE_SIZE,
+    both in KiB per dispatch). The copy of CALIBRATE_MIB MiB that such a run
     starts with reads and writes exactly that many bytes, which converts each
-    counter to bytes."""
+    counter to bytes. decode: one call is decode_bf16_kernel +
+    decode_merge_kernel at 32768 keys; prefill: one call is one
+    prefill_kernel launch, averaged over the 8 chunks of the 4096-token
+    prompt (chunk c reads keys 0 .. 512 c + 511)."""
     import csv
 
     def per_kernel(path):
@@ -139,24 +142,63 @@ def pmc_summary(fetch_csv: str, write_csv: str) -> dict:
         for r in csv.DictReader(open(path)):
             name = r["Kernel_Name"]
             key = ("copy" if "copy" in name.lower() else "merge" if "decode_merge" in name
-                   else "decode" if "decode" in name else None)
+                   else "decode" if "decode" in name else "prefill" if "prefill" in name else None)
             if key:
                 acc.setdefault(key, []).append(float(r["Counter_Value"]))
-        return {k: float(np.median(v)) for k, v in acc.items()}
+        return {k: float(np.median(v) if k != "prefill" else np.mean(v)) for k, v in acc.items()}
 
     f, w = per_kernel(fetch_csv), per_kernel(write_csv)
     copy_bytes = CALIBRATE_MIB << 20
     f_scale = copy_bytes / (f["copy"] * 1024)
     w_scale = copy_bytes / (w["copy"] * 1024)
-    fetch = (f["decode"] + f.get("merge", 0.0)) * 1024 * f_scale
-    write = (w["decode"] + w.get("merge", 0.0)) * 1024 * w_scale
-    return {"hbm_bytes_per_launch": int(round(fetch + write)), "fetch_bytes": int(round(fetch)),
-            "write_bytes": int(round(write)), "algorithmic_bytes": decode_bytes(CTX),
-            "fetch_kib_per_dispatch": {k: round(v, 1) for k, v in f.items()},
-            "write_kib_per_dispatch": {k: round(v, 1) for k, v in w.items()},
-            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
-            "calibration": f"torch copy_ of {CALIBRATE_MIB} MiB (reads and writes {copy_bytes} bytes)",
-            "launch": "one attend call: decode_bf16_kernel + decode_merge_kernel"}
+    parts = ("decode", "merge") if kind == "decode" else ("prefill",)
+    fetch = sum(f.get(k, 0.0) for k in parts) * 1024 * f_scale
+    write = sum(w.get(k, 0.0) for k in parts) * 1024 * w_scale
+    out = {"hbm_bytes_per_launch": int(round(fetch + write)), "fetch_bytes": int(round(fetch)),
+           "write_bytes": int(round(write)),
+           "fetch_kib_per_dispatch": {k: round(v, 1) for k, v in f.items()},
+           "write_kib_per_dispatch": {k: round(v, 1) for k, v in w.items()},
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+           "calibration": f"torch copy_ of {CALIBRATE_MIB} MiB (reads and writes {copy_bytes} bytes)"}
+    if kind == "decode":
+        out.update(algorithmic_bytes=decode_bytes(CTX), launch="one attend call: decode_bf16_kernel + decode_merge_kernel")
+    else:
+        kv_bytes = np.mean([2 * (c + 1) * CHUNK * KV_DIM * 2 for c in range(PROMPT // CHUNK)])
+        out.update(kv_bytes_per_launch=int(kv_bytes), q_out_bytes_per_launch=2 * CHUNK * N_HEAD * HD * 4,
+                   launch="one prefill_kernel launch (a 512-token chunk), mean over the 8 chunks")
+    return out
+
+
+def counter_summary(paths: list, pattern: str) -> dict:
+    """Per-dispatch counter values of the kernels whose name contains
+    `pattern`, from `rocprofv3 --pmc ... --output-format csv` files, averaged
+    over dispatches; with GRBM_GUI_ACTIVE (GPU cycles of the dispatch) the
+    busy fractions: SQ_VALU_MFMA_BUSY_CYCLES over all SIMDs (matrix cores
+    busy), TA_BUSY_avr (the texture-address units that issue the LDS-DMA
+    loads), SQ_VALU_MFMA_COEXEC_CYCLES (matrix core and vector ALU busy at
+    once)."""
+    import csv
+
+    per = {}
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            if pattern not in r["Kernel_Name"]:
+                continue
+            per.setdefault(r["Counter_Name"], {}).setdefault(int(r["Dispatch_Id"]), 0.0)
+            per[r["Counter_Name"]][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+    mean = {k: float(np.mean(list(v.values()))) for k, v in per.items()}
+    out = {"dispatches": max(len(v) for v in per.values()) if per else 0,
+           "mean_per_dispatch": {k: round(v, 1) for k, v in sorted(mean.items())}}
+    gui = mean.get("GRBM_GUI_ACTIVE")
+    if gui:
+        simds = 4 * 256
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+            out["mfma_busy"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * gui), 4)
+        if "SQ_VALU_MFMA_COEXEC_CYCLES" in mean:
+            out["mfma_valu_coexec"] = round(mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / (simds * gui), 4)
+        if "TA_BUSY_avr" in mean:
+            out["ta_busy"] = round(mean["TA_BUSY_avr"] / gui, 4)
+    return out
 
 
 CALIBRATE_MIB = 1024
@@ -414,9 +456,17 @@ def main() -> int:
                     help=f"start with a {CALIBRATE_MIB} MiB copy kernel (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
+    ap.add_argument("--pmc-kind", choices=["decode", "prefill"], default="decode",
+                    help="which attend call --pmc-summary describes")
+    ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
+                    help="print per-dispatch averages and busy fractions of rocprofv3 --pmc runs and exit (no GPU)")
+    ap.add_argument("--kernel", default="prefill_kernel", help="kernel name pattern for --counter-summary")
     args = ap.parse_args()
     if args.pmc_summary:
-        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        print(json.dumps(pmc_summary(*args.pmc_summary, kind=args.pmc_kind), indent=1))
+        return 0
+    if args.counter_summary:
+        print(json.dumps(counter_summary(args.counter_summary, args.kernel), indent=1))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
