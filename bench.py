@@ -14,9 +14,14 @@ Prints one JSON line. `value` is decode K/V bytes per second (the algorithmic
 prefill TFLOP/s (4 * head_dim * n_head * sum of span lengths) rides in
 `prefill`. `roofline` is the decode kernel's (HBM bound),
 `prefill.roofline` the prefill kernel's (MFMA bound, dense fp16/bf16 peak),
-both from HIP events on the op's stream. `cpu_baseline` times nnc's own CPU
-attention (oracle/_ref: the reference's kernels and worker pool) on a bounded
-sample of the same workload on this host.
+both from HIP events on the op's stream; their `traffic` comes from the
+counter summaries in profiles/. Beside them: a 16-token session batch, the
+pre-attention step, the weight gemvs, one decode layer through the
+host-buffer entry point, the other benchmark configurations (A, B, C, D at
+4096 keys, E; each step replayed from a HIP graph) and `cpu_baseline`, nnc's
+own CPU attention (oracle/_ref: the reference's kernels and worker pool) on a
+bounded sample of the same workload on this host at the reference's two
+thread settings.
 """
 from __future__ import annotations
 
@@ -169,35 +174,38 @@ def pmc_summary(fetch_csv: str, write_csv: str, kind: str = "decode") -> dict:
     return out
 
 
-def counter_summary(paths: list, pattern: str) -> dict:
+def counter_summary(paths: list, pattern: str, clock_mhz: float = 2400.0) -> dict:
     """Per-dispatch counter values of the kernels whose name contains
     `pattern`, from `rocprofv3 --pmc ... --output-format csv` files, averaged
-    over dispatches; with GRBM_GUI_ACTIVE (GPU cycles of the dispatch) the
-    busy fractions: SQ_VALU_MFMA_BUSY_CYCLES over all SIMDs (matrix cores
-    busy), TA_BUSY_avr (the texture-address units that issue the LDS-DMA
-    loads), SQ_VALU_MFMA_COEXEC_CYCLES (matrix core and vector ALU busy at
-    once)."""
+    over dispatches (a counter listed twice for one dispatch is counted once),
+    and busy fractions over the dispatch's duration (its timestamps) at
+    clock_mhz: SQ_VALU_MFMA_BUSY_CYCLES over the 1024 SIMDs (matrix cores
+    busy), SQ_VALU_MFMA_COEXEC_CYCLES (matrix core and vector ALU busy at
+    once), TA_BUSY_avr (the texture-address units that issue the loads)."""
     import csv
 
-    per = {}
+    per, dur = {}, {}
     for path in paths:
         for r in csv.DictReader(open(path)):
             if pattern not in r["Kernel_Name"]:
                 continue
-            per.setdefault(r["Counter_Name"], {}).setdefault(int(r["Dispatch_Id"]), 0.0)
-            per[r["Counter_Name"]][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+            d = int(r["Dispatch_Id"])
+            per.setdefault(r["Counter_Name"], {})[d] = float(r["Counter_Value"])
+            dur[d] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
     mean = {k: float(np.mean(list(v.values()))) for k, v in per.items()}
     out = {"dispatches": max(len(v) for v in per.values()) if per else 0,
            "mean_per_dispatch": {k: round(v, 1) for k, v in sorted(mean.items())}}
-    gui = mean.get("GRBM_GUI_ACTIVE")
-    if gui:
+    if dur:
+        cycles = float(np.mean(list(dur.values()))) * clock_mhz * 1e6
+        out["mean_duration_us"] = round(float(np.mean(list(dur.values()))) * 1e6, 3)
+        out["clock_mhz"] = clock_mhz
         simds = 4 * 256
         if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
-            out["mfma_busy"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * gui), 4)
+            out["mfma_busy"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * cycles), 4)
         if "SQ_VALU_MFMA_COEXEC_CYCLES" in mean:
-            out["mfma_valu_coexec"] = round(mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / (simds * gui), 4)
+            out["mfma_valu_coexec"] = round(mean["SQ_VALU_MFMA_COEXEC_CYCLES"] / (simds * cycles), 4)
         if "TA_BUSY_avr" in mean:
-            out["ta_busy"] = round(mean["TA_BUSY_avr"] / gui, 4)
+            out["ta_busy"] = round(mean["TA_BUSY_avr"] / cycles, 4)
     return out
 
 
@@ -688,7 +696,7 @@ def main() -> int:
                    "kv_dtype": "bf16", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dec_launch_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_launch_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_bf16_kernel<128,4,4,64,1> + decode_merge_kernel<128,4> (one attend call)",
+                     "kernel": "decode_bf16_kernel<128,4,4,64,1,2> + decode_merge_kernel<128,4> (one attend call)",
                      "avg_launch_us": round(dec_launch_us, 3), "bytes_per_launch": decode_bytes(CTX)},
         "prefill": {"metric": "prefill-attn TFLOP/s", "value": round(pre_tflops, 1), "unit": "TFLOP/s",
                     "ms_per_step": round(pre_step_ms, 3), "steps": args.prefill_steps,
@@ -696,7 +704,8 @@ def main() -> int:
                     "roofline": {"bound": "mfma", "achieved": round(pre_launch_tflops, 1),
                                  "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(pre_launch_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": pre_traffic,
-                                 "kernel": "prefill_kernel<128,4> (bf16 hi+lo QK, fp16 PV MFMA, fp32 accumulate)",
+                                 "kernel": "prefill_kernel<128,4,2> (64 rows per work-group; Q as bf16 hi+lo against the "
+                                           "bf16 K, fp16 P against the fp16 copy of V, fp32 accumulate)",
                                  "avg_launch_us": round(pre_launch_us, 3)}},
         "session_batch": {"what": f"one {SESSION_BATCH}-token forward pass of an nnc session (its batch size, "
                                   f"MTP verification included) ending at position {CTX - 1}, 36 layers; each token "
