@@ -2,14 +2,19 @@
 // attention core, reference src/libnnc/model.cpp:1731-1749, whose unit of
 // work is a (KV head, 256-key block) pair).
 //
-// Grid: (n_split, n_kv, n_tok). A work-group of 4 wavefronts owns one KV head
-// and one absolute-aligned range of split_keys keys of the query's span; each
-// wavefront streams chunks of CH keys, the next chunk's K and V loads in
-// flight while the current one is computed:
+// Grid: one dimension over (split, head group, token group) (wg_coords). A
+// work-group of 4 wavefronts owns a head group (BF16: two KV heads when n_kv
+// is even, heads h and h + 2 of a group of four; F32: one) and one
+// absolute-aligned range of split_keys keys of the query's span; each head's
+// 64-key chunks go to its wavefronts in turn, the next chunk's K and V loads
+// in flight while the current one is computed:
 //   scores   S^T[key][head] = K . Q^T on MFMA (v_mfma_f32_16x16x32_bf16): the
 //            16 keys of a tile are the M rows, loaded straight from HBM in
-//            the A-operand layout (16 contiguous bytes per lane); the group's
-//            query heads are the N columns. Q is split into bf16 hi + lo
+//            the A-operand layout (16 contiguous bytes per lane; BF16 through
+//            range-checked buffer descriptors with the non-temporal hint, a
+//            dead chunk's loads aimed past the range so they return zeros
+//            without touching memory); the group's query heads are the N
+//            columns. Q is split into bf16 hi + lo
 //            halves, so the product against the exact bf16 K is near-fp32;
 //   softmax  per head (column): the chunk max over keys, exp2 of the
 //            log2-scaled scores, a running (m, l) with the usual rescale;
