@@ -124,21 +124,22 @@ nnc_status nnc_hip_kv_append_f32_device(nnc_hip_kv* kv, int32_t buf, int32_t pos
 
 /* Parameters of the pre-attention step (nnc_hip_kv_prep_append_device): the
  * per-layer values attention_forward reads from the model (reference
- * model.cpp:1616-1660). Pointers are device memory. */
+ * model.cpp:1616-1660). The gammas are device memory; the frequency factors
+ * are host memory (the rotation angles are formed on the host, see below). */
 typedef struct nnc_hip_prep
 {
 	int32_t n_head; /* query heads */
 	int32_t n_kv; /* KV heads; n_kv * head_dim is the buffer's kv_dim */
 	int32_t head_dim; /* 1 .. 512 */
-	const float* q_gamma; /* head_dim floats (attn_q_norm), or NULL: no Q norm */
-	const float* k_gamma; /* head_dim floats (attn_k_norm), or NULL: no K norm */
+	const float* q_gamma; /* device: head_dim floats (attn_q_norm), or NULL: no Q norm */
+	const float* k_gamma; /* device: head_dim floats (attn_k_norm), or NULL: no K norm */
 	int32_t v_norm; /* nonzero: RMS-normalise V per head with no gamma (Gemma 4) */
 	float rms_eps; /* hparams.rms_eps */
 	int32_t n_rot; /* rotated values per head (L.n_rot): even, <= head_dim; 0: no RoPE */
 	float freq_base; /* RoPE base (the layer's freq) */
 	float pos_scale; /* RoPE position = (pos0 + t) * pos_scale (the layer's rope scale) */
 	int32_t rope_mode; /* 0 NEOX, 1 NORM (reference nn_ops.h:300-304) */
-	const float* freq_factors; /* n_rot / 2 floats (L.rope_freqs), or NULL */
+	const float* freq_factors; /* host: n_rot / 2 floats (L.rope_freqs), or NULL */
 } nnc_hip_prep;
 
 /* The step just before the attention core, for one layer and a batch of
@@ -146,9 +147,13 @@ typedef struct nnc_hip_prep
  * (reference model.cpp:1616-1691): per-head RMSNorm of Q and K with their
  * gammas (reference nn_ops.cpp:590-632) and of V without gamma when v_norm
  * (reference nn_ops.cpp:558-588), RoPE of Q and K (reference
- * nn_ops.cpp:1830-1873; the per-pair frequencies accumulated in fp32 as
- * there), then K and V of token t into row (pos0 + t) % rows of buffer `buf`
- * (BF16 with nnc_f32_to_bf16's rounding, reference runtime.h:106-113, or F32).
+ * nn_ops.cpp:1830-1873), then K and V of token t into row (pos0 + t) % rows
+ * of buffer `buf` (BF16 with nnc_f32_to_bf16's rounding, reference
+ * runtime.h:106-113, or F32). q, K and V get the bits nnc's CPU step gives:
+ * the norms take their sums in nnc's order, and the cos and sin of the
+ * rotation angles come from the host's libm (the one nnc calls) on the same
+ * fp32 angles; they are computed once per new (positions, RoPE setup) and
+ * kept for the next layers.
  *   q [n_tok][n_head * head_dim] F32, device memory: normalised and rotated in
  *     place, ready for nnc_hip_attend_device;
  *   k, v [n_tok][n_kv * head_dim] F32, device memory: read only.

@@ -84,13 +84,15 @@ namespace nnchip
 		int* n_bad; // the copy's count of elements past fp16's range
 		const float* q_gamma; // head_dim floats, or null: no Q norm
 		const float* k_gamma; // head_dim floats, or null: no K norm
-		const float* freq_factors; // n_rot / 2 floats, or null
+		// cos and sin of every rotation angle of the batch, [n_tok][n_rot / 2]
+		// (cos, sin) pairs, computed on the host as the reference computes them
+		const float2* rope_cs;
 		int n_head, n_kv, head_dim, rows, pos0, bf16;
 		int v_norm; // RMS-normalise V per head, no gamma
 		int n_rot; // rotated lanes per head (even); 0: no RoPE
 		int mode; // 0 NEOX, 1 NORM
-		float eps, pos_scale;
-		float inv[kPrepMaxPairs]; // base^(-2i/n_rot), accumulated in fp32 as the reference does
+		float eps;
+		float inv_dim; // 1 / head_dim in fp32 (the gamma norm's mean)
 	};
 
 	// Launches the pre-attention step over an (n_head + 2 n_kv, n_tok) grid of

@@ -8,12 +8,19 @@
 //
 // A work-group takes 16 head rows of one token, 4 per wavefront, all loaded at
 // once; a head's head_dim values are held 64 lanes wide (coalesced loads and
-// stores), the RMSNorm sum is a wavefront reduction (DPP and permlane swaps), and RoPE pairs meet
-// through the wavefront's LDS row. Each lane computes the rotation angles of
-// the pairs it rotates once for all its rows, following the reference's
-// schedule: the per-pair frequency base^(-2i/n_rot) accumulated step by step
-// in fp32 (computed on the host, the same sequence of products), times the
-// position, divided by the pair's frequency factor when there is one.
+// stores) and meet through the wavefront's LDS row. Every result has the
+// reference's bits:
+//   RMSNorm  the sum of squares as the reference's AVX2 loop takes it: eight
+//            fp32 fused multiply-add chains over x[l], x[l + 8], ... (lanes
+//            0..7, from the LDS row), summed in hsum_ymm's order, the tail in
+//            double; the mean, square root and reciprocal in double, rounded
+//            once to fp32 (reference nn_ops.cpp:28-36, 558-632); with gamma
+//            y = (x * gamma) * scale, the order its -ffast-math build
+//            multiplies in.
+//   RoPE     cos and sin of each angle from the host (nnc_hip.hip computes them
+//            with the host's libm from the reference's fp32 angle), and each
+//            pair as fma(c, a, -(s * b)), fma(s, a, c * b), the contraction the
+//            reference's build makes (reference nn_ops.cpp:1830-1873).
 #include "device_common.h"
 #include "kernels.h"
 
@@ -152,31 +159,21 @@ namespace nnchip
 				gk[j] = (p.k_gamma && in) ? p.k_gamma[i] : 1.0f;
 			}
 
-			// This lane's rotation angles: the pairs lane, lane + 64, ... it
-			// rotates in every row (no barrier: the loads above are in flight).
+			// cos and sin of the angles of the pairs lane, lane + 64, ... this
+			// lane rotates in every row of the token (no barrier: the loads above
+			// are in flight).
 			constexpr int NP = kPrepMaxPairs / 64;
 			float c_tab[NP], s_tab[NP];
 			if (half > 0)
 			{
-				const float rpos = static_cast<float>(p.pos0 + t) * p.pos_scale;
+				const float2* cs = p.rope_cs + static_cast<size_t>(t) * half;
 #pragma unroll
 				for (int u = 0; u < NP; ++u)
 				{
 					const int i = lane + 64 * u;
-					c_tab[u] = 1.0f;
-					s_tab[u] = 0.0f;
-					if (i < half)
-					{
-						float th = rpos * p.inv[i];
-						if (p.freq_factors) th /= p.freq_factors[i];
-						// sin and cos of the fp32 angle, reduced to [-pi, pi] in double
-						// first (exact to far below an fp32 ulp for the angles RoPE
-						// makes), so sincosf takes its small-argument path.
-						const double thd = static_cast<double>(th);
-						const double turns = rint(thd * 0.15915494309189535);
-						const float rr = static_cast<float>(fma(-turns, 6.283185307179586, thd));
-						sincosf(isfinite(th) ? rr : th, &s_tab[u], &c_tab[u]);
-					}
+					const float2 v = i < half ? cs[i] : make_float2(1.0f, 0.0f);
+					c_tab[u] = v.x;
+					s_tab[u] = v.y;
 				}
 			}
 
@@ -189,28 +186,42 @@ namespace nnchip
 				(void)row_src(hrow, kind, head);
 				float* xr = x[r];
 
-				// RMSNorm: scale = 1 / sqrt(mean of squares + eps), the mean in
-				// double as the reference takes it (times fp32 1/dim with gamma,
-				// divided by dim without, reference nn_ops.cpp:558-632).
+				// RMSNorm: scale = 1 / sqrt(mean of squares + eps) in double
+				// (times fp32 1/dim with gamma, divided by dim without, reference
+				// nn_ops.cpp:558-632), the sum of squares in the reference's order.
 				const float* gamma = kind == 0 ? p.q_gamma : kind == 1 ? p.k_gamma : nullptr;
 				const bool norm = kind == 2 ? p.v_norm != 0 : gamma != nullptr;
 				if (norm)
 				{
-					float ss = 0.0f;
-#pragma unroll
-					for (int j = 0; j < NJ; ++j) ss = fmaf(xr[j], xr[j], ss);
-					// (the reference takes the mean in double; the square root and
-					// its reciprocal in fp32 here, within an fp32 ulp of it)
-					const double sum2 = static_cast<double>(wave_sum_dpp(ss));
-					const double mean = gamma ? sum2 * static_cast<double>(1.0f / static_cast<float>(hd))
-					                          : sum2 / static_cast<double>(hd);
-					const float sc = 1.0f / sqrtf(static_cast<float>(mean + static_cast<double>(p.eps)));
+					float* xs = s_x[wave];
 #pragma unroll
 					for (int j = 0; j < NJ; ++j)
 					{
-						xr[j] = xr[j] * sc;
-						if (gamma) xr[j] *= kind == 0 ? gq[j] : gk[j];
+						const int i = pos(j);
+						if (FULL || i < hd) xs[i] = xr[j];
 					}
+					wave_sync();
+					// Chain l (lane l < 8): fma over x[l], x[l + 8], ... of the
+					// full runs of eight, in ascending order.
+					const int body = hd & ~7;
+					float chain = 0.0f;
+					if (lane < 8)
+						for (int i = lane; i < body; i += 8) chain = __builtin_fmaf(xs[i], xs[i], chain);
+					float c8[8];
+#pragma unroll
+					for (int l = 0; l < 8; ++l) c8[l] = __shfl(chain, l);
+					const float hs = __fadd_rn(__fadd_rn(__fadd_rn(c8[0], c8[4]), __fadd_rn(c8[1], c8[5])),
+					                           __fadd_rn(__fadd_rn(c8[2], c8[6]), __fadd_rn(c8[3], c8[7])));
+					double sum2 = body > 0 ? static_cast<double>(hs) : 0.0;
+					for (int i = body; i < hd; ++i)
+						sum2 = __dadd_rn(sum2, __dmul_rn(static_cast<double>(xs[i]), static_cast<double>(xs[i])));
+					wave_sync(); // the row buffer is free for RoPE
+					const double mean = gamma ? __dmul_rn(sum2, static_cast<double>(p.inv_dim))
+					                          : __ddiv_rn(sum2, static_cast<double>(hd));
+					const float sc = __double2float_rn(__ddiv_rn(1.0, sqrt(__dadd_rn(mean, static_cast<double>(p.eps)))));
+#pragma unroll
+					for (int j = 0; j < NJ; ++j)
+						xr[j] = gamma ? __fmul_rn(__fmul_rn(xr[j], kind == 0 ? gq[j] : gk[j]), sc) : __fmul_rn(xr[j], sc);
 				}
 
 				// RoPE on Q and K: NEOX pairs lanes i and i + n_rot/2, NORM lanes
@@ -235,8 +246,8 @@ namespace nnchip
 						const float c = c_tab[u], sn = s_tab[u];
 						const int i0 = i * stride, i1 = i0 + partner;
 						const float a = xs[i0], b = xs[i1];
-						xs[i0] = c * a - sn * b;
-						xs[i1] = sn * a + c * b;
+						xs[i0] = __builtin_fmaf(c, a, -__fmul_rn(sn, b));
+						xs[i1] = __builtin_fmaf(sn, a, __fmul_rn(c, b));
 					}
 					wave_sync();
 #pragma unroll

@@ -103,6 +103,19 @@ namespace
 		hipEvent_t free = nullptr;
 	};
 
+	// One table of RoPE cos/sin pairs on the device ([n_tok][n_rot / 2]) and
+	// what it was computed for; a model's layers share positions and usually
+	// one rotation setup, so most calls find their table already there.
+	struct rope_table
+	{
+		int32_t pos0 = -1, n_tok = 0, n_rot = 0;
+		float base = 0.0f, pos_scale = 0.0f;
+		bool has_ff = false;
+		std::vector<float> ff;
+		dev_scratch dev;
+		uint64_t used = 0; // last use (for replacing the older table)
+	};
+
 	// Where a call's decode partials go: a fixed array of `bytes` bytes, or
 	// (ptr null) the cache's grow-only scratch.
 	struct part_source
@@ -152,7 +165,9 @@ struct nnc_hip_kv
 	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now past fp16's range (device)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
-	host_staging pinned; // host rows in and out (q, gate, out; K/V appends)
+	host_staging pinned; // host rows in and out (q, gate, out; K/V appends; RoPE tables)
+	rope_table rope[2]; // the last two RoPE setups (Gemma 3 alternates local and global layers)
+	uint64_t rope_clock = 0;
 };
 
 namespace
@@ -167,7 +182,8 @@ namespace
 				if (ptr) (void)hipFree(ptr);
 		}
 		if (kv->n_bad) (void)hipFree(kv->n_bad);
-		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v})
+		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v,
+		                       &kv->rope[0].dev, &kv->rope[1].dev})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->pinned.ptr) (void)hipHostFree(kv->pinned.ptr);
 		if (kv->pinned.free) (void)hipEventDestroy(kv->pinned.free);
@@ -214,6 +230,73 @@ namespace
 		std::memcpy(kv->pinned.ptr, src, bytes);
 		NNC_HIP_TRY(hipMemcpyAsync(dst, kv->pinned.ptr, bytes, hipMemcpyHostToDevice, kv->stream), what);
 		NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), what);
+		return NNC_OK;
+	}
+
+	// The cos/sin of every RoPE angle of tokens pos0 .. pos0 + n_tok - 1 on the
+	// device, computed on the host the way the reference computes them
+	// (nn_ops.cpp:1840-1855, model.cpp:1645-1655): the position (pos0 + t) *
+	// pos_scale in fp32, the frequency ratio base^(-2/n_rot) with powf and the
+	// per-pair frequency multiplied in step by step in fp32, the angle
+	// position * frequency divided by the pair's frequency factor, and its cos
+	// and sin from the host's libm (sincosf, whose results equal glibc's cosf
+	// and sinf). The host's libm is the one nnc's own CPU path calls in the
+	// same process, so the bits agree. Kept for the next call with the same
+	// setup; the upload goes through the pinned staging on the cache's stream.
+	nnc_status rope_cs(nnc_hip_kv* kv, const nnc_hip_prep& pr, int32_t pos0, int32_t n_tok, const float2*& out)
+	{
+		const int half = pr.n_rot / 2;
+		auto same = [&](const rope_table& r)
+		{
+			if (r.pos0 != pos0 || r.n_tok != n_tok || r.n_rot != pr.n_rot) return false;
+			if (std::memcmp(&r.base, &pr.freq_base, 4) != 0 || std::memcmp(&r.pos_scale, &pr.pos_scale, 4) != 0)
+				return false;
+			if (r.has_ff != (pr.freq_factors != nullptr)) return false;
+			return !r.has_ff || std::memcmp(r.ff.data(), pr.freq_factors, sizeof(float) * half) == 0;
+		};
+		rope_table* hit = nullptr;
+		for (rope_table& r : kv->rope)
+			if (same(r)) hit = &r;
+		if (!hit)
+		{
+			hit = kv->rope[0].used <= kv->rope[1].used ? &kv->rope[0] : &kv->rope[1];
+			const size_t bytes = sizeof(float2) * static_cast<size_t>(n_tok) * half;
+			hit->pos0 = -1; // (invalid until filled)
+			if (nnc_status s = reserve(kv, hit->dev, bytes, "RoPE table")) return s;
+			if (nnc_status s = reserve_pinned(kv, bytes, "RoPE table staging")) return s;
+			float2* cs = static_cast<float2*>(kv->pinned.ptr);
+			const float ratio = std::pow(pr.freq_base, -2.0f / static_cast<float>(pr.n_rot));
+			std::vector<float> inv(half);
+			float f = 1.0f;
+			for (int i = 0; i < half; ++i)
+			{
+				inv[i] = f;
+				f *= ratio;
+			}
+			for (int32_t t = 0; t < n_tok; ++t)
+			{
+				const float rpos = static_cast<float>(pos0 + t) * pr.pos_scale;
+				for (int i = 0; i < half; ++i)
+				{
+					float th = rpos * inv[i];
+					if (pr.freq_factors) th /= pr.freq_factors[i];
+					float s, c;
+					::sincosf(th, &s, &c);
+					cs[static_cast<size_t>(t) * half + i] = make_float2(c, s);
+				}
+			}
+			NNC_HIP_TRY(hipMemcpyAsync(hit->dev.ptr, cs, bytes, hipMemcpyHostToDevice, kv->stream), "RoPE table");
+			NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), "RoPE table");
+			hit->pos0 = pos0;
+			hit->n_tok = n_tok;
+			hit->n_rot = pr.n_rot;
+			hit->base = pr.freq_base;
+			hit->pos_scale = pr.pos_scale;
+			hit->has_ff = pr.freq_factors != nullptr;
+			hit->ff.assign(pr.freq_factors ? pr.freq_factors : nullptr, pr.freq_factors ? pr.freq_factors + half : nullptr);
+		}
+		hit->used = ++kv->rope_clock;
+		out = static_cast<const float2*>(hit->dev.ptr);
 		return NNC_OK;
 	}
 
@@ -636,7 +719,6 @@ nnc_status nnc_hip_kv_prep_append_device(nnc_hip_kv* kv, int32_t buf, int32_t po
 	p.n_bad = b.v16 ? kv->n_bad + buf : nullptr;
 	p.q_gamma = pr.q_gamma;
 	p.k_gamma = pr.k_gamma;
-	p.freq_factors = pr.freq_factors;
 	p.n_head = pr.n_head;
 	p.n_kv = pr.n_kv;
 	p.head_dim = pr.head_dim;
@@ -647,19 +729,10 @@ nnc_status nnc_hip_kv_prep_append_device(nnc_hip_kv* kv, int32_t buf, int32_t po
 	p.n_rot = pr.n_rot;
 	p.mode = pr.rope_mode;
 	p.eps = pr.rms_eps;
-	p.pos_scale = pr.pos_scale;
-	// The reference's frequency schedule (nn_ops.cpp:1840-1851): the ratio
-	// base^(-2/n_rot) in fp32, multiplied in step by step.
+	p.inv_dim = 1.0f / static_cast<float>(pr.head_dim); // (reference nn_ops.cpp:594)
+	p.rope_cs = nullptr;
 	if (pr.n_rot > 0)
-	{
-		const float ratio = std::pow(pr.freq_base, -2.0f / static_cast<float>(pr.n_rot));
-		float inv = 1.0f;
-		for (int i = 0; i < pr.n_rot / 2; ++i)
-		{
-			p.inv[i] = inv;
-			inv *= ratio;
-		}
-	}
+		if (nnc_status s = rope_cs(kv, pr, pos0, n_tok, p.rope_cs)) return s;
 	if (!nnchip::launch_prep(p, n_tok, kv->stream))
 		return fail(NNC_ERR_UNSUPPORTED_MODEL, "no pre-attention kernel for head_dim %d", pr.head_dim);
 	NNC_HIP_TRY(hipGetLastError(), "pre-attention step");

@@ -299,13 +299,15 @@ class KVCache:
                     head_dim: int, q_gamma: np.ndarray | None = None, k_gamma: np.ndarray | None = None,
                     v_norm: bool = False, eps: float = 1e-6, n_rot: int = 0, base: float = 10000.0,
                     pos_scale: float = 1.0, mode: int = 0, freq_factors: np.ndarray | None = None) -> np.ndarray:
-        """prep_append_device from host arrays (uploaded to scratch device
-        memory, freed afterwards); returns the normalised, rotated q."""
+        """prep_append_device from host arrays (q, k, v and the gammas uploaded
+        to scratch device memory, freed afterwards; the frequency factors stay
+        in host memory); returns the normalised, rotated q."""
         from . import hip_rt
 
         q = np.ascontiguousarray(q, dtype=np.float32)
         arrays = [q, np.ascontiguousarray(k, dtype=np.float32), np.ascontiguousarray(v, dtype=np.float32)]
-        extras = [q_gamma, k_gamma, freq_factors]
+        extras = [q_gamma, k_gamma]
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
         ptrs, dev = [], []
         try:
             for a in arrays + [None if e is None else np.ascontiguousarray(e, dtype=np.float32) for e in extras]:
@@ -317,7 +319,7 @@ class KVCache:
                 hip_rt.to_device(d, a)
                 ptrs.append(d)
             prep = NncHipPrep(n_head, n_kv, head_dim, ptrs[3], ptrs[4], int(bool(v_norm)), eps, n_rot, base, pos_scale,
-                              mode, ptrs[5])
+                              mode, None if ff is None else ff.ctypes.data)
             n_tok = q.size // (n_head * head_dim)
             self.prep_append_device(buf, ptrs[0], ptrs[1], ptrs[2], pos0=pos0, n_tok=n_tok, prep=prep)
             self.sync()

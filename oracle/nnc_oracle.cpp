@@ -339,8 +339,13 @@ void orc_rope_ff(float* x, int n_heads, int head_dim, int n_rot, float pos, floa
 		{
 			float* p = xh + i * stride;
 			const float a = p[0], b = p[partner];
-			p[0] = c[i] * a - s[i] * b;
-			p[partner] = s[i] * a + c[i] * b;
+			// The reference's build contracts each of the two expressions into
+			// one fused multiply-add, the first product fused and the second
+			// rounded (its -ffast-math build, reference CMakeLists.txt:66-76);
+			// bit for bit against it in tests/test_oracle.py.
+			const float sb = s[i] * b, cb = c[i] * b;
+			p[0] = std::fma(c[i], a, -sb);
+			p[partner] = std::fma(s[i], a, cb);
 		}
 	}
 }
@@ -350,43 +355,60 @@ void orc_rope(float* x, int n_heads, int head_dim, int n_rot, float pos, float b
 	orc_rope_ff(x, n_heads, head_dim, n_rot, pos, base, mode, nullptr);
 }
 
-// RMSNorm of n_groups vectors of dim floats, in place, gamma = 1: the sum of
-// squares in double, y = x * (1 / sqrt(mean + eps)).
-void orc_rmsnorm_groups(float* x, size_t n_groups, size_t dim, float eps)
+// The sum of squares of dim floats as the reference's AVX2 loop takes it
+// (reference nn_ops.cpp:562-575, :600-613): eight fp32 fused multiply-add
+// chains over x[l], x[l + 8], ... for the full runs of eight, their sum in
+// hsum_ymm's order ((c0 + c4) + (c1 + c5)) + ((c2 + c6) + (c3 + c7))
+// (reference nn_ops.cpp:28-36), then the tail in double.
+void orc_rmsnorm_gamma(float* x, size_t n_groups, size_t dim, const float* gamma, float eps);
+
+static double rms_sum_squares(const float* x, size_t dim)
 {
-	for (size_t g = 0; g < n_groups; ++g)
+	double s2 = 0.0;
+	size_t i = 0;
+	if (dim >= 8)
 	{
-		float* xg = x + g * dim;
-		double s2 = 0.0;
-		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
-		const float r = static_cast<float>(1.0 / std::sqrt(s2 / static_cast<double>(dim) + eps));
-		for (size_t i = 0; i < dim; ++i) xg[i] *= r;
+		float c[8] = {};
+		for (; i + 8 <= dim; i += 8)
+			for (int l = 0; l < 8; ++l) c[l] = std::fma(x[i + l], x[i + l], c[l]);
+		const float hs = ((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7]));
+		s2 = static_cast<double>(hs);
 	}
+	for (; i < dim; ++i) s2 += static_cast<double>(x[i]) * x[i];
+	return s2;
 }
 
-// RMSNorm with a learned gamma (NULL = 1), in place: the sum of squares in
-// double, scale = 1 / sqrt(sum * (1/dim as fp32) + eps), y = x * scale * gamma.
+// RMSNorm of n_groups vectors of dim floats, in place, gamma = 1
+// (nnc_rmsnorm_gamma_multi_f32 with unit gamma).
+void orc_rmsnorm_groups(float* x, size_t n_groups, size_t dim, float eps)
+{
+	orc_rmsnorm_gamma(x, n_groups, dim, nullptr, eps);
+}
+
+// RMSNorm with a learned gamma (NULL = 1), in place: scale = 1 / sqrt(sum *
+// (1/dim as fp32) + eps) in double, rounded to fp32; y = (x * gamma) * scale,
+// the order the reference's -ffast-math build multiplies in (bit for bit
+// against it in tests/test_oracle.py).
 void orc_rmsnorm_gamma(float* x, size_t n_groups, size_t dim, const float* gamma, float eps)
 {
 	const float inv_dim = 1.0f / static_cast<float>(dim);
 	for (size_t g = 0; g < n_groups; ++g)
 	{
 		float* xg = x + g * dim;
-		double s2 = 0.0;
-		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
+		const double s2 = rms_sum_squares(xg, dim);
 		const float r = static_cast<float>(1.0 / std::sqrt(s2 * inv_dim + eps));
-		for (size_t i = 0; i < dim; ++i) xg[i] = xg[i] * r * (gamma ? gamma[i] : 1.0f);
+		for (size_t i = 0; i < dim; ++i) xg[i] = (xg[i] * (gamma ? gamma[i] : 1.0f)) * r;
 	}
 }
 
-// RMSNorm without gamma, in place: scale = 1 / sqrt(sum / dim + eps).
+// RMSNorm without gamma, in place: scale = 1 / sqrt(sum / dim + eps) in
+// double, rounded to fp32; y = x * scale.
 void orc_rmsnorm_plain(float* x, size_t n_groups, size_t dim, float eps)
 {
 	for (size_t g = 0; g < n_groups; ++g)
 	{
 		float* xg = x + g * dim;
-		double s2 = 0.0;
-		for (size_t i = 0; i < dim; ++i) s2 += static_cast<double>(xg[i]) * xg[i];
+		const double s2 = rms_sum_squares(xg, dim);
 		const float r = static_cast<float>(1.0 / std::sqrt(s2 / static_cast<double>(dim) + eps));
 		for (size_t i = 0; i < dim; ++i) xg[i] *= r;
 	}

@@ -360,10 +360,10 @@ def test_rope_and_rmsnorm_match_reference(orc, ref):
         for pos in (0.0, 7.0, 4095.0, 32767.0):
             a = orc.rope(x, 8, 128, 128, pos, 500000.0, mode)
             b = ref.rope(x, 8, 128, 128, pos, 500000.0, mode)
-            assert np.allclose(a, b, atol=1e-5), (mode, pos)
+            assert np.array_equal(a, b), (mode, pos)
     a = orc.rmsnorm_groups(x, 128)
     b = ref.rmsnorm_groups(x, 128)
-    assert np.allclose(a, b, rtol=1e-6, atol=1e-7)
+    assert np.array_equal(a, b)
     c = synth.rmsnorm_heads(x.reshape(1, -1), 128).reshape(-1)
     assert np.allclose(c, b, rtol=1e-6, atol=1e-7)
     assert np.allclose(np.sqrt((c.reshape(8, 128) ** 2).mean(axis=1)), 1.0, atol=1e-3)

@@ -7,11 +7,11 @@ reference's pieces called in the reference's order, and closed forms.
 GPU: nnc_hip_kv_prep_append_device against the same vectors and against
 the oracle over model-shaped cases, then prep + attend end to end.
 
-Tolerances. q and F32 K/V: rtol 1e-5, atol 1e-5 (the device's cosf/sinf and
-fp32 sums differ from glibc's in the last bits). BF16 K/V: at most one
-BF16 unit in the last place per element, on at most 0.5 % of the elements
-(a value that differs in its last fp32 bits can round to the neighbouring
-BF16). End to end: the attention bound of the BF16 cache, 5e-3."""
+Tolerances. None for the step itself: q, F32 K/V and BF16 K/V bits equal
+the reference's (the oracle is bit for bit against the reference's compiled
+RoPE and RMSNorm; the device takes the same sums in the same order and the
+rotation angles' cos/sin from the host's libm, as the reference does). End to
+end: the attention bound of the BF16 cache, 5e-3."""
 from __future__ import annotations
 
 import zlib
@@ -43,13 +43,33 @@ def test_rope_ff_and_norms_match_reference_vectors(orc, gold):
         for n_rot in (128, 64):
             for pos in (7, 32767):
                 got = orc.rope_ff(x, 4, 128, n_rot, float(pos), 1000000.0, mode, ff[: n_rot // 2])
-                assert np.allclose(got, gold[f"rope_ff/{mode}/{n_rot}/{pos}"], rtol=1e-6, atol=1e-6), (mode, n_rot, pos)
-    assert np.allclose(orc.rmsnorm_gamma(x, 128, gold["rmsnorm_gamma/gamma"]), gold["rmsnorm_gamma/out"], rtol=1e-6,
-                       atol=1e-7)
+                assert np.array_equal(got, gold[f"rope_ff/{mode}/{n_rot}/{pos}"]), (mode, n_rot, pos)
+    assert np.array_equal(orc.rmsnorm_gamma(x, 128, gold["rmsnorm_gamma/gamma"]), gold["rmsnorm_gamma/out"])
     x80 = gold["rmsnorm_gamma80/in"]
-    assert np.allclose(orc.rmsnorm_gamma(x80, 80, gold["rmsnorm_gamma80/gamma"]), gold["rmsnorm_gamma80/out"],
-                       rtol=1e-6, atol=1e-7)
-    assert np.allclose(orc.rmsnorm_plain(x80, 80), gold["rmsnorm_plain80/out"], rtol=1e-6, atol=1e-7)
+    assert np.array_equal(orc.rmsnorm_gamma(x80, 80, gold["rmsnorm_gamma80/gamma"]), gold["rmsnorm_gamma80/out"])
+    assert np.array_equal(orc.rmsnorm_plain(x80, 80), gold["rmsnorm_plain80/out"])
+
+
+def test_rope_and_norms_bitwise_against_reference(orc, ref):
+    """The restatements give the reference's compiled bits over random inputs:
+    RoPE in both modes, with and without frequency factors, positions up to
+    2^17 and fractional (scaled) positions; RMSNorm with and without gamma at
+    head sizes with and without a tail past the last run of eight."""
+    rng = np.random.default_rng(21)
+    for mode in (0, 1):
+        for n_rot, hd in ((64, 64), (64, 128), (128, 128), (256, 256), (32, 80)):
+            ff = np.exp(rng.uniform(0.0, 3.0, n_rot // 2)).astype(np.float32)
+            for pos in (1.0, 77.0, 4095.0, 32767.0, 131071.0, 1234.5):
+                x = (2.0 * rng.standard_normal(4 * hd)).astype(np.float32)
+                for f in (None, ff):
+                    a = orc.rope_ff(x, 4, hd, n_rot, pos, 1000000.0, mode, f)
+                    b = ref.rope_ff(x, 4, hd, n_rot, pos, 1000000.0, mode, f)
+                    assert np.array_equal(a, b), (mode, n_rot, hd, pos, f is None)
+    for dim in (4, 6, 12, 64, 80, 84, 128, 136, 256, 512):
+        x = (2.0 * rng.standard_normal(300 * dim)).astype(np.float32)
+        g = rng.uniform(0.5, 1.5, dim).astype(np.float32)
+        assert np.array_equal(orc.rmsnorm_gamma(x, dim, g), ref.rmsnorm_gamma(x, dim, g)), dim
+        assert np.array_equal(orc.rmsnorm_plain(x, dim), ref.rmsnorm_plain(x, dim)), dim
 
 
 def test_rope_closed_forms(orc):
@@ -106,25 +126,20 @@ def test_prep_append_composes_the_reference_pieces(orc, ref):
             rpos = np.float32(pos0 + t) * np.float32(0.5)
             want_q[t] = ref.rope_ff(want_q[t], n_head, hd, hd // 2, float(rpos), 10000.0, 0, ff)
             want_k[t] = ref.rope_ff(want_k[t], n_kv, hd, hd // 2, float(rpos), 10000.0, 0, ff)
-        assert np.allclose(qo, want_q, rtol=1e-6, atol=1e-6)
+        assert np.array_equal(qo, want_q)
         for t in range(n_tok):
             r = (pos0 + t) % rows
             if bf16:
                 assert np.array_equal(Ko[r], ref.bf16_round(want_k[t])), t
                 assert np.array_equal(Vo[r], ref.bf16_round(want_v[t])), t
             else:
-                assert np.allclose(Ko[r], want_k[t], rtol=1e-6, atol=1e-6)
-                assert np.allclose(Vo[r], want_v[t], rtol=1e-6, atol=1e-6)
+                assert np.array_equal(Ko[r], want_k[t])
+                assert np.array_equal(Vo[r], want_v[t])
         untouched = sorted(set(range(rows)) - {(pos0 + t) % rows for t in range(n_tok)})
         assert not Ko[untouched].any() and not Vo[untouched].any()
 
 
 # ---- GPU: the device step ------------------------------------------------------------------
-
-def bf16_ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """|a - b| in BF16 units in the last place, for BF16 bit patterns of equal sign."""
-    return np.abs(a.astype(np.int32) - b.astype(np.int32))
-
 
 @pytest.mark.gpu
 def test_hip_prep_matches_reference_vectors(gold):
@@ -139,20 +154,20 @@ def test_hip_prep_matches_reference_vectors(gold):
                     say(f"case golden rope mode {mode} n_rot {n_rot} pos {pos}")
                     got = kv.prep_append(0, x, dummy, dummy, pos0=pos, n_head=4, n_kv=1, head_dim=128, n_rot=n_rot,
                                          base=1000000.0, mode=mode, freq_factors=ff[: n_rot // 2])
-                    assert np.allclose(got.reshape(-1), gold[f"rope_ff/{mode}/{n_rot}/{pos}"], rtol=1e-5, atol=1e-5)
+                    assert np.array_equal(got.reshape(-1), gold[f"rope_ff/{mode}/{n_rot}/{pos}"])
         say("case golden rmsnorm gamma")
         got = kv.prep_append(0, x, dummy, dummy, pos0=0, n_head=4, n_kv=1, head_dim=128,
                              q_gamma=gold["rmsnorm_gamma/gamma"])
-        assert np.allclose(got.reshape(-1), gold["rmsnorm_gamma/out"], rtol=1e-5, atol=1e-6)
+        assert np.array_equal(got.reshape(-1), gold["rmsnorm_gamma/out"])
     x80 = gold["rmsnorm_gamma80/in"].reshape(1, 6 * 80)
     with nh.KVCache([4], [480], bf16=False) as kv:
         say("case golden rmsnorm 80 (Q gamma, V plain, F32 cache)")
         got = kv.prep_append(0, x80, x80, x80, pos0=1, n_head=6, n_kv=6, head_dim=80,
                              q_gamma=gold["rmsnorm_gamma80/gamma"], v_norm=True)
-        assert np.allclose(got.reshape(-1), gold["rmsnorm_gamma80/out"], rtol=1e-5, atol=1e-6)
+        assert np.array_equal(got.reshape(-1), gold["rmsnorm_gamma80/out"])
         K, V = kv.read(0, 1, 1)
         assert np.array_equal(K.reshape(-1), x80.reshape(-1))  # no K norm, no RoPE: stored as given
-        assert np.allclose(V.reshape(-1), gold["rmsnorm_plain80/out"], rtol=1e-5, atol=1e-6)
+        assert np.array_equal(V.reshape(-1), gold["rmsnorm_plain80/out"])
 
 
 PREP_CASES = {
@@ -166,6 +181,9 @@ PREP_CASES = {
                                                                           base=10000.0, mode=0, ff=True)),
     "f32_cache_one_token": (16, 4, 128, 1, 32767, 32768, False, dict(kg=True, n_rot=128, base=10000.0, mode=1)),
     "no_rope_hd80": (6, 2, 80, 3, 5, 16, True, dict(qg=True, kg=True, n_rot=0)),
+    # a head size with a tail past the last run of eight, NORM pairs with factors, far positions in a ring
+    "hd100_tail_norm_ff_far": (4, 2, 100, 5, 131000, 256, True, dict(qg=True, kg=True, v_norm=True, n_rot=100,
+                                                                     base=1000000.0, mode=1, ff=True)),
 }
 
 
@@ -199,18 +217,39 @@ def test_hip_prep_matches_oracle(orc, name):
     with nh.KVCache([rows], [n_kv * hd], bf16=bf16) as kv:
         got_q = kv.prep_append(0, q, k, v, pos0=pos0, n_head=n_head, n_kv=n_kv, head_dim=hd, **kw)
         K, V = kv.read(0, 0, rows)
-    err = float(np.abs(got_q - want_q).max())
-    say(f"  q max-abs {err:.3e}")
-    assert np.allclose(got_q, want_q, rtol=1e-5, atol=1e-5)
-    if bf16:
-        for got, want, what in ((K, want_K, "K"), (V, want_V, "V")):
-            ulps = bf16_ulps(got, want)
-            frac = float((ulps > 0).mean())
-            say(f"  {what}: {int((ulps > 0).sum())} of {ulps.size} elements differ (max {int(ulps.max())} ulp)")
-            assert ulps.max() <= 1 and frac <= 0.005, what
-    else:
-        assert np.allclose(K, want_K, rtol=1e-5, atol=1e-5)
-        assert np.allclose(V, want_V, rtol=1e-5, atol=1e-5)
+    for got, want, what in ((got_q, want_q, "q"), (K, want_K, "K"), (V, want_V, "V")):
+        say(f"  {what}: {int((got != want).sum())} of {got.size} elements differ")
+        assert np.array_equal(got, want), what
+
+
+@pytest.mark.gpu
+def test_hip_prep_rope_tables_follow_each_call(orc):
+    """The bridge keeps the RoPE tables of its last two setups: alternating
+    setups (Gemma 3's local and global layers), a repeated call, new positions
+    and a third setup that replaces the older table all give the oracle's bits."""
+    n_head, n_kv, hd, rows = 4, 2, 128, 64
+    rng = np.random.default_rng(31)
+    ff = np.exp(rng.uniform(0.0, 2.0, 32)).astype(np.float32)
+    setups = {"local": dict(n_rot=128, base=10000.0, pos_scale=1.0, mode=0),
+              "global": dict(n_rot=128, base=1000000.0, pos_scale=0.125, mode=0),
+              "partial_ff": dict(n_rot=64, base=10000.0, pos_scale=1.0, mode=1, freq_factors=ff)}
+    calls = [("local", 100, 3), ("global", 100, 3), ("local", 100, 3), ("global", 103, 1), ("partial_ff", 103, 1),
+             ("local", 100, 3), ("partial_ff", 103, 1), ("global", 104, 2)]
+    with nh.KVCache([rows], [n_kv * hd], bf16=True) as kv:
+        K_host = np.zeros((rows, n_kv * hd), np.uint16)
+        V_host = np.zeros_like(K_host)
+        for name, pos0, n_tok in calls:
+            say(f"case rope table: {name} at {pos0} x {n_tok}")
+            q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+            k = rng.standard_normal((n_tok, n_kv * hd)).astype(np.float32)
+            v = rng.standard_normal((n_tok, n_kv * hd)).astype(np.float32)
+            kw = dict(setups[name], eps=1e-6)
+            want_q, K_host, V_host = orc.prep_append(q, k, v, K_host, V_host, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                                                     pos0=pos0, kv_bf16=True, **kw)
+            got_q = kv.prep_append(0, q, k, v, pos0=pos0, n_head=n_head, n_kv=n_kv, head_dim=hd, **kw)
+            K, V = kv.read(0, 0, rows)
+            assert np.array_equal(got_q, want_q), (name, pos0)
+            assert np.array_equal(K, K_host) and np.array_equal(V, V_host), (name, pos0)
 
 
 @pytest.mark.gpu
