@@ -233,10 +233,13 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
     x = hip_rt.malloc(16 * 9728 * 4)
     y = hip_rt.malloc(16 * 9728 * 4)
     nh.fill_normal(x, 16 * 9728, 99, 0, False, stream)
+    # Every buffer is freed only after the last timing: the driver clears freed
+    # device memory in the background, which takes HBM bandwidth for seconds.
+    bufs = []
     for fmt in ("bf16", "q8_0", "q4_s"):
         layer_bytes = sum(gemv_bytes(fmt, r, c) for r, c in GEMV_LAYER)
         n_layers = -(-GEMV_WORKING_SET // layer_bytes)
-        mats, bufs = [], []
+        mats = []
         for li in range(n_layers):
             for mi, (r, c) in enumerate(GEMV_LAYER):
                 parts = {"bf16": [2 * r * c], "q8_0": [r * c, 2 * r * c // 32],
@@ -263,8 +266,6 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
             gbs = nbytes / (us_layer * 1e-6) / 1e9
             res[f"{fmt}_n{n}"] = {"us_per_layer": round(us_layer, 2), "bytes_per_layer": nbytes,
                                   "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-        for d in bufs:
-            hip_rt.free(d)
     # Greedy decode's lm_head: the argmax of the BF16 projection onto the
     # vocabulary (Qwen3-4B ties it to the token embeddings), 778 MB per call;
     # the call waits for its result, so the time includes the index's copy
@@ -282,9 +283,8 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
                              "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                              "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "kernels": "gemv_vec_kernel<bf16, argmax> + gemv_argmax_final_kernel"}
-    hip_rt.free(w)
-    hip_rt.free(x)
-    hip_rt.free(y)
+    for d in bufs + [w, x, y]:
+        hip_rt.free(d)
     return {"what": "Qwen3-4B layer weight gemvs (q, k, v, o, gate, up, down) per weight layout; n1 = one "
                     "vector (decode), n16 = a 16-token session batch; weights in HBM, rotated past the "
                     "Infinity Cache; seven launches per layer", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -316,6 +316,9 @@ def configs_bench(nh, hip_rt, synth) -> dict:
 
     lib = nh.load_library()
     out = {}
+    # Caches and fill buffers live until the end: nothing is freed before a
+    # timed step (the driver clears freed device memory in the background).
+    keep = []
 
     def build(cfg, n_ctx, n_batch):
         rows = [cfg.layer_rows(li, n_ctx, n_batch) for li in range(cfg.n_layer)]
@@ -323,6 +326,7 @@ def configs_bench(nh, hip_rt, synth) -> dict:
         st = kv.stream
         n_max = max(rows) * cfg.kv_dim
         k_dev, v_dev = hip_rt.malloc(4 * n_max), hip_rt.malloc(4 * n_max)
+        keep.append((kv, k_dev, v_dev))
         for li, r in enumerate(rows):
             seed = (synth.BASE_SEED + 1000 * cfg.index + li) * 256
             nh.fill_normal(k_dev, r * cfg.kv_dim, seed + 1, cfg.head_dim if cfg.qk_norm else 0, False, st)
@@ -332,8 +336,6 @@ def configs_bench(nh, hip_rt, synth) -> dict:
             if status:
                 raise nh.NncError(status, lib.nnc_hip_last_error().decode())
         kv.sync()
-        hip_rt.free(k_dev)
-        hip_rt.free(v_dev)
         return kv
 
     def measure(kv, calls, n_tok_max, n_out, cfg, reps):
@@ -398,15 +400,12 @@ def configs_bench(nh, hip_rt, synth) -> dict:
     kv = build(A, 1024, 1)
     decode_entry(A, "A_decode_1024", kv, 1024, reps=50)
     out["A_decode_1024"]["note"] = "18 x 2 MB of K/V stay in the 256 MB Infinity Cache: not an HBM rate"
-    kv.close()
     kv = build(B, 16384, 1)
     for ctx in (512, 4096, 16384):
         decode_entry(B, f"B_decode_{ctx}", kv, ctx)
-    kv.close()
     kv = build(Cc, 8192, 2048)
     decode_entry(Cc, "C_decode_8192", kv, 8192)
     prefill_entry(Cc, "C_prefill_8192", kv, 8192, 2048)
-    kv.close()
     n_ctx = 16384 + 256
     kv = build(E, n_ctx, 1024)
     prefill_entry(E, "E_prefill_16384", kv, 16384, 1024, reps=2)
@@ -420,7 +419,10 @@ def configs_bench(nh, hip_rt, synth) -> dict:
                            "ms_per_step": round(ms / 256, 4), "bytes_per_step": nbytes // 256, "value": round(gbs, 1),
                            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "replay_equals_eager": same}
     log(f"[bench] E_decode_256: {ms / 256 * 1e3:.1f} us/step, {gbs:.0f} GB/s")
-    kv.close()
+    for kv_, k_dev, v_dev in keep:
+        kv_.close()
+        hip_rt.free(k_dev)
+        hip_rt.free(v_dev)
     return out
 
 
@@ -497,19 +499,21 @@ def main() -> int:
     lib = nh.load_library()
     import ctypes as C
 
+    # The cache's own buffers are filled through the device generator:
+    # positions 0..CTX-1 of K (RMS-normed per head) and V, as appended. The
+    # fill buffers (like everything else) are freed only after the last
+    # timing: the driver clears freed device memory in the background, which
+    # takes HBM bandwidth for seconds (decode measured 30.2 instead of 28.55
+    # us per layer right after 8 GiB were freed).
+    k_dev = hip_rt.malloc(CTX * KV_DIM * 4)
+    v_dev = hip_rt.malloc(CTX * KV_DIM * 4)
     for li in range(N_LAYER):
-        # The cache's own buffers are filled through the device generator:
-        # positions 0..CTX-1 of K (RMS-normed per head) and V, as appended.
-        k_dev = hip_rt.malloc(CTX * KV_DIM * 4)
-        v_dev = hip_rt.malloc(CTX * KV_DIM * 4)
         nh.fill_normal(k_dev, CTX * KV_DIM, (1234 + 3000 + li) * 256 + 1, HD, False, stream)
         nh.fill_normal(v_dev, CTX * KV_DIM, (1234 + 3000 + li) * 256 + 2, 0, False, stream)
         st = lib.nnc_hip_kv_append_f32_device(kv.handle, li, 0, CTX, C.c_void_p(k_dev), C.c_void_p(v_dev))
         if st:
             raise nh.NncError(st, lib.nnc_hip_last_error().decode())
         kv.sync()
-        hip_rt.free(k_dev)
-        hip_rt.free(v_dev)
     q_dec = hip_rt.malloc(N_LAYER * N_HEAD * HD * 4)
     o_dec = hip_rt.malloc(N_LAYER * N_HEAD * HD * 4)
     q_pre = hip_rt.malloc(N_LAYER * PROMPT * N_HEAD * HD * 4)
@@ -565,7 +569,6 @@ def main() -> int:
         log(f"[bench] gemv {json.dumps(gemv_bench(nh, hip_rt, kv, stream, timed))}")
         return 0
     if args.only == "configs":
-        kv.close()
         from libllmcpu_amd import synth
 
         log(f"[bench] configs {json.dumps(configs_bench(nh, hip_rt, synth))}")
@@ -669,7 +672,6 @@ def main() -> int:
     if not args.no_cpu:
         log(f"[bench] cpu baseline ~{args.cpu_seconds:.0f} s per setting")
         cpu = cpu_baseline(kv, args.cpu_seconds)
-    kv.close()
 
     configs = None
     if not args.no_configs:
@@ -677,6 +679,9 @@ def main() -> int:
 
         log("[bench] other configurations")
         configs = configs_bench(nh, hip_rt, synth)
+    kv.close()
+    for p_ in (k_dev, v_dev, q_dec, o_dec, q_pre, o_pre):
+        hip_rt.free(p_)
 
     line = {
         "metric": METRIC,
@@ -725,8 +730,6 @@ def main() -> int:
         "wall_ms": {"decode": round(dec_wall, 2), "prefill": round(pre_wall, 2)},
     }
     print(json.dumps(line), flush=True)
-    for p in (q_dec, o_dec, q_pre, o_pre):
-        hip_rt.free(p)
     return 0
 
 

@@ -84,6 +84,70 @@ namespace nnchip
 		template <int HD>
 		constexpr int part_pitch() { return HD + 4; }
 
+		// The P operand of one 32-key half of a chunk (the 8 weights a lane
+		// supplies) and its part of the row sum, for O^T += V^T . P^T. F16 (V
+		// read from the cache's fp16 copy): P rounded to the nearest fp16, the
+		// sum from the same rounded weights (v_dot2_f32_f16), one MFMA per
+		// product. Else P split into bf16 hi + lo against the bf16 V (near-fp32),
+		// the sum of the fp32 weights, two MFMAs. Every BF16 decode kernel goes
+		// through these two functions, so a token's bits do not depend on which
+		// kernel computes it.
+		template <bool F16>
+		__device__ __forceinline__ void p_operand(const float (&w)[8], u32x4 (&pb)[2], float& lsum)
+		{
+			if constexpr (F16)
+			{
+				const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+#pragma unroll
+				for (int q = 0; q < 4; ++q)
+				{
+					const uint32_t w2 = pack_f16x2(w[2 * q], w[2 * q + 1]);
+					pb[0][q] = w2;
+					lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, lsum, false);
+				}
+			}
+			else
+			{
+#pragma unroll
+				for (int e = 0; e < 8; ++e) lsum += w[e];
+				bf16x8 hi, lo;
+				split_bf16x8(w, hi, lo);
+				pb[0] = __builtin_bit_cast(u32x4, hi);
+				pb[1] = __builtin_bit_cast(u32x4, lo);
+			}
+		}
+
+		template <bool F16>
+		__device__ __forceinline__ void pv_mfma(f32x4& acc, const u32x4& v, const u32x4 (&pb)[2])
+		{
+			if constexpr (F16)
+				acc = mfma16x16x32(as_f16x8(v), as_f16x8(pb[0]), acc);
+			else
+			{
+				acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[0]), acc);
+				acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[1]), acc);
+			}
+		}
+
+		// Scores of one 16-key tile against Q split into bf16 hi + lo: the hi
+		// products and the lo products each accumulate over d in their own
+		// chain, and the two sums are added once. (The one-token kernel puts Q's
+		// lo halves in spare MFMA columns and adds the columns instead: the
+		// same two chains, the same final addition.)
+		template <int KK>
+		__device__ __forceinline__ f32x4 scores_hilo(const u32x4 (&k)[KK], const bf16x8 (&qh)[KK], const bf16x8 (&ql)[KK])
+		{
+			f32x4 sh = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, sl = sh;
+#pragma unroll
+			for (int kk = 0; kk < KK; ++kk)
+			{
+				const bf16x8 a = as_bf16x8(k[kk]);
+				sh = mfma16x16x32(a, qh[kk], sh);
+				sl = mfma16x16x32(a, ql[kk], sl);
+			}
+			return sh + sl;
+		}
+
 		// The work-group's result from its wavefronts' partials in s_wpart
 		// (o[head_dim], m, l per column, per wavefront). The work-group holds
 		// the HPW KV heads of head group hg (head_of); wavefront w works for
@@ -680,7 +744,11 @@ namespace nnchip
 			const int s1 = min(lL, send);
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const __amdgpu_buffer_rsrc_t rk = layer_rsrc(p.K, static_cast<uint32_t>(p.rows) * row_bytes);
-			const __amdgpu_buffer_rsrc_t rv = layer_rsrc(p.V, static_cast<uint32_t>(p.rows) * row_bytes);
+			// V from its fp16 copy when the cache has one and every value in it
+			// fits fp16 (then P goes in fp16, one MFMA per product).
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
+			const __amdgpu_buffer_rsrc_t rv =
+				layer_rsrc(use16 ? p.V16 : p.V, static_cast<uint32_t>(p.rows) * row_bytes);
 			const uint32_t k_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * grp; // + 64 kk
 			const uint32_t v_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * (lane % LPK);
 			uint16_t* vt = s_v[wave];
@@ -732,9 +800,15 @@ namespace nnchip
 
 			// Q first (its loads return before the K/V rows issued after them),
 			// then the first two chunks of K and V, then Q^T as the B operand,
-			// scaled into log2 units and split into bf16 hi + lo.
-			const bool q_ok = tt < n_tt;
-			const float* qp = p.q + (static_cast<size_t>(tok0 + (q_ok ? tt : 0)) * p.n_head + kvh * G + col % G) * HD + 8 * grp;
+			// scaled into log2 units and split into bf16 hi + lo. One token
+			// (PACK): column c < G holds head c's hi half and column G + c its lo
+			// half, so a score takes one MFMA per 32 elements of d (the columns
+			// are added after); columns from 2G on are zero.
+			constexpr bool PACK = T == 1;
+			static_assert(!PACK || 2 * G <= 16, "packed columns");
+			const bool q_ok = PACK ? col < 2 * G : tt < n_tt;
+			const float* qp =
+				p.q + (static_cast<size_t>(tok0 + (PACK || !q_ok ? 0 : tt)) * p.n_head + kvh * G + col % G) * HD + 8 * grp;
 			float4 qa[KK], qb[KK];
 #pragma unroll
 			for (int kk = 0; kk < KK; ++kk)
@@ -760,6 +834,8 @@ namespace nnchip
 #pragma unroll
 				for (int j = 0; j < 8; ++j) x[j] = q_ok ? x[j] : 0.0f;
 				split_bf16x8(x, qhi[kk], qlo[kk]);
+				if constexpr (PACK)
+					if (col >= G) qhi[kk] = qlo[kk]; // this lane's B operand is qhi
 			}
 
 			float m_run = -INFINITY, l_run = 0.0f;
@@ -768,8 +844,9 @@ namespace nnchip
 			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
 			// The wavefront's i-th chunk from X; X is then reloaded with chunk i + DEPTH.
-			auto chunk = [&](regs& X, int i) __attribute__((always_inline))
+			auto chunk = [&](auto f16_tag, regs& X, int i) __attribute__((always_inline))
 			{
+				constexpr bool F16 = decltype(f16_tag)::value;
 				int cbase, clo, chi, rb;
 				chunk_bounds(c_wave + i * LPH, cbase, clo, chi, rb);
 
@@ -777,14 +854,20 @@ namespace nnchip
 #pragma unroll
 				for (int t = 0; t < NT; ++t)
 				{
-					sc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-					for (int kk = 0; kk < KK; ++kk)
+					if constexpr (PACK)
 					{
-						const bf16x8 a = as_bf16x8(X.k[t][kk]);
-						sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
-						sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
+						f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+						for (int kk = 0; kk < KK; ++kk) s = mfma16x16x32(as_bf16x8(X.k[t][kk]), qhi[kk], s);
+						// column c + G (lane + G of the 16-lane row) holds the lo sum
+#pragma unroll
+						for (int e = 0; e < 4; ++e)
+							s[e] = s[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s[e]), 0x100 + G, 0xf,
+							                                                         0xf, false));
+						sc[t] = s;
 					}
+					else
+						sc[t] = scores_hilo<KK>(X.k[t], qhi, qlo);
 				}
 				const bool reload = i + DEPTH < n_wchunks; // uniform
 				if (reload) load_k(X, i + DEPTH);
@@ -815,7 +898,7 @@ namespace nnchip
 				const float alpha = fast_exp2(m_run - m_use);
 				m_run = m_new;
 				float lsum = 0.0f;
-				bf16x8 phi[NC], plo[NC];
+				u32x4 pb[NC][2];
 #pragma unroll
 				for (int c = 0; c < NC; ++c)
 				{
@@ -826,9 +909,7 @@ namespace nnchip
 						w[e] = fast_exp2(sc[2 * c][e] - m_use);
 						w[4 + e] = fast_exp2(sc[2 * c + 1][e] - m_use);
 					}
-#pragma unroll
-					for (int e = 0; e < 8; ++e) lsum += w[e];
-					split_bf16x8(w, phi[c], plo[c]);
+					p_operand<F16>(w, pb[c], lsum);
 				}
 				l_run = l_run * alpha + lsum;
 #pragma unroll
@@ -843,20 +924,25 @@ namespace nnchip
 						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
 						const u32x2 lo = vt_read(r0);
 						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-						const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-						acc_o[db] = mfma16x16x32(a, phi[c], acc_o[db]);
-						acc_o[db] = mfma16x16x32(a, plo[c], acc_o[db]);
+						pv_mfma<F16>(acc_o[db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
 					}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			int i = 0;
-			if constexpr (DEPTH == 2)
-				for (; i + 1 < n_wchunks; i += 2)
-				{
-					chunk(X0, i);
-					chunk(X1, i + 1);
-				}
-			for (; i < n_wchunks; ++i) chunk(X0, i);
+			auto run = [&](auto f16_tag) __attribute__((always_inline))
+			{
+				int i = 0;
+				if constexpr (DEPTH == 2)
+					for (; i + 1 < n_wchunks; i += 2)
+					{
+						chunk(f16_tag, X0, i);
+						chunk(f16_tag, X1, i + 1);
+					}
+				for (; i < n_wchunks; ++i) chunk(f16_tag, X0, i);
+			};
+			if (use16)
+				run(std::true_type{});
+			else
+				run(std::false_type{});
 
 			// Wavefront partial: each (head, d) of O^T has one owner lane.
 			l_run += __shfl_xor(l_run, 16);
@@ -929,7 +1015,10 @@ namespace nnchip
 			const int s1 = min(lL, send);
 			const size_t head_off = static_cast<size_t>(kvh) * HD;
 			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
-			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
+			// V from its fp16 copy when the cache has one and every value in it
+			// fits fp16 (as in decode_bf16_kernel).
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
+			const uint16_t* Vg = static_cast<const uint16_t*>(use16 ? p.V16 : p.V) + head_off;
 			uint16_t* vt = s_v[wave];
 
 			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
@@ -1028,18 +1117,31 @@ namespace nnchip
 				for (int db = 0; db < DB; ++db) acc_o[tl][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 			}
 
-			auto chunk = [&](int cw) __attribute__((always_inline))
+			auto chunk = [&](auto f16_tag, int cw) __attribute__((always_inline))
 			{
+				constexpr bool F16 = decltype(f16_tag)::value;
 				int cbase, clo, chi, rb;
 				chunk_bounds(cw, cbase, clo, chi, rb);
+				// This chunk's V rows (loaded through the previous chunk) into the
+				// wavefront's V^T tile first, so their registers are free for the
+				// scores.
+#pragma unroll
+				for (int j = 0; j < NV; ++j)
+					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
 
-				f32x4 sc[NTL][NT];
+				wave_sync();
+
+				// One tile at a time: its scores (the hi and lo products in their
+				// own chains, added once: the operations of scores_hilo), then its
+				// softmax and P.V. The next chunk's K and V rows load once the
+				// last tile's scores no longer need the K registers.
 #pragma unroll
 				for (int tl = 0; tl < NTL; ++tl)
+				{
+					// (the lo chain accumulates in sc, the hi chain in sh)
+					f32x4 sc[NT], sh[NT];
 #pragma unroll
-					for (int t = 0; t < NT; ++t) sc[tl][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-				for (int tl = 0; tl < NTL; ++tl)
+					for (int t = 0; t < NT; ++t) sh[t] = sc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
 					for (int kk = 0; kk < KK; ++kk)
 					{
@@ -1049,21 +1151,18 @@ namespace nnchip
 						for (int t = 0; t < NT; ++t)
 						{
 							const bf16x8 a = as_bf16x8(kreg[t][kk]);
-							sc[tl][t] = mfma16x16x32(a, qh, sc[tl][t]);
-							sc[tl][t] = mfma16x16x32(a, ql, sc[tl][t]);
+							sh[t] = mfma16x16x32(a, qh, sh[t]);
+							sc[t] = mfma16x16x32(a, ql, sc[t]);
 						}
 					}
-				load_k(cw + LPH);
-
 #pragma unroll
-				for (int j = 0; j < NV; ++j)
-					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
-				load_v(cw + LPH);
-				wave_sync();
+					for (int t = 0; t < NT; ++t) sc[t] = sh[t] + sc[t];
+					if (tl == NTL - 1)
+					{
+						load_k(cw + LPH);
+						load_v(cw + LPH);
+					}
 
-#pragma unroll
-				for (int tl = 0; tl < NTL; ++tl)
-				{
 					float m_loc = -INFINITY;
 #pragma unroll
 					for (int t = 0; t < NT; ++t)
@@ -1071,8 +1170,8 @@ namespace nnchip
 						for (int i = 0; i < 4; ++i)
 						{
 							const int k = cbase + 16 * t + 4 * grp + i;
-							const float v = (k >= col_s0[tl] && k <= col_s1[tl]) ? sc[tl][t][i] : -INFINITY;
-							sc[tl][t][i] = v;
+							const float v = (k >= col_s0[tl] && k <= col_s1[tl]) ? sc[t][i] : -INFINITY;
+							sc[t][i] = v;
 							m_loc = fmaxf(m_loc, v);
 						}
 					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
@@ -1082,7 +1181,7 @@ namespace nnchip
 					const float alpha = fast_exp2(m_run[tl] - m_use);
 					m_run[tl] = m_new;
 					float lsum = 0.0f;
-					bf16x8 phi[NC], plo[NC];
+					u32x4 pb[NC][2];
 #pragma unroll
 					for (int c = 0; c < NC; ++c)
 					{
@@ -1090,12 +1189,10 @@ namespace nnchip
 #pragma unroll
 						for (int i = 0; i < 4; ++i)
 						{
-							w[i] = fast_exp2(sc[tl][2 * c][i] - m_use);
-							w[4 + i] = fast_exp2(sc[tl][2 * c + 1][i] - m_use);
+							w[i] = fast_exp2(sc[2 * c][i] - m_use);
+							w[4 + i] = fast_exp2(sc[2 * c + 1][i] - m_use);
 						}
-#pragma unroll
-						for (int i = 0; i < 8; ++i) lsum += w[i];
-						split_bf16x8(w, phi[c], plo[c]);
+						p_operand<F16>(w, pb[c], lsum);
 					}
 					l_run[tl] = l_run[tl] * alpha + lsum;
 #pragma unroll
@@ -1108,14 +1205,15 @@ namespace nnchip
 							const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
 							const u32x2 lo = vt_read(r0);
 							const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-							const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-							acc_o[tl][db] = mfma16x16x32(a, phi[c], acc_o[tl][db]);
-							acc_o[tl][db] = mfma16x16x32(a, plo[c], acc_o[tl][db]);
+							pv_mfma<F16>(acc_o[tl][db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
 						}
 				}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(c_wave);
+			if (use16)
+				for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(std::true_type{}, c_wave);
+			else
+				for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(std::false_type{}, c_wave);
 
 			// One tile at a time through the wavefront merge; a wavefront's
 			// partials go into its own V tile (read by it only until here).

@@ -16,6 +16,8 @@ namespace nnchip
 		float* out; // [n_tok][n_head * head_dim]
 		const void* K; // [rows][kv_dim], BF16 bits or F32
 		const void* V;
+		const void* V16; // BF16 caches: V's fp16 copy, or null
+		const int* n_bad; // elements of the copy past fp16's range (kF16Bad); not 0: use V
 		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		float* part; // [n_tok][n_kv][n_split][group][head_dim + 4]: o, then m (log2 units), then l
 		int rows, kv_dim, n_head, n_kv;

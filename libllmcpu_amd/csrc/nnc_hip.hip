@@ -401,6 +401,8 @@ namespace
 		p.gate = gate;
 		p.K = b.k;
 		p.V = b.v;
+		p.V16 = b.v16;
+		p.n_bad = b.v16 ? kv->n_bad + (&b - kv->bufs.data()) : nullptr;
 		p.part = part;
 		p.rows = b.rows;
 		p.kv_dim = b.kv_dim;
