@@ -213,48 +213,43 @@ namespace nnchip
 			}
 		}
 
-		// max over the wavefront, on every lane (DPP within 16-lane rows, then
-		// the permlane swaps across rows).
-		__device__ __forceinline__ float wave_max_dpp(float x)
-		{
-			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false)));
-			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false)));
-			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false)));
-			x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false)));
-			const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-			x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-			return max_with_other_half(x);
-		}
-
-		// LDS of one merge (256 threads).
-		template <int HD>
+		// A merge work-group takes 1 / SLICES of one (token, query head)'s
+		// HD / 4 float4 columns of o: COLS columns times PARTS parts of the
+		// splits, 256 / SLICES threads.
+		template <int HD, int SLICES>
 		struct merge_lds
 		{
-			static constexpr int PARTS = 1024 / HD; // 256 threads over HD / 4 float4s of o
-			float m[kDecodeMaxSplits], l[kDecodeMaxSplits];
-			float4 o[PARTS][HD / 4];
-			float ls[PARTS];
-			float wmax[4];
+			static constexpr int PARTS = 1024 / HD, COLS = HD / 4 / SLICES, THREADS = COLS * PARTS;
+			float4 o[PARTS][COLS];
+			float ls[PARTS], ms[PARTS];
 		};
 
 		// Merges the n_split partials of one (token, query head) and writes
-		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492). 256 threads:
-		// thread t owns elements 4 (t % (HD / 4)) .. + 3 of o for the splits
-		// of part t / (HD / 4), so a work-group's loads are issued together,
-		// 16 per thread at a time. A split belongs to part (its absolute
-		// number, split_base / split_keys + s) % PARTS; o and l are summed in
-		// ascending split order within a part, then the parts in order. A
-		// split outside the token's span holds m = -inf, l = 0, o = 0 and adds
-		// exact zeros, and the parts are fixed by the absolute split grid, so
-		// a token's result depends only on its own splits, whatever else the
-		// launch covered.
-		template <int HD, int G>
-		__device__ __forceinline__ void merge_splits(const decode_params& p, int tok, int qh, merge_lds<HD>& sh)
+		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492), columns
+		// COLS * slice .. + COLS - 1 of it. Lane t owns float4 column
+		// COLS * slice + t % COLS of o for the splits of part t / COLS, whose
+		// o, m and l it loads together (16 splits per batch), so the common
+		// case is one round trip to memory and one barrier. Every element goes
+		// through the same operations whatever SLICES is.
+		// (For one token, four one-wavefront work-groups per head spread the
+		// reads over more CUs than one 256-thread work-group: 0.5 us less per
+		// call at 64 splits; for 16 tokens they are 2.9 us slower.) A split belongs to part (its absolute number,
+		// split_base / split_keys + s) % PARTS; a part sums its splits in
+		// ascending order against its own largest m, then the parts are summed
+		// in order, each scaled by 2^(its m - the largest). A split outside
+		// the token's span holds m = -inf, l = 0, o = 0 and adds exact zeros,
+		// and the parts are fixed by the absolute split grid, so a token's
+		// result depends only on its own splits, whatever else the launch
+		// covered.
+		template <int HD, int G, int SLICES>
+		__device__ __forceinline__ void merge_splits(const decode_params& p, int tok, int qh, int slice,
+		                                             merge_lds<HD, SLICES>& sh)
 		{
-			constexpr int PL = part_pitch<HD>(), Q4 = HD / 4, PARTS = merge_lds<HD>::PARTS, B = 16;
+			using S = merge_lds<HD, SLICES>;
+			constexpr int PL = part_pitch<HD>(), COLS = S::COLS, PARTS = S::PARTS, B = 16;
 			const int kvh = qh / G, h = qh % G;
 			const int ns = p.n_split;
-			const int d4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
+			const int c = threadIdx.x % COLS, part = threadIdx.x / COLS, d4 = COLS * slice + c;
 			const size_t sstride = static_cast<size_t>(G) * PL;
 			const float* hp = p.part + ((static_cast<size_t>(tok) * p.n_kv + kvh) * ns * G + h) * PL;
 			// This part's splits: s_first, s_first + PARTS, ... below ns.
@@ -265,71 +260,68 @@ namespace nnchip
 			// A batch of B of them (indices clamped to a valid split; the ones
 			// past the part's last are not used).
 			float4 o[B];
+			float2 ml[B];
 			auto load_batch = [&](int b0) __attribute__((always_inline))
 			{
 #pragma unroll
 				for (int u = 0; u < B; ++u)
-					o[u] = *reinterpret_cast<const float4*>(hp + min(s_first + PARTS * (b0 + u), ns - 1) * sstride + 4 * d4);
+				{
+					const float* sp = hp + min(s_first + PARTS * (b0 + u), ns - 1) * sstride;
+					o[u] = *reinterpret_cast<const float4*>(sp + 4 * d4);
+					ml[u] = *reinterpret_cast<const float2*>(sp + HD);
+				}
 			};
 			load_batch(0);
-			float mx = -INFINITY;
-			for (int s = threadIdx.x; s < ns; s += 256)
-			{
-				const float2 ml = *reinterpret_cast<const float2*>(hp + s * sstride + HD);
-				sh.m[s] = ml.x;
-				sh.l[s] = ml.y;
-				mx = fmaxf(mx, ml.x);
-			}
-			// The maximum over the splits: per wavefront by DPP and lane swaps,
-			// then over the four wavefronts through LDS.
-			mx = wave_max_dpp(mx);
-			if ((threadIdx.x & 63) == 0) sh.wmax[threadIdx.x >> 6] = mx;
-			__syncthreads();
-			mx = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
-			const float m_use = mx == -INFINITY ? 0.0f : mx;
+			float mp = -INFINITY;
+#pragma unroll
+			for (int u = 0; u < B; ++u)
+				if (u < n_mine) mp = fmaxf(mp, ml[u].x);
+			for (int i = B; i < n_mine; ++i) mp = fmaxf(mp, hp[(s_first + PARTS * i) * sstride + HD]);
+			const float m_use = mp == -INFINITY ? 0.0f : mp;
 			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 			float L = 0.0f;
 			for (int b0 = 0; b0 < n_mine; b0 += B)
 			{
 				if (b0 > 0) load_batch(b0);
-				float mw[B], lw[B];
-#pragma unroll
-				for (int u = 0; u < B; ++u)
-				{
-					const int s = min(s_first + PARTS * (b0 + u), ns - 1);
-					mw[u] = sh.m[s];
-					lw[u] = sh.l[s];
-				}
 #pragma unroll
 				for (int u = 0; u < B; ++u)
 				{
 					if (b0 + u < n_mine)
 					{
-						const float f = fast_exp2(mw[u] - m_use);
+						const float f = fast_exp2(ml[u].x - m_use);
 						acc.x = fmaf(o[u].x, f, acc.x);
 						acc.y = fmaf(o[u].y, f, acc.y);
 						acc.z = fmaf(o[u].z, f, acc.z);
 						acc.w = fmaf(o[u].w, f, acc.w);
-						L = fmaf(lw[u], f, L);
+						L = fmaf(ml[u].y, f, L);
 					}
 				}
 			}
-			sh.o[part][d4] = acc;
-			if (d4 == 0) sh.ls[part] = L;
+			sh.o[part][c] = acc;
+			if (c == 0)
+			{
+				sh.ls[part] = L;
+				sh.ms[part] = mp;
+			}
 			__syncthreads();
 			if (part == 0)
 			{
-				float4 r = sh.o[0][d4];
-				float lt = sh.ls[0];
+				float M = sh.ms[0];
 #pragma unroll
-				for (int j = 1; j < PARTS; ++j)
+				for (int j = 1; j < PARTS; ++j) M = fmaxf(M, sh.ms[j]);
+				const float M_use = M == -INFINITY ? 0.0f : M;
+				float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				float lt = 0.0f;
+#pragma unroll
+				for (int j = 0; j < PARTS; ++j)
 				{
-					const float4 v = sh.o[j][d4];
-					r.x += v.x;
-					r.y += v.y;
-					r.z += v.z;
-					r.w += v.w;
-					lt += sh.ls[j];
+					const float f = fast_exp2(sh.ms[j] - M_use);
+					const float4 v = sh.o[j][c];
+					r.x = fmaf(v.x, f, r.x);
+					r.y = fmaf(v.y, f, r.y);
+					r.z = fmaf(v.z, f, r.z);
+					r.w = fmaf(v.w, f, r.w);
+					lt = fmaf(sh.ls[j], f, lt);
 				}
 				const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 				const size_t oi = (static_cast<size_t>(tok) * p.n_head + qh) * HD + 4 * d4;
@@ -342,17 +334,17 @@ namespace nnchip
 			}
 		}
 
-		// The split merge, launched after the split kernel: one work-group per
-		// (query head, token). (A merge inside the split launch, by extra
+		// The split merge, launched after the split kernel: SLICES work-groups
+		// per (query head, token). (A merge inside the split launch, by extra
 		// work-groups that wait on per-head counts and read the partials with
 		// device-coherent loads, measured slower: 35 vs 32 us per call at 32k
 		// keys, the coherent loads and the polling being slower than the
 		// launch boundary.)
-		template <int HD, int G>
-		__global__ __launch_bounds__(256) void decode_merge_kernel(const decode_params p)
+		template <int HD, int G, int SLICES>
+		__global__ __launch_bounds__(256 / SLICES) void decode_merge_kernel(const decode_params p)
 		{
-			__shared__ merge_lds<HD> sh;
-			merge_splits<HD, G>(p, blockIdx.y, blockIdx.x, sh);
+			__shared__ merge_lds<HD, SLICES> sh;
+			merge_splits<HD, G, SLICES>(p, blockIdx.y, blockIdx.x / SLICES, blockIdx.x % SLICES, sh);
 		}
 
 		// F32 K/V: scores on MFMA with both operands split into bf16 hi + lo
@@ -1287,7 +1279,13 @@ namespace nnchip
 			}
 			else
 				f32_decode_kernel<HD, G><<<dim3(p.n_split, p.n_kv, n_tok), 256, 0, stream>>>(p);
-			if (p.n_split > 1) decode_merge_kernel<HD, G><<<dim3(p.n_kv * G, n_tok), 256, 0, stream>>>(p);
+			// The merge: a quarter head per work-group while that makes at most
+			// 256 work-groups, else whole heads.
+			if (p.n_split > 1 && p.n_kv * G * n_tok <= 64)
+				decode_merge_kernel<HD, G, 4>
+					<<<dim3(p.n_kv * G * 4, n_tok), merge_lds<HD, 4>::THREADS, 0, stream>>>(p);
+			else if (p.n_split > 1)
+				decode_merge_kernel<HD, G, 1><<<dim3(p.n_kv * G, n_tok), merge_lds<HD, 1>::THREADS, 0, stream>>>(p);
 		}
 
 		template <int HD, bool BF16>

@@ -45,7 +45,7 @@ namespace nnchip
 	int decode_wg_keys(int head_dim, bool bf16, int n_kv);
 
 	// Launches the decode kernel over an (n_split, head groups, token groups)
-	// grid, then (n_split > 1) the split merge over (n_kv * group, n_tok);
+	// grid, then (n_split > 1) the split merge over (n_kv * group * slices, n_tok);
 	// returns false when (head_dim, group, bf16) has no instantiation. A
 	// token's result depends only on its own span and the split grid
 	// (split_keys and the absolute split boundaries), not on the other tokens
