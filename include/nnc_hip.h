@@ -68,10 +68,10 @@ typedef struct nnc_hip_kv nnc_hip_kv;
  * model.cpp:1908-1957; rows come from the same rule: n_ctx, or a ring of
  * round_up(window + n_batch, 256) rows for a sliding layer). A BF16 cache
  * also keeps an fp16 copy of every V buffer, written by every append, for the
- * prefill kernel, which uses it while every value in it fits fp16 (1.5 times
- * the device memory of K and V alone; NNC_HIP_F16_SHADOW=0 in the environment
- * at creation leaves it out, and prefill then runs slower). The nnc-visible
- * buffers stay BF16 in nnc's layout.
+ * prefill kernel, which uses it while every value in it is within +-32 (1.5
+ * times the device memory of K and V alone; NNC_HIP_F16_SHADOW=0 in the
+ * environment at creation leaves it out, and prefill then runs slower). The
+ * nnc-visible buffers stay BF16 in nnc's layout.
  * NNC_ERR_INVALID_ARGUMENT: n_buf <= 0, a NULL pointer, rows or kv_dim <= 0.
  * NNC_ERR_OUT_OF_MEMORY: the device allocation failed.
  * NNC_ERR_UNSUPPORTED_CPU: no usable HIP device (the nearest existing status:

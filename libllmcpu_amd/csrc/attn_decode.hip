@@ -85,48 +85,27 @@ namespace nnchip
 		constexpr int part_pitch() { return HD + 4; }
 
 		// The P operand of one 32-key half of a chunk (the 8 weights a lane
-		// supplies) and its part of the row sum, for O^T += V^T . P^T. F16 (V
-		// read from the cache's fp16 copy): P rounded to the nearest fp16, the
-		// sum from the same rounded weights (v_dot2_f32_f16), one MFMA per
-		// product. Else P split into bf16 hi + lo against the bf16 V (near-fp32),
-		// the sum of the fp32 weights, two MFMAs. Every BF16 decode kernel goes
-		// through these two functions, so a token's bits do not depend on which
-		// kernel computes it.
-		template <bool F16>
+		// supplies) and its part of the row sum, for O^T += V^T . P^T: P split
+		// into bf16 hi + lo against the exact bf16 V (near-fp32), the sum of
+		// the fp32 weights, two MFMAs per product. Every BF16 decode kernel
+		// goes through these two functions, so a token's bits do not depend on
+		// which kernel computes it. (P rounded to fp16 against V's fp16 copy,
+		// one MFMA per product, was 0.5 % faster per Qwen3-4B decode call but
+		// its error grows with |V|: 2e-2 max-abs where V reaches 400.)
 		__device__ __forceinline__ void p_operand(const float (&w)[8], u32x4 (&pb)[2], float& lsum)
 		{
-			if constexpr (F16)
-			{
-				const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
-				for (int q = 0; q < 4; ++q)
-				{
-					const uint32_t w2 = pack_f16x2(w[2 * q], w[2 * q + 1]);
-					pb[0][q] = w2;
-					lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, lsum, false);
-				}
-			}
-			else
-			{
-#pragma unroll
-				for (int e = 0; e < 8; ++e) lsum += w[e];
-				bf16x8 hi, lo;
-				split_bf16x8(w, hi, lo);
-				pb[0] = __builtin_bit_cast(u32x4, hi);
-				pb[1] = __builtin_bit_cast(u32x4, lo);
-			}
+			for (int e = 0; e < 8; ++e) lsum += w[e];
+			bf16x8 hi, lo;
+			split_bf16x8(w, hi, lo);
+			pb[0] = __builtin_bit_cast(u32x4, hi);
+			pb[1] = __builtin_bit_cast(u32x4, lo);
 		}
 
-		template <bool F16>
 		__device__ __forceinline__ void pv_mfma(f32x4& acc, const u32x4& v, const u32x4 (&pb)[2])
 		{
-			if constexpr (F16)
-				acc = mfma16x16x32(as_f16x8(v), as_f16x8(pb[0]), acc);
-			else
-			{
-				acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[0]), acc);
-				acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[1]), acc);
-			}
+			acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[0]), acc);
+			acc = mfma16x16x32(as_bf16x8(v), as_bf16x8(pb[1]), acc);
 		}
 
 		// Scores of one 16-key tile against Q split into bf16 hi + lo: the hi
@@ -736,11 +715,7 @@ namespace nnchip
 			const int s1 = min(lL, send);
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const __amdgpu_buffer_rsrc_t rk = layer_rsrc(p.K, static_cast<uint32_t>(p.rows) * row_bytes);
-			// V from its fp16 copy when the cache has one and every value in it
-			// fits fp16 (then P goes in fp16, one MFMA per product).
-			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
-			const __amdgpu_buffer_rsrc_t rv =
-				layer_rsrc(use16 ? p.V16 : p.V, static_cast<uint32_t>(p.rows) * row_bytes);
+			const __amdgpu_buffer_rsrc_t rv = layer_rsrc(p.V, static_cast<uint32_t>(p.rows) * row_bytes);
 			const uint32_t k_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * grp; // + 64 kk
 			const uint32_t v_col = static_cast<uint32_t>(kvh) * HD * 2 + 16 * (lane % LPK);
 			uint16_t* vt = s_v[wave];
@@ -836,9 +811,8 @@ namespace nnchip
 			for (int db = 0; db < DB; ++db) acc_o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
 			// The wavefront's i-th chunk from X; X is then reloaded with chunk i + DEPTH.
-			auto chunk = [&](auto f16_tag, regs& X, int i) __attribute__((always_inline))
+			auto chunk = [&](regs& X, int i) __attribute__((always_inline))
 			{
-				constexpr bool F16 = decltype(f16_tag)::value;
 				int cbase, clo, chi, rb;
 				chunk_bounds(c_wave + i * LPH, cbase, clo, chi, rb);
 
@@ -901,7 +875,7 @@ namespace nnchip
 						w[e] = fast_exp2(sc[2 * c][e] - m_use);
 						w[4 + e] = fast_exp2(sc[2 * c + 1][e] - m_use);
 					}
-					p_operand<F16>(w, pb[c], lsum);
+					p_operand(w, pb[c], lsum);
 				}
 				l_run = l_run * alpha + lsum;
 #pragma unroll
@@ -916,25 +890,18 @@ namespace nnchip
 						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
 						const u32x2 lo = vt_read(r0);
 						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-						pv_mfma<F16>(acc_o[db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
+						pv_mfma(acc_o[db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
 					}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			auto run = [&](auto f16_tag) __attribute__((always_inline))
-			{
-				int i = 0;
-				if constexpr (DEPTH == 2)
-					for (; i + 1 < n_wchunks; i += 2)
-					{
-						chunk(f16_tag, X0, i);
-						chunk(f16_tag, X1, i + 1);
-					}
-				for (; i < n_wchunks; ++i) chunk(f16_tag, X0, i);
-			};
-			if (use16)
-				run(std::true_type{});
-			else
-				run(std::false_type{});
+			int i = 0;
+			if constexpr (DEPTH == 2)
+				for (; i + 1 < n_wchunks; i += 2)
+				{
+					chunk(X0, i);
+					chunk(X1, i + 1);
+				}
+			for (; i < n_wchunks; ++i) chunk(X0, i);
 
 			// Wavefront partial: each (head, d) of O^T has one owner lane.
 			l_run += __shfl_xor(l_run, 16);
@@ -1007,10 +974,7 @@ namespace nnchip
 			const int s1 = min(lL, send);
 			const size_t head_off = static_cast<size_t>(kvh) * HD;
 			const uint16_t* Kg = static_cast<const uint16_t*>(p.K) + head_off;
-			// V from its fp16 copy when the cache has one and every value in it
-			// fits fp16 (as in decode_bf16_kernel).
-			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
-			const uint16_t* Vg = static_cast<const uint16_t*>(use16 ? p.V16 : p.V) + head_off;
+			const uint16_t* Vg = static_cast<const uint16_t*>(p.V) + head_off;
 			uint16_t* vt = s_v[wave];
 
 			const int c_first = s0 <= s1 ? (s0 - sbase) / CH : 0;
@@ -1109,9 +1073,8 @@ namespace nnchip
 				for (int db = 0; db < DB; ++db) acc_o[tl][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 			}
 
-			auto chunk = [&](auto f16_tag, int cw) __attribute__((always_inline))
+			auto chunk = [&](int cw) __attribute__((always_inline))
 			{
-				constexpr bool F16 = decltype(f16_tag)::value;
 				int cbase, clo, chi, rb;
 				chunk_bounds(cw, cbase, clo, chi, rb);
 				// This chunk's V rows (loaded through the previous chunk) into the
@@ -1184,7 +1147,7 @@ namespace nnchip
 							w[i] = fast_exp2(sc[2 * c][i] - m_use);
 							w[4 + i] = fast_exp2(sc[2 * c + 1][i] - m_use);
 						}
-						p_operand<F16>(w, pb[c], lsum);
+						p_operand(w, pb[c], lsum);
 					}
 					l_run[tl] = l_run[tl] * alpha + lsum;
 #pragma unroll
@@ -1197,15 +1160,12 @@ namespace nnchip
 							const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
 							const u32x2 lo = vt_read(r0);
 							const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-							pv_mfma<F16>(acc_o[tl][db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
+							pv_mfma(acc_o[tl][db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
 						}
 				}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
-			if (use16)
-				for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(std::true_type{}, c_wave);
-			else
-				for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(std::false_type{}, c_wave);
+			for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(c_wave);
 
 			// One tile at a time through the wavefront merge; a wavefront's
 			// partials go into its own V tile (read by it only until here).
@@ -1233,6 +1193,7 @@ namespace nnchip
 				__syncthreads(); // the partials are read before the next tile overwrites them
 			}
 		}
+
 
 		// Keys per wavefront chunk of the BF16 kernel (4 wavefronts, one per
 		// SIMD). Measured at 32k keys: 8 wavefronts of 32-key chunks (two per

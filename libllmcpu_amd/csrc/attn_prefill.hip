@@ -21,10 +21,11 @@
 // wavefront then keeps both halves of its B operand in registers (at
 // head_dim 256 it reads them from LDS). V comes from one of two copies:
 //   - an fp16 copy (exact copies of the bf16 values, kept beside the cache
-//     and used while every value in it fits fp16): P goes in fp16 rounded to
-//     nearest, one MFMA per product;
-//   - the bf16 V itself (no copy, or a value past fp16's range in it): P is
-//     split into bf16 hi + lo, two MFMAs per product, near-fp32.
+//     and used while every value in it is within +-32, kF16CopyMax, where
+//     P's rounding stays well inside the tolerance): P goes in fp16 rounded
+//     to nearest, one MFMA per product;
+//   - the bf16 V itself (no copy, or a larger value in it): P is split into
+//     bf16 hi + lo, two MFMAs per product, near-fp32.
 // Per step, a key group's 32 K rows and 32 V rows arrive in its LDS tiles
 // by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled in
 // 16-byte slots so the reads below are conflict-free), issued during the
@@ -251,7 +252,7 @@ namespace nnchip
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
 			// V's fp16 copy when the buffer has one and every value now in it
-			// fits fp16; else the bf16 V itself.
+			// is within the copy's limit; else the bf16 V itself.
 			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
 			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
 			const char* vbase = static_cast<const char*>(use16 ? p.V16 : p.V) + head_bytes;

@@ -164,18 +164,24 @@ namespace nnchip
 
 	__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-	// The fp16 copy of a BF16 K/V element kept for the prefill kernel (RNE;
-	// exact for every finite bf16 up to 65504 in magnitude down to 2^-14, and
-	// within 2^-25 below). A finite value past fp16's range is stored as
-	// kF16Bad, a NaN pattern that no conversion of a bf16 value produces (its
-	// lowest mantissa bit is set, where bf16's 7 mantissa bits fill only fp16's
-	// top 7), so the copy itself records which of its elements are unusable.
+	// The fp16 copy of a BF16 V element kept for the prefill kernel (RNE;
+	// exact for every bf16 from 2^-14 up to fp16's range, within 2^-25 below).
+	// The prefill kernel multiplies it by P rounded to fp16, whose error in an
+	// output is up to 2^-11 of the spread of the V values it weighs (measured
+	// with sharply peaked scores: about 1.2e-4 of max |V|). So only values up
+	// to kF16CopyMax in magnitude are kept; a larger (or non-finite) one is
+	// stored as kF16Bad, a NaN pattern that no conversion of a bf16 value
+	// produces (its lowest mantissa bit is set, where bf16's 7 mantissa bits
+	// fill only fp16's top 7), so the copy itself records which of its
+	// elements are unusable, and a buffer holding one runs the exact bf16
+	// path until such rows are overwritten.
 	constexpr uint16_t kF16Bad = 0x7e01;
+	constexpr float kF16CopyMax = 32.0f;
 
 	__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint32_t b)
 	{
 		const float f = bf16_bits_to_f32(b);
-		if (fabsf(f) > 65504.0f && fabsf(f) < INFINITY) return kF16Bad;
+		if (!(fabsf(f) <= kF16CopyMax)) return kF16Bad;
 		return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 	}
 

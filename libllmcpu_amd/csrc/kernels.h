@@ -16,8 +16,6 @@ namespace nnchip
 		float* out; // [n_tok][n_head * head_dim]
 		const void* K; // [rows][kv_dim], BF16 bits or F32
 		const void* V;
-		const void* V16; // BF16 caches: V's fp16 copy, or null
-		const int* n_bad; // elements of the copy past fp16's range (kF16Bad); not 0: use V
 		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		float* part; // [n_tok][n_kv][n_split][group][head_dim + 4]: o, then m (log2 units), then l
 		int rows, kv_dim, n_head, n_kv;
@@ -61,7 +59,7 @@ namespace nnchip
 		const void* K; // [rows][kv_dim]
 		const void* V;
 		const void* V16; // fp16 copy of V, or null
-		const int* n_bad; // elements of the copy past fp16's range (kF16Bad); not 0: use V
+		const int* n_bad; // elements of the copy marked kF16Bad (beyond kF16CopyMax); not 0: use V
 		int rows, kv_dim, n_head, n_kv;
 		int n_tok, pos0, n_seq, window;
 		int causal;
@@ -83,7 +81,7 @@ namespace nnchip
 		void* K; // the layer's buffers: [rows][kv_dim], BF16 bits or F32
 		void* V;
 		void* V16; // V's fp16 copy (BF16 buffers), or null
-		int* n_bad; // the copy's count of elements past fp16's range
+		int* n_bad; // the copy's count of kF16Bad elements
 		const float* q_gamma; // head_dim floats, or null: no Q norm
 		const float* k_gamma; // head_dim floats, or null: no K norm
 		// cos and sin of every rotation angle of the batch, [n_tok][n_rot / 2]
@@ -101,9 +99,9 @@ namespace nnchip
 	// head rows; false for a head_dim or n_rot outside the supported range.
 	bool launch_prep(const prep_params& p, int n_tok, hipStream_t stream);
 
-	// V16, n_bad: the buffer's fp16 copy of V and its count of elements past
-	// fp16's range (kept up to date as elements are replaced), or null (no
-	// copy).
+	// V16, n_bad: the buffer's fp16 copy of V and its count of kF16Bad
+	// elements (values beyond kF16CopyMax; kept up to date as elements are
+	// replaced), or null (no copy).
 	bool launch_append_f32(void* K, void* V, const float* k_rows, const float* v_rows, int rows, int kv_dim, int pos0,
 	                       int n_tok, bool bf16, hipStream_t stream, void* V16, int* n_bad);
 

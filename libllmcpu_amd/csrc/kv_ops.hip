@@ -12,8 +12,8 @@ namespace nnchip
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
 		// With a shadow (V16 not null) the fp16 copy of the same V rows is
-		// written too, and `n_bad` (the copy's count of elements that do not
-		// fit fp16) follows the elements replaced and written.
+		// written too, and `n_bad` (the copy's count of kF16Bad elements,
+		// values beyond kF16CopyMax) follows the elements replaced and written.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
 		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* V16,
 		                                   int* n_bad)

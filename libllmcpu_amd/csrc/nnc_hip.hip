@@ -162,7 +162,7 @@ struct nnc_hip_kv
 	dev_scratch out;
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
-	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now past fp16's range (device)
+	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now marked kF16Bad (device)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 	host_staging pinned; // host rows in and out (q, gate, out; K/V appends; RoPE tables)
@@ -401,8 +401,6 @@ namespace
 		p.gate = gate;
 		p.K = b.k;
 		p.V = b.v;
-		p.V16 = b.v16;
-		p.n_bad = b.v16 ? kv->n_bad + (&b - kv->bufs.data()) : nullptr;
 		p.part = part;
 		p.rows = b.rows;
 		p.kv_dim = b.kv_dim;

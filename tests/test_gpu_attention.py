@@ -156,12 +156,14 @@ def test_prefill_odd_batches(orc):
 
 def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
     """BF16 caches keep an fp16 copy of V for the prefill kernel (P in fp16,
-    one MFMA per P . V product). A V value past fp16's range sends the prefill
-    through the bf16 path (P as bf16 hi + lo against the exact bf16 V); without
-    the copy (NNC_HIP_F16_SHADOW=0) it always runs there. K is read as bf16 with
-    Q as hi + lo on both paths, so large K or Q values need no fallback. Every
-    variant stays within the BF16 bound of the oracle, and within
-    5e-3 * (1 + |ref|) where a V of 1e5 makes outputs large."""
+    one MFMA per P . V product) holding values up to 32 in magnitude. A V
+    value beyond that (40, or 1e5 past fp16's range) sends the prefill through
+    the bf16 path (P as bf16 hi + lo against the exact bf16 V), bit for bit
+    what a cache without the copy (NNC_HIP_F16_SHADOW=0) gives; a value of 30
+    keeps the fp16 path. K is read as bf16 with Q as hi + lo on both paths, so
+    large K or Q values need no fallback. Every variant stays within the BF16
+    bound of the oracle, and within 5e-3 * (1 + |ref|) where a V of 1e5 makes
+    outputs large."""
     cfg = synth.CONFIGS["D"]
     n_seq, n_tok = 1024, 64
     pos0 = n_seq - n_tok
@@ -183,11 +185,20 @@ def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
             assert d.max() <= cfg.tol, label
         return got, want
 
-    base, _ = run(K, V, q, "fp16 shadow")
-    monkeypatch.setenv("NNC_HIP_F16_SHADOW", "0")
-    plain, _ = run(K, V, q, "no shadow (bf16 K/V, Q hi + lo)")
-    monkeypatch.delenv("NNC_HIP_F16_SHADOW")
+    def bits(K, V, label):  # with the copy, then without it
+        with_copy, _ = run(K, V, q, label)
+        monkeypatch.setenv("NNC_HIP_F16_SHADOW", "0")
+        without, _ = run(K, V, q, label + ", no shadow (bf16 K/V, Q hi + lo)")
+        monkeypatch.delenv("NNC_HIP_F16_SHADOW")
+        return with_copy.view(np.uint32), without.view(np.uint32)
+
+    base, plain = bits(K, V, "fp16 shadow")
     assert not np.array_equal(base, plain)  # the two paths round differently
+    for val, copy_used in ((30.0, True), (40.0, False)):  # the copy's limit is 32
+        V3 = V.copy()
+        V3[200, 9] = nh.bf16_round(np.array([val], np.float32))[0]
+        a, b = bits(K, V3, f"cache V value {val:g}")
+        assert np.array_equal(a, b) != copy_used, val
     big = nh.bf16_round(np.array([1.0e5], np.float32))[0]  # past fp16's range
     K2 = K.copy()
     K2[100, 5] = big
@@ -202,7 +213,7 @@ def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
 
 
 def test_fp16_shadow_follows_current_contents(monkeypatch):
-    """V's fp16 copy counts its elements past fp16's range as they are written
+    """V's fp16 copy counts its elements beyond its limit as they are written
     and replaced: once the ring row holding such a value is overwritten (by a
     raw append or an F32 append), prefill is back on the fp16 path and gives
     the bits of a cache that never held it. A cache still holding one gives the

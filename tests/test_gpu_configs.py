@@ -165,6 +165,37 @@ def test_peaked_scores(orc, n_tok):
     assert d.max() <= cfg.tol
 
 
+@pytest.mark.parametrize("n_tok,v_mul", ((1, 100.0), (16, 100.0), (200, 100.0), (200, 5.0)))
+def test_large_values(orc, n_tok, v_mul):
+    """V scaled up and Q by 6 (peaked weights, scores up to ~90 in log2 units).
+    With V x100 (|V| up to about 550) outputs reach a few hundred; there a
+    score's own fp32 rounding moves a weight by ~1e-5 and an output by ~1e-3
+    in any fp32 implementation, the reference's included, so the bound is the
+    relative one, 5e-3 (1 + |ref|) per element, for decode and a session
+    batch (split-K kernels, P as bf16 hi + lo) and for the prefill kernel
+    (values beyond 32 keep it off V's fp16 copy, so it also takes P as bf16
+    hi + lo). With V x5 (|V| below 32) the prefill kernel reads the fp16 copy
+    with P rounded to fp16, whose error grows with |V|: both bounds hold."""
+    cfg = synth.CONFIGS["D"]
+    n_seq = 8192
+    K, V = synth.cache_buffer(cfg, 2, n_seq, n_seq)
+    V = synth.to_cache_dtype(cfg, v_mul * nh.bf16_to_f32(V))
+    pos0 = n_seq - n_tok
+    q = 6.0 * synth.qk_rows(cfg, 2, 0, np.arange(pos0, n_seq), cfg.n_head)
+    kw = dict(n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+    say(f"case V x{v_mul:g} (max |V| {np.abs(nh.bf16_to_f32(V)).max():.1f}), Q x6, D, {n_tok} tokens")
+    with nh.KVCache([n_seq], [cfg.kv_dim]) as kv:
+        kv.append(0, 0, K, V)
+        got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+    want = orc.attend_layer(q, K, V, kv_bf16=True, rows=n_seq, pos0=pos0, n_seq=n_seq, **kw)
+    d = np.abs(got.astype(np.float64) - want)
+    say(f"  max-abs {d.max():.3e}; max of d / (1 + |ref|) {(d / (1 + np.abs(want))).max():.3e}; "
+        f"max |ref| {np.abs(want).max():.1f}")
+    assert np.all(d <= cfg.tol * (1.0 + np.abs(want)))
+    if v_mul < 32.0 / 6.0:
+        assert d.max() <= cfg.tol
+
+
 @pytest.mark.parametrize("n_tok", (1, 16, 100))
 def test_dominant_key_returns_its_value_row(n_tok):
     """Closed form: when every query of a KV head is a large multiple of one
