@@ -84,6 +84,57 @@ namespace nnchip
 		template <int HD>
 		constexpr int part_pitch() { return HD + 4; }
 
+		// The masked maximum of one chunk's scores for a lane's column (keys
+		// cbase + 16 t + 4 (lane / 16) + e in sc[t][e]; each column's keys
+		// span the 16-lane rows): keys outside [s0, s1] become -inf. When the
+		// chunk lies inside the span of every real column of the wavefront
+		// (uniform), the masking changes nothing and is skipped. Columns that
+		// are not real (past the batch) hold an empty span; they are masked
+		// whenever any masking runs and are never read.
+		template <int NT>
+		__device__ __forceinline__ float softmax_mask_max(f32x4 (&sc)[NT], int cbase, int s0, int s1, bool real, int ch)
+		{
+			const int grp = (threadIdx.x & 63) >> 4;
+			const bool inside = __builtin_amdgcn_ballot_w64(real && !(cbase >= s0 && cbase + ch - 1 <= s1)) == 0 &&
+			                    __builtin_amdgcn_ballot_w64(real) != 0;
+			float m = -INFINITY;
+			if (inside)
+			{
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int e = 0; e < 4; ++e) m = fmaxf(m, sc[t][e]);
+			}
+			else
+			{
+#pragma unroll
+				for (int t = 0; t < NT; ++t)
+#pragma unroll
+					for (int e = 0; e < 4; ++e)
+					{
+						const int k = cbase + 16 * t + 4 * grp + e;
+						const float v = (k >= s0 && k <= s1) ? sc[t][e] : -INFINITY;
+						sc[t][e] = v;
+						m = fmaxf(m, v);
+					}
+			}
+			m = fmaxf(m, __shfl_xor(m, 16));
+			return fmaxf(m, __shfl_xor(m, 32));
+		}
+
+		// The running offset of a column's online softmax (log2 units): raised
+		// to the chunk's maximum only when that exceeds it by more than
+		// kLazyOffset, so most chunks keep it and need no rescale (weights then
+		// reach up to 2^kLazyOffset, which the fp32 sums and the bf16 hi + lo
+		// split of P carry at full relative precision). Every BF16 decode
+		// kernel applies it per column, so a token's bits do not depend on the
+		// kernel.
+		constexpr float kLazyOffset = 8.0f;
+		__device__ __forceinline__ float lazy_offset(float m_run, float m_chunk)
+		{
+			return m_chunk > m_run + kLazyOffset ? m_chunk : m_run;
+		}
+
 		// The P operand of one 32-key half of a chunk (the 8 weights a lane
 		// supplies) and its part of the row sum, for O^T += V^T . P^T: P split
 		// into bf16 hi + lo against the exact bf16 V (near-fp32), the sum of
@@ -706,8 +757,9 @@ namespace nnchip
 			// token, last of the last] (both ends move forward with the position).
 			int first, last;
 			attn_span(p.causal, p.window, p.pos0 + tok0 + tt, p.n_seq, first, last);
-			const int col_s0 = tt < n_tt ? max(first, sbase) : 1;
-			const int col_s1 = tt < n_tt ? min(last, send) : 0;
+			const bool col_real = tt < n_tt;
+			const int col_s0 = col_real ? max(first, sbase) : 1;
+			const int col_s1 = col_real ? min(last, send) : 0;
 			int f0, l0, fL, lL;
 			attn_span(p.causal, p.window, p.pos0 + tok0, p.n_seq, f0, l0);
 			attn_span(p.causal, p.window, p.pos0 + tok0 + n_tt - 1, p.n_seq, fL, lL);
@@ -845,23 +897,12 @@ namespace nnchip
 					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = X.v[j];
 				if (reload) load_v(X, i + DEPTH);
 
-				// Online softmax per head (column).
-				float m_loc = -INFINITY;
-#pragma unroll
-				for (int t = 0; t < NT; ++t)
-#pragma unroll
-					for (int e = 0; e < 4; ++e)
-					{
-						const int k = cbase + 16 * t + 4 * grp + e;
-						const float v = (k >= col_s0 && k <= col_s1) ? sc[t][e] : -INFINITY;
-						sc[t][e] = v;
-						m_loc = fmaxf(m_loc, v);
-					}
-				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
-				m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
-				const float m_new = fmaxf(m_run, m_loc);
+				// Online softmax per head (column), with a lazy offset.
+				float m_loc = softmax_mask_max<NT>(sc, cbase, col_s0, col_s1, col_real, CH);
+				const float m_new = lazy_offset(m_run, m_loc);
 				const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-				const float alpha = fast_exp2(m_run - m_use);
+				const float alpha = m_new == m_run ? 1.0f : fast_exp2(m_run - m_use);
+				const bool rescale = __builtin_amdgcn_ballot_w64(col_real && m_new != m_run) != 0; // uniform
 				m_run = m_new;
 				float lsum = 0.0f;
 				u32x4 pb[NC][2];
@@ -878,8 +919,9 @@ namespace nnchip
 					p_operand(w, pb[c], lsum);
 				}
 				l_run = l_run * alpha + lsum;
+				if (rescale)
 #pragma unroll
-				for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
+					for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
 
 				wave_sync();
 #pragma unroll
@@ -1083,8 +1125,19 @@ namespace nnchip
 #pragma unroll
 				for (int j = 0; j < NV; ++j)
 					*reinterpret_cast<u32x4*>(vt + (j * KPL + lane / LPK) * VPITCH + 8 * (lane % LPK)) = vreg[j];
-
 				wave_sync();
+				// V^T read back once for all tiles (the A operands of P.V).
+				u32x4 vta[NC][DB];
+#pragma unroll
+				for (int c = 0; c < NC; ++c)
+#pragma unroll
+					for (int db = 0; db < DB; ++db)
+					{
+						const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
+						const u32x2 lo = vt_read(r0);
+						const u32x2 hi = vt_read(r0 + 16 * VPITCH);
+						vta[c][db] = u32x4{lo.x, lo.y, hi.x, hi.y};
+					}
 
 				// One tile at a time: its scores (the hi and lo products in their
 				// own chains, added once: the operations of scores_hilo), then its
@@ -1118,22 +1171,12 @@ namespace nnchip
 						load_v(cw + LPH);
 					}
 
-					float m_loc = -INFINITY;
-#pragma unroll
-					for (int t = 0; t < NT; ++t)
-#pragma unroll
-						for (int i = 0; i < 4; ++i)
-						{
-							const int k = cbase + 16 * t + 4 * grp + i;
-							const float v = (k >= col_s0[tl] && k <= col_s1[tl]) ? sc[t][i] : -INFINITY;
-							sc[t][i] = v;
-							m_loc = fmaxf(m_loc, v);
-						}
-					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 16));
-					m_loc = fmaxf(m_loc, __shfl_xor(m_loc, 32));
-					const float m_new = fmaxf(m_run[tl], m_loc);
+					const bool real = (16 * tl + col) / G < n_tt;
+					const float m_loc = softmax_mask_max<NT>(sc, cbase, col_s0[tl], col_s1[tl], real, CH);
+					const float m_new = lazy_offset(m_run[tl], m_loc);
 					const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-					const float alpha = fast_exp2(m_run[tl] - m_use);
+					const float alpha = m_new == m_run[tl] ? 1.0f : fast_exp2(m_run[tl] - m_use);
+					const bool rescale = __builtin_amdgcn_ballot_w64(real && m_new != m_run[tl]) != 0; // uniform
 					m_run[tl] = m_new;
 					float lsum = 0.0f;
 					u32x4 pb[NC][2];
@@ -1150,18 +1193,13 @@ namespace nnchip
 						p_operand(w, pb[c], lsum);
 					}
 					l_run[tl] = l_run[tl] * alpha + lsum;
+					if (rescale)
 #pragma unroll
-					for (int db = 0; db < DB; ++db) acc_o[tl][db] *= alpha;
+						for (int db = 0; db < DB; ++db) acc_o[tl][db] *= alpha;
 #pragma unroll
 					for (int c = 0; c < NC; ++c)
 #pragma unroll
-						for (int db = 0; db < DB; ++db)
-						{
-							const uint16_t* r0 = vt + (32 * c + 4 * grp + (col >> 2)) * VPITCH + 16 * db + 4 * (col & 3);
-							const u32x2 lo = vt_read(r0);
-							const u32x2 hi = vt_read(r0 + 16 * VPITCH);
-							pv_mfma(acc_o[tl][db], u32x4{lo.x, lo.y, hi.x, hi.y}, pb[c]);
-						}
+						for (int db = 0; db < DB; ++db) pv_mfma(acc_o[tl][db], vta[c][db], pb[c]);
 				}
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
