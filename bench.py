@@ -214,6 +214,7 @@ CALIBRATE_MIB = 1024
 
 # Qwen3-4B's weight gemvs of one layer (rows, cols): q, k, v, o, gate, up, down.
 GEMV_LAYER = [(4096, 2560), (1024, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (9728, 2560), (2560, 9728)]
+GEMV_GROUPS = [(0, 1, 2), (3,), (4, 5), (6,)]  # launches per layer: q/k/v and gate/up share their input
 LM_HEAD = (151936, 2560)  # Qwen3-4B vocabulary x n_embd
 GEMV_WORKING_SET = 640 << 20  # bytes of distinct weights per format, past the 256 MB Infinity Cache
 
@@ -231,7 +232,7 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
     Cache. Algorithmic bytes: the weights (with scales and biases) plus X and Y."""
     res = {}
     x = hip_rt.malloc(16 * 9728 * 4)
-    y = hip_rt.malloc(16 * 9728 * 4)
+    y = hip_rt.malloc(16 * 2 * 9728 * 4)  # room for a group's outputs side by side
     nh.fill_normal(x, 16 * 9728, 99, 0, False, stream)
     # Every buffer is freed only after the last timing: the driver clears freed
     # device memory in the background, which takes HBM bandwidth for seconds.
@@ -255,8 +256,18 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
         kv.sync()
         for n in (1, 16):
             def step():
-                for w, r, c in mats:
-                    kv.gemv_device(fmt, w, x, y, rows=r, cols=c, n_batch=n)
+                # Per layer: q, k and v over the same input in one launch, then
+                # o, gate and up (one launch), down.
+                for li in range(0, len(mats), len(GEMV_LAYER)):
+                    lm = mats[li:li + len(GEMV_LAYER)]
+                    for grp in GEMV_GROUPS:
+                        if len(grp) == 1:
+                            w, r, c = lm[grp[0]]
+                            kv.gemv_device(fmt, w, x, y, rows=r, cols=c, n_batch=n)
+                        else:
+                            ys = [y + 4 * 16 * sum(lm[j][1] for j in grp[:k]) for k in range(len(grp))]
+                            kv.gemv_group_device(fmt, [(lm[j][0], ys[k], lm[j][1]) for k, j in enumerate(grp)], x,
+                                                 cols=lm[grp[0]][2], n_batch=n)
 
             step()
             hip_rt.sync()
@@ -287,7 +298,7 @@ def gemv_bench(nh, hip_rt, kv, stream, timed) -> dict:
         hip_rt.free(d)
     return {"what": "Qwen3-4B layer weight gemvs (q, k, v, o, gate, up, down) per weight layout; n1 = one "
                     "vector (decode), n16 = a 16-token session batch; weights in HBM, rotated past the "
-                    "Infinity Cache; seven launches per layer", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "Infinity Cache; four launches per layer (q/k/v and gate/up as nnc_hip_gemv_group calls)", "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "kernels": "gemv_vec_kernel (one vector), gemv_kernel + gemv_reduce_kernel (batches)", **res}
 
 

@@ -270,6 +270,39 @@ nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* 
                              const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
                              size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch);
 
+/* Several of the gemvs above over the same X in one launch: the QKV
+ * projections (reference model.cpp:1596-1602, three gemv_batch calls on the
+ * same normed input) or the FFN gate and up projections (:1816-1817). No
+ * counterpart in nnc, which runs them one by one; every mats[m].y receives
+ * exactly what the single-matrix call for that matrix writes (the same
+ * kernels, the same sums per row). format is NNC_HIP_GEMV_BF16, _Q8_0 or
+ * _Q4_S, n_mat 1 .. NNC_HIP_GEMV_MAX_GROUP, every matrix of cols columns in
+ * that layout (scales for Q8_0 and Q4_S, biases for Q4_S, NULL otherwise);
+ * XSUM as for nnc_hip_gemv_q4_s (ignored for other formats). One launch per
+ * 16 vectors for the whole group when every matrix but the last has a
+ * multiple of 16 rows (nnc's projections do), else one per matrix. Errors as
+ * for the single-matrix calls, and NNC_ERR_INVALID_ARGUMENT for an unknown
+ * format or n_mat out of range. */
+enum
+{
+	NNC_HIP_GEMV_BF16 = 0,
+	NNC_HIP_GEMV_Q8_0 = 1,
+	NNC_HIP_GEMV_Q4_S = 2,
+	NNC_HIP_GEMV_MAX_GROUP = 3
+};
+typedef struct nnc_hip_gemv_mat
+{
+	const void* w; /* BF16 W, Q8_0 qs or Q4_S nibbles [rows][...] */
+	const uint16_t* scales; /* [rows][cols / 32] BF16 (Q8_0, Q4_S) */
+	const uint16_t* biases; /* [rows][cols / 32] BF16 (Q4_S) */
+	float* y; /* n_batch vectors of rows floats, y_stride apart */
+	size_t y_stride;
+	uint32_t rows;
+} nnc_hip_gemv_mat;
+nnc_status nnc_hip_gemv_group(nnc_hip_kv* kv, int32_t format, int32_t n_mat, const nnc_hip_gemv_mat* mats,
+                              const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, uint32_t cols,
+                              uint32_t n_batch);
+
 /* Greedy decode's lm_head projection: the row of the largest element of
  * y = W x for a BF16 W [rows][cols] and one vector x, without writing y
  * (reference nn_ops.h:98-113, nn_ops.cpp:1055-1197 nnc_gemv_bf16w_argmax_f32x;

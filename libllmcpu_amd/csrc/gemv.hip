@@ -31,6 +31,20 @@ namespace nnchip
 		constexpr int kAhead = 8; // blocks of weights in flight per wavefront (batch kernel)
 		constexpr int kVecAhead = 8; // 16-byte loads in flight per lane (one-vector kernel)
 
+		// The matrix holding stacked row `row` and the row's index in it (row
+		// uniform over the caller's rows: a row pair or a 16-row tile).
+		struct mat_row
+		{
+			gemv_mat m;
+			int r;
+		};
+		__device__ __forceinline__ mat_row locate(const gemv_params& p, int row)
+		{
+			const int k = (row >= p.mrow[1]) + (row >= p.mrow[2]);
+			const gemv_mat& m = k == 0 ? p.mats[0] : (k == 1 ? p.mats[1] : p.mats[2]);
+			return {m, row - (k == 0 ? 0 : (k == 1 ? p.mrow[1] : p.mrow[2]))};
+		}
+
 		// MFMA k-slots of a 32-column block: a lane of k-group g holds slots
 		// 8 g .. 8 g + 7. For BF16 and Q8_0 slot s is column s. Q4_S packs
 		// elements i and i + 16 into byte i, so a lane reading bytes 4 g .. 4 g + 3
@@ -78,20 +92,21 @@ namespace nnchip
 			u32x4 v; // BF16: 8 weights; Q8_0: 8 int8 in v[0..1]; Q4_S: 4 bytes in v[0]
 		};
 
+		// Row `row` of W (cols columns), block blk, the lane's k-group grp.
 		template <int F>
-		__device__ __forceinline__ a_block<F> load_a(const gemv_params& p, int row, int blk, int grp)
+		__device__ __forceinline__ a_block<F> load_a(const void* W, int cols, int row, int blk, int grp)
 		{
 			a_block<F> a;
-			const size_t base = static_cast<size_t>(row) * p.cols + 32 * blk;
+			const size_t base = static_cast<size_t>(row) * cols + 32 * blk;
 			if constexpr (F == kGemvBf16)
-				a.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.w) + base + 8 * grp);
+				a.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(W) + base + 8 * grp);
 			else if constexpr (F == kGemvQ8_0)
 			{
-				const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(p.w) + base + 8 * grp);
+				const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(W) + base + 8 * grp);
 				a.v = u32x4{w.x, w.y, 0u, 0u};
 			}
 			else
-				a.v = u32x4{*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.w) + base / 2 + 4 * grp), 0u,
+				a.v = u32x4{*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(W) + base / 2 + 4 * grp), 0u,
 				            0u, 0u};
 			return a;
 		}
@@ -130,12 +145,15 @@ namespace nnchip
 			// the range, kAhead of them in flight, the first ones while X^T is
 			// staged.
 			const int row0 = blockIdx.x * 16;
-			const int ra = min(row0 + col, p.rows - 1); // this lane's A row (clamped; not stored)
+			// The tile's matrix (one for all 16 rows) and its rows in it.
+			const mat_row mr = locate(p, row0);
+			const int m_rows = min(16, p.rows - row0); // rows of the tile (only the last matrix's last tile is short)
+			const int ra = mr.r + min(col, m_rows - 1); // this lane's A row in the matrix (clamped; not stored)
 			const int n_mine = nblk > wave ? (nblk - wave + 3) / 4 : 0; // blocks of this wavefront
 			auto my_block = [&](int i) { return b0 + wave + 4 * min(i, max(n_mine - 1, 0)); };
 			a_block<F> ab[kAhead];
 #pragma unroll
-			for (int j = 0; j < kAhead; ++j) ab[j] = load_a<F>(p, ra, min(my_block(j), p.cols / 32 - 1), grp);
+			for (int j = 0; j < kAhead; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
 
 			// X^T of the range, four columns per piece (consecutive threads read
 			// consecutive 16 bytes of a token's row), loads issued eight at a time.
@@ -208,9 +226,9 @@ namespace nnchip
 				for (int i = threadIdx.x; i < nblk * 16; i += 256)
 				{
 					const int r = i / nblk, b = i % nblk;
-					const size_t src = static_cast<size_t>(min(row0 + r, p.rows - 1)) * nb_all + b0 + b;
-					s_sc[b * 16 + r] = p.scales[src];
-					if constexpr (F == kGemvQ4S) s_bi[b * 16 + r] = p.biases[src];
+					const size_t src = static_cast<size_t>(mr.r + min(r, m_rows - 1)) * nb_all + b0 + b;
+					s_sc[b * 16 + r] = mr.m.scales[src];
+					if constexpr (F == kGemvQ4S) s_bi[b * 16 + r] = mr.m.biases[src];
 				}
 			}
 			__syncthreads();
@@ -227,7 +245,7 @@ namespace nnchip
 					const bf16x8 a = a_operand<F>(ab[j]);
 					// The next load into this slot, kAhead blocks on (clamped: a
 					// load is never under a branch).
-					ab[j] = load_a<F>(p, ra, min(my_block(i + kAhead), nb_all - 1), grp);
+					ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(i + kAhead), nb_all - 1), grp);
 					if (i < n_mine) // uniform
 					{
 						const size_t at = (static_cast<size_t>(bl) * nt + col) * 32 + 8 * grp;
@@ -274,10 +292,10 @@ namespace nnchip
 				float v = s_red[r * 16 + t];
 #pragma unroll
 				for (int w = 1; w < 4; ++w) v += s_red[(w * 16 + r) * 16 + t];
-				if (row0 + r < p.rows && t < nt)
+				if (r < m_rows && t < nt)
 				{
 					if (p.n_split == 1)
-						p.y[t * p.y_stride + row0 + r] = v;
+						mr.m.y[t * mr.m.y_stride + mr.r + r] = v;
 					else
 						p.part[(static_cast<size_t>(split) * nt + t) * p.rows + row0 + r] = v;
 				}
@@ -320,11 +338,15 @@ namespace nnchip
 			using V = vec_shape<F>;
 			constexpr int CPL = V::CPL, CW = V::CW, NA = kVecAhead;
 			extern __shared__ __attribute__((aligned(16))) float s_x[]; // x, then (Q4_S) its block sums
-			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+			// (wave uniform: every row index below, and the matrix lookup, stays scalar)
+			const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 			const int nb_all = p.cols / 32;
 
 			// Items: for each of this wavefront's row pairs, chunk c of row 0,
-			// then of row 1, for every chunk c of CW columns.
+			// then of row 1, for every chunk c of CW columns. Two cursors walk
+			// them, the loads' (kVecAhead ahead) and the sums': (pair, item within
+			// the pair), stepped by one item at a time (no division per item);
+			// a pair's matrix is looked up when the load cursor enters it.
 			const int nch = (p.cols + CW - 1) / CW;
 			const int per_pair = 2 * nch;
 			const int gw = blockIdx.x * 4 + wave, n_gw = gridDim.x * 4;
@@ -332,33 +354,46 @@ namespace nnchip
 			const int my_pairs = gw < n_pairs ? (n_pairs - 1 - gw) / n_gw + 1 : 0;
 			const int n_items = my_pairs * per_pair;
 			// (A wavefront without rows still takes part in staging x.)
-			// Row of item k (clamped to the matrix) and the lane's first column.
-			auto item_pos = [&](int k, int& row, int& c0) __attribute__((always_inline))
+			int l_pi = 0, l_rem = 0; // the next load's pair and item
+			gemv_mat l_m = p.mats[0];
+			int l_r0 = 0, l_two = 0; // the pair's first row in its matrix; whether it has a second row
+			auto enter_pair = [&]() __attribute__((always_inline))
 			{
-				k = max(0, min(k, n_items - 1));
-				const int pi = k / per_pair, rem = k % per_pair;
-				row = min(2 * (gw + pi * n_gw) + (rem & 1), p.rows - 1);
-				c0 = (rem >> 1) * CW + lane * CPL;
+				const int row0 = 2 * (gw + min(l_pi, max(my_pairs - 1, 0)) * n_gw);
+				const mat_row mr = locate(p, min(row0, p.rows - 1));
+				l_m = mr.m;
+				l_r0 = mr.r;
+				l_two = row0 + 1 < p.rows;
 			};
-			auto pair_row = [&](int k) { return 2 * (gw + (k / per_pair) * n_gw); };
-			auto load = [&](int k) __attribute__((always_inline)) -> vec_item<F>
+			enter_pair();
+			// The next item's load (past the wavefront's last item: its last item
+			// again, so no load is under a branch), then the cursor steps on.
+			auto load = [&]() __attribute__((always_inline)) -> vec_item<F>
 			{
-				int row, c0;
-				item_pos(k, row, c0);
+				const bool past = l_pi >= my_pairs;
+				const int rem = past ? per_pair - 1 : l_rem;
+				const int r = l_r0 + ((rem & 1) & l_two);
+				const int c0 = (rem >> 1) * CW + lane * CPL;
 				const int cc = min(c0, p.cols - CPL); // lanes past the row's end re-read its last bytes (not used)
 				vec_item<F> it;
-				const size_t off = static_cast<size_t>(row) * p.cols + cc;
+				const size_t off = static_cast<size_t>(r) * p.cols + cc;
 				if constexpr (F == kGemvBf16)
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.w) + off);
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(l_m.w) + off);
 				else if constexpr (F == kGemvQ8_0)
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(p.w) + off);
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(l_m.w) + off);
 				else
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.w) + off / 2);
+					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(l_m.w) + off / 2);
 				if constexpr (F != kGemvBf16)
 				{
-					const size_t si = static_cast<size_t>(row) * nb_all + cc / 32;
-					it.sc = bf16_bits_to_f32(p.scales[si]);
-					if constexpr (F == kGemvQ4S) it.bi = bf16_bits_to_f32(p.biases[si]);
+					const size_t si = static_cast<size_t>(r) * nb_all + cc / 32;
+					it.sc = bf16_bits_to_f32(l_m.scales[si]);
+					if constexpr (F == kGemvQ4S) it.bi = bf16_bits_to_f32(l_m.biases[si]);
+				}
+				if (!past && ++l_rem == per_pair)
+				{
+					l_rem = 0;
+					++l_pi;
+					if (l_pi < my_pairs) enter_pair();
 				}
 				return it;
 			};
@@ -422,7 +457,7 @@ namespace nnchip
 			// The first loads go out before x is staged.
 			vec_item<F> ring[NA];
 #pragma unroll
-			for (int j = 0; j < NA; ++j) ring[j] = load(j);
+			for (int j = 0; j < NA; ++j) ring[j] = load();
 
 			// x into LDS, thread t taking elements 4 t .. 4 t + 3 of each 1024.
 			// Q4_S without the caller's block sums: the eight threads of a block
@@ -458,24 +493,22 @@ namespace nnchip
 			float acc[2] = {0.0f, 0.0f};
 			float best_v = -INFINITY; // ARGMAX: this wavefront's best row so far (lane 0)
 			int best_r = -1;
+			int u_pi = 0, u_rem = 0; // the next sum's pair and item
 			for (int k0 = 0; k0 < n_items; k0 += NA)
 			{
 #pragma unroll
 				for (int j = 0; j < NA; ++j)
 				{
 					const int k = k0 + j;
-					int row, c0;
-					item_pos(k, row, c0);
-					(void)row;
 					const vec_item<F> it = ring[j];
-					ring[j] = load(k + NA); // clamped past the end: never under a branch
+					ring[j] = load(); // past the end: a repeat, never under a branch
 					if (k < n_items) // uniform
 					{
-						acc[j & 1] += dot(it, c0);
-						if (k % per_pair == per_pair - 1) // the pair's last item: both rows are complete
+						acc[j & 1] += dot(it, (u_rem >> 1) * CW + lane * CPL);
+						if (u_rem == per_pair - 1) // the pair's last item: both rows are complete
 						{
 							const float y0 = wave_sum_dpp(acc[0]), y1 = wave_sum_dpp(acc[1]);
-							const int r0 = pair_row(k);
+							const int r0 = 2 * (gw + u_pi * n_gw);
 							if constexpr (ARGMAX)
 							{
 								if (r0 == 0 && lane == 0) p.argmax[1] = __builtin_isnan(y0);
@@ -492,10 +525,16 @@ namespace nnchip
 							}
 							else if (lane == 0)
 							{
-								p.y[r0] = y0;
-								if (r0 + 1 < p.rows) p.y[r0 + 1] = y1;
+								const mat_row mr = locate(p, r0); // the pair's matrix (pairs never span two)
+								mr.m.y[mr.r] = y0;
+								if (r0 + 1 < p.rows) mr.m.y[mr.r + 1] = y1;
 							}
 							acc[0] = acc[1] = 0.0f;
+						}
+						if (++u_rem == per_pair)
+						{
+							u_rem = 0;
+							++u_pi;
 						}
 					}
 				}
@@ -573,7 +612,7 @@ namespace nnchip
 			int br = -1;
 			for (int i = blockIdx.x * 256 + threadIdx.x; i < p.rows; i += gridDim.x * 256)
 			{
-				const float v = p.y[i];
+				const float v = p.mats[0].y[i];
 				if (i == 0) p.argmax[1] = __builtin_isnan(v);
 				if (argmax_better(v, i, bv, br))
 				{
@@ -616,8 +655,9 @@ namespace nnchip
 					for (int u = 0; u < 8; ++u)
 						if (k0 + u < p.n_split) s = k0 + u == 0 ? v[u] : s + v[u];
 				}
-				const int t = static_cast<int>(i / p.rows), r = static_cast<int>(i % p.rows);
-				p.y[t * p.y_stride + r] = s;
+				const int t = static_cast<int>(i / p.rows);
+				const mat_row mr = locate(p, static_cast<int>(i % p.rows));
+				mr.m.y[t * mr.m.y_stride + mr.r] = s;
 			}
 		}
 	}

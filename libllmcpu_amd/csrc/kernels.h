@@ -125,18 +125,34 @@ namespace nnchip
 		return static_cast<size_t>(blocks) * (128 * n_batch + 64 + 4 * n_batch) + 4 * 256 * 4;
 	}
 
-	struct gemv_params
+	// One weight matrix of a gemv: its rows' weights, scales and biases, and
+	// where its outputs go.
+	struct gemv_mat
 	{
-		int format; // kGemvBf16, kGemvQ8_0 or kGemvQ4S
 		const void* w; // BF16 [rows][cols], Q8_0 int8 [rows][cols], Q4_S nibbles [rows][cols / 2]
 		const uint16_t* scales; // [rows][cols / 32] BF16 (Q8_0, Q4_S)
 		const uint16_t* biases; // [rows][cols / 32] BF16 (Q4_S)
+		float* y; // [n_batch] vectors of rows floats, y_stride apart
+		size_t y_stride;
+	};
+
+	// Matrices sharing X in one launch, stacked along the rows.
+	constexpr int kGemvMaxMats = 3;
+
+	struct gemv_params
+	{
+		int format; // kGemvBf16, kGemvQ8_0 or kGemvQ4S
+		// Matrix m holds stacked rows mrow[m] .. mrow[m + 1] - 1 (mrow[0] = 0,
+		// mrow[n_mat] = rows, later entries INT_MAX). Every matrix but the last
+		// has a multiple of 16 rows, so no row pair of the one-vector kernel
+		// and no 16-row tile of the batch kernel spans two matrices.
+		gemv_mat mats[kGemvMaxMats];
+		int mrow[kGemvMaxMats + 1];
 		const float* x; // [n_batch] vectors of cols floats, x_stride apart
 		const float* xsum; // Q4_S: [n_batch] runs of cols / 32 block sums, xsum_stride apart; or null
-		float* y; // [n_batch] vectors of rows floats, y_stride apart
-		float* part; // [n_split][n_batch][rows] partial sums when n_split > 1
-		size_t x_stride, xsum_stride, y_stride;
-		int rows, cols, n_batch;
+		float* part; // [n_split][n_batch][rows] partial sums when n_split > 1 (stacked rows)
+		size_t x_stride, xsum_stride;
+		int rows, cols, n_batch; // rows: all matrices' rows
 		int n_split, split_blocks; // K splits, and 32-column blocks per split
 		// argmax of y instead of y (BF16, one vector): each work-group's best
 		// (value, row) pair, then the row

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -760,7 +761,7 @@ namespace
 	// The host-buffer form of the op: q (and gate) staged to the device
 	// through pinned memory, out downloaded through it, the call synchronous
 	// with respect to out.
-	nnc_status attend_host(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out, int32_t n_tok,
+	static nnc_status attend_host(nnc_hip_kv* kv, int32_t buf, const float* q, const float* gate, float* out, int32_t n_tok,
 	                       int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
 	                       int32_t head_dim, float scale)
 	{
@@ -818,7 +819,7 @@ namespace
 {
 	// The device address of `scratch` on the cache's device: looked up once
 	// per device, on its first no-alloc call, with that device current.
-	nnc_status noalloc_scratch(const nnc_hip_kv* kv, void** out)
+	static nnc_status noalloc_scratch(const nnc_hip_kv* kv, void** out)
 	{
 		if (kv->device < 0 || kv->device >= kMaxDevices)
 			return fail(NNC_ERR_UNSUPPORTED_CPU, "device %d is past the library's %d-device table", kv->device, kMaxDevices);
@@ -874,47 +875,89 @@ nnc_status nnc_hip_attend_gated_device(nnc_hip_kv* kv, int32_t buf, const float*
 
 namespace
 {
-	// One weight gemv on the context's stream, in chunks of at most
-	// kGemvMaxBatch vectors.
-	nnc_status gemv_impl(nnc_hip_kv* kv, int format, const void* w, const uint16_t* scales, const uint16_t* biases,
-	                     const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
-	                     size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
+	// p.mrow and p.rows for n matrices of the given row counts, stacked.
+	static void stack_rows(nnchip::gemv_params& p, const uint32_t* rows, int n)
+	{
+		int acc = 0;
+		p.mrow[0] = 0;
+		for (int m = 0; m < n; ++m)
+		{
+			acc += static_cast<int>(rows[m]);
+			p.mrow[m + 1] = acc;
+		}
+		for (int m = n + 1; m <= nnchip::kGemvMaxMats; ++m) p.mrow[m] = INT_MAX;
+		p.rows = acc;
+	}
+
+	// Weight gemvs over the same X on the context's stream: one launch per
+	// chunk of at most kGemvMaxBatch vectors for all the matrices together
+	// (stacked along the rows), or one per matrix when a matrix other than
+	// the last has a row count that is not a multiple of 16.
+	static nnc_status gemv_impl(nnc_hip_kv* kv, int format, int n_mat, const nnc_hip_gemv_mat* mats, const float* X,
+	                     size_t x_stride, const float* XSUM, size_t xsum_stride, uint32_t cols, uint32_t n_batch)
 	{
 		if (!kv) return fail(NNC_ERR_INVALID_ARGUMENT, "the context (cache) is NULL");
-		if (!w || !X || !Y || (format != nnchip::kGemvBf16 && !scales) || (format == nnchip::kGemvQ4S && !biases))
-			return fail(NNC_ERR_INVALID_ARGUMENT, "NULL weight, scale, bias, input or output pointer");
-		if (rows == 0 || cols == 0 || n_batch == 0) return NNC_OK; // nothing to do, as in the reference
-		if (rows > 0x7fffffffu || cols > 0x7fffffffu)
-			return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %u x %u", rows, cols);
+		if (format != nnchip::kGemvBf16 && format != nnchip::kGemvQ8_0 && format != nnchip::kGemvQ4S)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "gemv format %d", format);
+		if (!mats || n_mat < 1 || n_mat > nnchip::kGemvMaxMats)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "%d matrices in a gemv group (1 to %d)", n_mat, nnchip::kGemvMaxMats);
+		if (!X) return fail(NNC_ERR_INVALID_ARGUMENT, "NULL input pointer");
+		uint64_t total = 0;
+		bool stackable = true;
+		for (int m = 0; m < n_mat; ++m)
+		{
+			const nnc_hip_gemv_mat& M = mats[m];
+			if (!M.w || !M.y || (format != nnchip::kGemvBf16 && !M.scales) || (format == nnchip::kGemvQ4S && !M.biases))
+				return fail(NNC_ERR_INVALID_ARGUMENT, "NULL weight, scale, bias or output pointer (matrix %d)", m);
+			if (M.rows > 0x7fffffffu) return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %u rows", M.rows);
+			if (M.y_stride < M.rows)
+				return fail(NNC_ERR_INVALID_ARGUMENT, "y_stride %zu below %u rows (matrix %d)", M.y_stride, M.rows, m);
+			if (reinterpret_cast<uintptr_t>(M.w) & 15)
+				return fail(NNC_ERR_INVALID_ARGUMENT, "weights must be 16-byte aligned (matrix %d)", m);
+			total += M.rows;
+			if (m + 1 < n_mat && M.rows % 16 != 0) stackable = false;
+		}
+		if (total == 0 || cols == 0 || n_batch == 0) return NNC_OK; // nothing to do, as in the reference
+		if (total > 0x7fffffffu || cols > 0x7fffffffu)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %llu x %u", static_cast<unsigned long long>(total), cols);
 		if (cols % 32 != 0)
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "gemv with %u columns (a multiple of 32 is required)", cols);
-		if (x_stride < cols || y_stride < rows || (format == nnchip::kGemvQ4S && XSUM && xsum_stride < cols / 32))
-			return fail(NNC_ERR_INVALID_ARGUMENT, "strides %zu / %zu / %zu for a %u x %u gemv", x_stride, y_stride,
-			            xsum_stride, rows, cols);
-		if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(X)) & 15 || x_stride % 4 != 0)
-			return fail(NNC_ERR_INVALID_ARGUMENT, "weights and X must be 16-byte aligned, x_stride a multiple of 4");
+		if (x_stride < cols || (format == nnchip::kGemvQ4S && XSUM && xsum_stride < cols / 32))
+			return fail(NNC_ERR_INVALID_ARGUMENT, "strides %zu / %zu for %u columns", x_stride, xsum_stride, cols);
+		if ((reinterpret_cast<uintptr_t>(X) & 15) || x_stride % 4 != 0)
+			return fail(NNC_ERR_INVALID_ARGUMENT, "X must be 16-byte aligned, x_stride a multiple of 4");
+		if (!stackable)
+		{
+			for (int m = 0; m < n_mat; ++m)
+				if (nnc_status s = gemv_impl(kv, format, 1, mats + m, X, x_stride, XSUM, xsum_stride, cols, n_batch))
+					return s;
+			return NNC_OK;
+		}
+		uint32_t rows[nnchip::kGemvMaxMats];
+		for (int m = 0; m < n_mat; ++m) rows[m] = mats[m].rows;
 		for (uint32_t t0 = 0; t0 < n_batch; t0 += nnchip::kGemvMaxBatch)
 		{
 			const int nb = static_cast<int>(std::min<uint32_t>(n_batch - t0, nnchip::kGemvMaxBatch));
-			int n_split = 1, split_blocks = 1;
-			nnchip::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), nb, n_split, split_blocks);
-			if (n_split > 1)
-				if (nnc_status s = reserve(kv, kv->gemv_part, static_cast<size_t>(n_split) * nb * rows * sizeof(float),
-				                           "gemv scratch"))
-					return s;
 			nnchip::gemv_params p{};
 			p.format = format;
-			p.w = w;
-			p.scales = scales;
-			p.biases = biases;
+			stack_rows(p, rows, n_mat);
+			int n_split = 1, split_blocks = 1;
+			nnchip::gemv_plan(p.rows, static_cast<int>(cols), nb, n_split, split_blocks);
+			if (n_split > 1)
+				if (nnc_status s = reserve(kv, kv->gemv_part,
+				                           static_cast<size_t>(n_split) * nb * static_cast<size_t>(p.rows) * sizeof(float),
+				                           "gemv scratch"))
+					return s;
+			for (int m = 0; m < n_mat; ++m)
+			{
+				const nnc_hip_gemv_mat& M = mats[m];
+				p.mats[m] = nnchip::gemv_mat{M.w, M.scales, M.biases, M.y + t0 * M.y_stride, M.y_stride};
+			}
 			p.x = X + t0 * x_stride;
 			p.xsum = XSUM ? XSUM + t0 * xsum_stride : nullptr;
-			p.y = Y + t0 * y_stride;
 			p.part = static_cast<float*>(kv->gemv_part.ptr);
 			p.x_stride = x_stride;
 			p.xsum_stride = xsum_stride;
-			p.y_stride = y_stride;
-			p.rows = static_cast<int>(rows);
 			p.cols = static_cast<int>(cols);
 			p.n_batch = nb;
 			p.n_split = n_split;
@@ -947,10 +990,10 @@ nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* 
 	nnchip::gemv_params p{};
 	p.format = nnchip::kGemvBf16;
 	p.first_sticks = rows % 4 != 0; // the reference's fallback scans from y[0] (nn_ops.cpp:1184-1196)
-	p.w = W;
+	p.mats[0].w = W;
+	stack_rows(p, &rows, 1);
 	p.x = x;
 	p.x_stride = cols;
-	p.rows = static_cast<int>(rows);
 	p.cols = static_cast<int>(cols);
 	p.n_batch = 1;
 	p.n_split = 1;
@@ -979,8 +1022,8 @@ nnc_status nnc_hip_argmax_f32(nnc_hip_kv* kv, const float* y, uint32_t n, int32_
 	const size_t best_bytes = static_cast<size_t>(nnchip::kArgmaxGroups) * sizeof(float2);
 	if (nnc_status s = reserve(kv, kv->gemv_part, best_bytes + 2 * sizeof(int32_t), "gemv scratch")) return s;
 	nnchip::gemv_params p{};
-	p.y = const_cast<float*>(y);
-	p.rows = static_cast<int>(n);
+	p.mats[0].y = const_cast<float*>(y);
+	stack_rows(p, &n, 1);
 	p.best = static_cast<float2*>(kv->gemv_part.ptr);
 	p.argmax = reinterpret_cast<int*>(static_cast<char*>(kv->gemv_part.ptr) + best_bytes);
 	p.first_sticks = 1;
@@ -996,23 +1039,34 @@ nnc_status nnc_hip_argmax_f32(nnc_hip_kv* kv, const float* y, uint32_t n, int32_
 nnc_status nnc_hip_gemv_bf16(nnc_hip_kv* kv, const void* W, const float* X, size_t x_stride, float* Y, size_t y_stride,
                              uint32_t rows, uint32_t cols, uint32_t n_batch)
 {
-	return gemv_impl(kv, nnchip::kGemvBf16, W, nullptr, nullptr, X, x_stride, nullptr, 0, Y, y_stride, rows, cols,
-	                 n_batch);
+	const nnc_hip_gemv_mat m{W, nullptr, nullptr, Y, y_stride, rows};
+	return gemv_impl(kv, nnchip::kGemvBf16, 1, &m, X, x_stride, nullptr, 0, cols, n_batch);
 }
 
 nnc_status nnc_hip_gemv_q8_0(nnc_hip_kv* kv, const int8_t* qs, const uint16_t* scales, const float* X,
                              size_t x_stride, float* Y, size_t y_stride, uint32_t rows, uint32_t cols,
                              uint32_t n_batch)
 {
-	return gemv_impl(kv, nnchip::kGemvQ8_0, qs, scales, nullptr, X, x_stride, nullptr, 0, Y, y_stride, rows, cols,
-	                 n_batch);
+	const nnc_hip_gemv_mat m{qs, scales, nullptr, Y, y_stride, rows};
+	return gemv_impl(kv, nnchip::kGemvQ8_0, 1, &m, X, x_stride, nullptr, 0, cols, n_batch);
 }
 
 nnc_status nnc_hip_gemv_q4_s(nnc_hip_kv* kv, const uint8_t* qs, const uint16_t* scales, const uint16_t* biases,
                              const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, float* Y,
                              size_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_batch)
 {
-	return gemv_impl(kv, nnchip::kGemvQ4S, qs, scales, biases, X, x_stride, XSUM, xsum_stride, Y, y_stride, rows, cols,
+	const nnc_hip_gemv_mat m{qs, scales, biases, Y, y_stride, rows};
+	return gemv_impl(kv, nnchip::kGemvQ4S, 1, &m, X, x_stride, XSUM, xsum_stride, cols, n_batch);
+}
+
+nnc_status nnc_hip_gemv_group(nnc_hip_kv* kv, int32_t format, int32_t n_mat, const nnc_hip_gemv_mat* mats,
+                              const float* X, size_t x_stride, const float* XSUM, size_t xsum_stride, uint32_t cols,
+                              uint32_t n_batch)
+{
+	static_assert(NNC_HIP_GEMV_BF16 == nnchip::kGemvBf16 && NNC_HIP_GEMV_Q8_0 == nnchip::kGemvQ8_0 &&
+	                  NNC_HIP_GEMV_Q4_S == nnchip::kGemvQ4S && NNC_HIP_GEMV_MAX_GROUP == nnchip::kGemvMaxMats,
+	              "format codes");
+	return gemv_impl(kv, format, n_mat, mats, X, x_stride, format == nnchip::kGemvQ4S ? XSUM : nullptr, xsum_stride, cols,
 	                 n_batch);
 }
 

@@ -61,6 +61,15 @@ _F = C.c_float
 _B = C.c_bool
 _U64 = C.c_uint64
 
+class NncHipGemvMat(C.Structure):
+    """nnc_hip_gemv_mat: one matrix of a gemv group."""
+    _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("y", C.c_void_p),
+                ("y_stride", C.c_size_t), ("rows", C.c_uint32)]
+
+
+GEMV_FORMATS = {"bf16": 0, "q8_0": 1, "q4_s": 2}
+
+
 class NncHipPrep(C.Structure):
     """struct nnc_hip_prep of include/nnc_hip.h (pointers are device addresses)."""
 
@@ -89,6 +98,8 @@ SIGNATURES = {
     "nnc_hip_gemv_bf16_argmax": (C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
     "nnc_hip_argmax_f32": (C.c_int, [_P, _P, C.c_uint32, C.POINTER(C.c_int32)]),
     "nnc_hip_gemv_q8_0": (C.c_int, [_P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "nnc_hip_gemv_group": (C.c_int, [_P, C.c_int32, C.c_int32, C.POINTER(NncHipGemvMat), _P, C.c_size_t, _P,
+                                     C.c_size_t, C.c_uint32, C.c_uint32]),
     "nnc_hip_gemv_q4_s": (C.c_int, [_P, _P, _P, _P, _P, C.c_size_t, _P, C.c_size_t, _P, C.c_size_t, C.c_uint32,
                                     C.c_uint32, C.c_uint32]),
     "nnc_hip_kv_sync": (C.c_int, [_P]),
@@ -347,6 +358,23 @@ class KVCache:
         else:
             raise ValueError(f"unknown weight format {fmt!r}")
         _check(st)
+
+    def gemv_group_device(self, fmt: str, mats: list, x_dev: int, *, cols: int, n_batch: int,
+                          x_stride: int | None = None, xsum_dev: int = 0, xsum_stride: int = 0) -> None:
+        """Several gemvs over the same X in one launch: mats is a list of (w, y_dev,
+        rows) or (w, y_dev, rows, y_stride) with w as in gemv_device; queued on
+        the cache's stream."""
+        arr = (NncHipGemvMat * max(1, len(mats)))()
+        for i, m in enumerate(mats):
+            w, y_dev, rows = m[0], m[1], m[2]
+            ys = m[3] if len(m) > 3 else rows
+            w = tuple(w) + (None,) * (3 - len(w))
+            arr[i] = NncHipGemvMat(w[0], w[1], w[2], y_dev, ys, rows)
+        if fmt not in GEMV_FORMATS:
+            raise ValueError(f"unknown weight format {fmt!r}")
+        _check(self._lib.nnc_hip_gemv_group(self.handle, GEMV_FORMATS[fmt], len(mats), arr, x_dev,
+                                            cols if x_stride is None else x_stride, xsum_dev or None, xsum_stride,
+                                            cols, n_batch))
 
     def gemv(self, fmt: str, w: tuple, x: np.ndarray, *, rows: int, cols: int,
              xsum: np.ndarray | None = None) -> np.ndarray:

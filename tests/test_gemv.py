@@ -201,6 +201,82 @@ def test_hip_gemv_strides_and_errors(orc):
             hip_rt.free(d)
 
 
+# (rows of each matrix, cols, vectors): q/k/v-like and gate/up-like groups, a
+# last matrix with a partial 16-row tile, a batch over 16 vectors (two
+# launches), a K range past one LDS copy (K splits), and a group whose first
+# matrix has 40 rows (not a multiple of 16: run one matrix at a time).
+GROUPS = [
+    ((256, 64, 64), 512, 1),
+    ((256, 64, 64), 512, 5),
+    ((96, 96), 2560, 16),
+    ((64, 32, 40), 256, 20),
+    ((48, 16), 9728, 3),
+    ((40, 64), 256, 1),
+    ((40, 64), 256, 4),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,n", GROUPS, ids=[f"{'+'.join(map(str, r))}x{c}x{n}" for r, c, n in GROUPS])
+def test_hip_gemv_group_equals_single_calls(orc, rows, cols, n):
+    """nnc_hip_gemv_group writes into each matrix's Y exactly the bits its
+    single-matrix call writes (the same kernels and sums per row, the matrices
+    stacked along the rows), for every format; each within the bound of the
+    oracle too."""
+    import libllmcpu_amd as nh
+    from libllmcpu_amd import hip_rt
+
+    rng = np.random.default_rng(sum(rows) + cols + n)
+    wfs = [(rng.standard_normal((r, cols)) * 0.05).astype(np.float32) for r in rows]
+    x = (rng.standard_normal((n, cols)) * 2).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        for fmt in ("bf16", "q8_0", "q4_s"):
+            print(f"case gemv group {fmt} {rows} x {cols}, {n} vectors", flush=True)
+            wls = [layouts(orc, wf)[fmt] for wf in wfs]
+            dev = []
+            try:
+                def up(a):
+                    a = np.ascontiguousarray(a)
+                    d = hip_rt.malloc(max(a.nbytes, 16))
+                    dev.append(d)
+                    hip_rt.to_device(d, a)
+                    return d
+
+                w_dev = [tuple(up(a) for a in wl) for wl in wls]
+                x_dev = up(x)
+                y_grp = [up(np.full((n, r), 7.0, np.float32)) for r in rows]
+                y_one = [up(np.full((n, r), 7.0, np.float32)) for r in rows]
+                kv.gemv_group_device(fmt, [(w, y, r) for w, y, r in zip(w_dev, y_grp, rows)], x_dev, cols=cols,
+                                     n_batch=n)
+                for w, y, r in zip(w_dev, y_one, rows):
+                    kv.gemv_device(fmt, w, x_dev, y, rows=r, cols=cols, n_batch=n)
+                kv.sync()
+                for m, (r, wl) in enumerate(zip(rows, wls)):
+                    got = hip_rt.to_host(np.empty((n, r), np.float32), y_grp[m])
+                    one = hip_rt.to_host(np.empty((n, r), np.float32), y_one[m])
+                    assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), (fmt, m)
+                    err = np.abs(got.astype(np.float64) - oracle_gemv(orc, fmt, wl, x))
+                    assert np.all(err <= bound(fmt, wl, x)), (fmt, m)
+            finally:
+                for d in dev:
+                    hip_rt.free(d)
+
+
+@pytest.mark.gpu
+def test_hip_gemv_group_errors():
+    import libllmcpu_amd as nh
+
+    with nh.KVCache([16], [64]) as kv:
+        print("case gemv group errors", flush=True)
+        for bad in (dict(fmt="bf16", mats=[]), dict(fmt="bf16", mats=[((16,), 16, 16)] * 4)):
+            with pytest.raises(nh.NncError) as e:
+                kv.gemv_group_device(bad["fmt"], bad["mats"], 16, cols=32, n_batch=1)
+            assert e.value.status == nh.NncStatus.INVALID_ARGUMENT
+        with pytest.raises(nh.NncError) as e:  # Q8_0 without scales
+            kv.gemv_group_device("q8_0", [((16,), 16, 16)], 16, cols=32, n_batch=1)
+        assert e.value.status == nh.NncStatus.INVALID_ARGUMENT
+
+
 # ---- the lm_head argmax (reference nn_ops.cpp:1055-1197, model.cpp:2181-2190) ----------
 
 def bf16_rows(rng, rows, cols):
