@@ -15,8 +15,8 @@
 //
 // Grid: (row groups of 64, K splits). A work-group of 4 wavefronts stages its
 // K range of X^T (hi, lo, and for Q4_S the block sums) in LDS once; each
-// wavefront then streams the weights of its 16 rows block by block, four
-// blocks of loads in flight. With one K split the rows go straight to Y; with
+// wavefront then streams the weights of its own 16 rows block by block over
+// the whole range, kAhead blocks of loads in flight. With one K split the rows go straight to Y; with
 // several, each split writes a partial and a second kernel adds the splits in
 // split order, so results are the same run to run.
 #include "device_common.h"
@@ -137,20 +137,20 @@ namespace nnchip
 			uint16_t* s_xh = reinterpret_cast<uint16_t*>(s_raw);
 			uint16_t* s_xl = s_xh + static_cast<size_t>(p.split_blocks) * nt * 32;
 			uint16_t* s_sc = s_xl + static_cast<size_t>(p.split_blocks) * nt * 32;
-			uint16_t* s_bi = s_sc + p.split_blocks * 16;
-			float* s_xs = reinterpret_cast<float*>(s_bi + p.split_blocks * 16); // Q4_S: [block][token] sums of x
-			float* s_red = s_xs + p.split_blocks * nt; // [wavefront][16 rows][16 tokens]
+			uint16_t* s_bi = s_sc + p.split_blocks * 64;
+			float* s_xs = reinterpret_cast<float*>(s_bi + p.split_blocks * 64); // Q4_S: [block][token] sums of x
 
-			// The work-group's 16 rows; wavefront w takes blocks w, w + 4, ... of
-			// the range, kAhead of them in flight, the first ones while X^T is
-			// staged.
-			const int row0 = blockIdx.x * 16;
-			// The tile's matrix (one for all 16 rows) and its rows in it.
-			const mat_row mr = locate(p, row0);
-			const int m_rows = min(16, p.rows - row0); // rows of the tile (only the last matrix's last tile is short)
-			const int ra = mr.r + min(col, m_rows - 1); // this lane's A row in the matrix (clamped; not stored)
-			const int n_mine = nblk > wave ? (nblk - wave + 3) / 4 : 0; // blocks of this wavefront
-			auto my_block = [&](int i) { return b0 + wave + 4 * min(i, max(n_mine - 1, 0)); };
+			// The work-group's 64 rows; wavefront w takes rows 16 w .. 16 w + 15
+			// over every block of the range, kAhead blocks in flight, the first
+			// ones while X^T is staged.
+			const int row0 = blockIdx.x * 64 + 16 * wave;
+			// The tile's matrix (one for all 16 rows) and its rows in it (a tile
+			// past the last row has none and only helps stage X^T).
+			const int m_rows = max(0, min(16, p.rows - row0)); // (only the last matrix's last tile is short)
+			const mat_row mr = locate(p, min(row0, p.rows - 1));
+			const int ra = mr.r + min(col, max(m_rows - 1, 0)); // this lane's A row in the matrix (clamped; not stored)
+			const int n_mine = m_rows > 0 ? nblk : 0; // blocks of this wavefront
+			auto my_block = [&](int i) { return b0 + min(i, max(n_mine - 1, 0)); };
 			a_block<F> ab[kAhead];
 #pragma unroll
 			for (int j = 0; j < kAhead; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
@@ -221,14 +221,16 @@ namespace nnchip
 			}
 			if constexpr (F != kGemvBf16)
 			{
-				// The rows' scales (and biases) of the range, [block][row], so a
-				// lane reads its four rows with one 8-byte read.
-				for (int i = threadIdx.x; i < nblk * 16; i += 256)
+				// The 64 rows' scales (and biases) of the range, [block][row], so
+				// a lane reads its four rows with one 8-byte read.
+				for (int i = threadIdx.x; i < nblk * 64; i += 256)
 				{
 					const int r = i / nblk, b = i % nblk;
-					const size_t src = static_cast<size_t>(mr.r + min(r, m_rows - 1)) * nb_all + b0 + b;
-					s_sc[b * 16 + r] = mr.m.scales[src];
-					if constexpr (F == kGemvQ4S) s_bi[b * 16 + r] = mr.m.biases[src];
+					const int sr = min(blockIdx.x * 64 + r, p.rows - 1); // stacked row (clamped; not used past the end)
+					const mat_row sm = locate(p, sr);
+					const size_t src = static_cast<size_t>(sm.r) * nb_all + b0 + b;
+					s_sc[b * 64 + r] = sm.m.scales[src];
+					if constexpr (F == kGemvQ4S) s_bi[b * 64 + r] = sm.m.biases[src];
 				}
 			}
 			__syncthreads();
@@ -261,7 +263,7 @@ namespace nnchip
 							f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 							d = mfma16x16x32(a, xh, d);
 							d = mfma16x16x32(a, xl, d);
-							const u32x2 sc = *reinterpret_cast<const u32x2*>(s_sc + bl * 16 + 4 * grp);
+							const u32x2 sc = *reinterpret_cast<const u32x2*>(s_sc + bl * 64 + 16 * wave + 4 * grp);
 							acc[0] = fmaf(bf16_lo(sc.x), d[0], acc[0]);
 							acc[1] = fmaf(bf16_hi(sc.x), d[1], acc[1]);
 							acc[2] = fmaf(bf16_lo(sc.y), d[2], acc[2]);
@@ -269,7 +271,7 @@ namespace nnchip
 							if constexpr (F == kGemvQ4S)
 							{
 								// The bias term: bias * (block sum of x).
-								const u32x2 bi = *reinterpret_cast<const u32x2*>(s_bi + bl * 16 + 4 * grp);
+								const u32x2 bi = *reinterpret_cast<const u32x2*>(s_bi + bl * 64 + 16 * wave + 4 * grp);
 								const float xs = col < nt ? s_xs[bl * nt + col] : 0.0f;
 								acc_b[0] = fmaf(bf16_lo(bi.x), xs, acc_b[0]);
 								acc_b[1] = fmaf(bf16_hi(bi.x), xs, acc_b[1]);
@@ -281,17 +283,12 @@ namespace nnchip
 				}
 			}
 
-			// The wavefronts' sums, added in wavefront order: lane (grp, col)
-			// holds rows 4 grp + i of token col.
+			// Lane (grp, col) holds rows 4 grp + i of token col.
 #pragma unroll
 			for (int i = 0; i < 4; ++i)
-				s_red[(wave * 16 + 4 * grp + i) * 16 + col] = F == kGemvQ4S ? acc[i] + acc_b[i] : acc[i];
-			__syncthreads();
 			{
-				const int r = threadIdx.x >> 4, t = threadIdx.x & 15;
-				float v = s_red[r * 16 + t];
-#pragma unroll
-				for (int w = 1; w < 4; ++w) v += s_red[(w * 16 + r) * 16 + t];
+				const int r = 4 * grp + i, t = col;
+				const float v = F == kGemvQ4S ? acc[i] + acc_b[i] : acc[i];
 				if (r < m_rows && t < nt)
 				{
 					if (p.n_split == 1)
@@ -699,7 +696,7 @@ namespace nnchip
 			default: return false;
 			}
 		}
-		const dim3 grid((p.rows + 15) / 16, p.n_split);
+		const dim3 grid((p.rows + 63) / 64, p.n_split);
 		const size_t lds = gemv_lds_bytes(p.split_blocks, p.n_batch);
 		switch (p.format)
 		{

@@ -118,11 +118,11 @@ namespace nnchip
 	constexpr size_t kGemvLdsBudget = 64 << 10; // dynamic LDS per gemv work-group
 
 	// LDS of a gemv work-group over `blocks` 32-column blocks and n_batch
-	// tokens: X^T hi and lo (bf16), 16 rows' scales and biases, the Q4_S block
-	// sums, and the four wavefronts' 16 x 16 sums.
+	// tokens: X^T hi and lo (bf16), the 64 rows' scales and biases, and the
+	// Q4_S block sums.
 	__host__ __device__ inline size_t gemv_lds_bytes(int blocks, int n_batch)
 	{
-		return static_cast<size_t>(blocks) * (128 * n_batch + 64 + 4 * n_batch) + 4 * 256 * 4;
+		return static_cast<size_t>(blocks) * (128 * n_batch + 256 + 4 * n_batch);
 	}
 
 	// One weight matrix of a gemv: its rows' weights, scales and biases, and
