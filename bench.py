@@ -467,7 +467,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other configurations (A, B, C, E)")
-    ap.add_argument("--only", choices=["decode", "prefill", "batch", "gemv", "configs"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "batch", "prep", "gemv", "configs"], default=None,
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
                     help="rocprofv3 --pmc summary giving HBM bytes per decode launch")
@@ -584,6 +584,39 @@ def main() -> int:
 
         log(f"[bench] configs {json.dumps(configs_bench(nh, hip_rt, synth))}")
         return 0
+    def prep_bench():
+        # The pre-attention step (per-head RMSNorm of Q/K, RoPE, K/V append) at
+        # the same shape, after the attention timings (it rewrites q and the
+        # cache rows it appends): one token per layer, then 512-token chunks.
+        k_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
+        v_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
+        gam = hip_rt.malloc(2 * HD * 4)
+        nh.fill_normal(k_in, CHUNK * KV_DIM, 77, 0, False, stream)
+        nh.fill_normal(v_in, CHUNK * KV_DIM, 78, 0, False, stream)
+        hip_rt.to_device(gam, np.ones(2 * HD, np.float32))
+        prep = nh.NncHipPrep(N_HEAD, N_KV, HD, gam, gam + HD * 4, 0, 1e-6, HD, 1000000.0, 1.0, 0, None)
+
+        def prep_step(n_tok, pos0):
+            for li in range(N_LAYER):
+                kv.prep_append_device(li, q_pre + li * PROMPT * N_HEAD * HD * 4, k_in, v_in, pos0=pos0, n_tok=n_tok,
+                                      prep=prep)
+
+        prep_res = {}
+        for label, n_tok, pos0 in (("decode", 1, CTX - 1), ("chunk", CHUNK, PROMPT - CHUNK)):
+            prep_step(n_tok, pos0)
+            ms, _ = timed(lambda: prep_step(n_tok, pos0), 10)
+            us = ms * 1e3 / (10 * N_LAYER)
+            prep_res[label] = {"n_tok": n_tok, "us_per_layer": round(us, 3), "bytes_per_layer": prep_bytes(n_tok),
+                               "gbs": round(prep_bytes(n_tok) / (us * 1e-6) / 1e9, 1)}
+        log(f"[bench] prep decode {prep_res['decode']['us_per_layer']} us/layer, "
+            f"chunk {prep_res['chunk']['us_per_layer']} us/layer ({prep_res['chunk']['gbs']} GB/s)")
+        for p_ in (k_in, v_in, gam):
+            hip_rt.free(p_)
+        return prep_res
+
+    if args.only == "prep":
+        prep_bench()
+        return 0
     if args.only == "batch":
         batch_step()
         hip_rt.sync()
@@ -631,33 +664,7 @@ def main() -> int:
     b_bytes = decode_bytes(CTX) + 2 * (SESSION_BATCH - 1) * N_HEAD * HD * 4
     log(f"[bench] session batch {b_us:.2f} us/layer")
 
-    # The pre-attention step (per-head RMSNorm of Q/K, RoPE, K/V append) at
-    # the same shape, after the attention timings (it rewrites q and the
-    # cache rows it appends): one token per layer, then 512-token chunks.
-    k_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
-    v_in = hip_rt.malloc(CHUNK * KV_DIM * 4)
-    gam = hip_rt.malloc(2 * HD * 4)
-    nh.fill_normal(k_in, CHUNK * KV_DIM, 77, 0, False, stream)
-    nh.fill_normal(v_in, CHUNK * KV_DIM, 78, 0, False, stream)
-    hip_rt.to_device(gam, np.ones(2 * HD, np.float32))
-    prep = nh.NncHipPrep(N_HEAD, N_KV, HD, gam, gam + HD * 4, 0, 1e-6, HD, 1000000.0, 1.0, 0, None)
-
-    def prep_step(n_tok, pos0):
-        for li in range(N_LAYER):
-            kv.prep_append_device(li, q_pre + li * PROMPT * N_HEAD * HD * 4, k_in, v_in, pos0=pos0, n_tok=n_tok,
-                                  prep=prep)
-
-    prep_res = {}
-    for label, n_tok, pos0 in (("decode", 1, CTX - 1), ("chunk", CHUNK, PROMPT - CHUNK)):
-        prep_step(n_tok, pos0)
-        ms, _ = timed(lambda: prep_step(n_tok, pos0), 10)
-        us = ms * 1e3 / (10 * N_LAYER)
-        prep_res[label] = {"n_tok": n_tok, "us_per_layer": round(us, 3), "bytes_per_layer": prep_bytes(n_tok),
-                           "gbs": round(prep_bytes(n_tok) / (us * 1e-6) / 1e9, 1)}
-    log(f"[bench] prep decode {prep_res['decode']['us_per_layer']} us/layer, "
-        f"chunk {prep_res['chunk']['us_per_layer']} us/layer ({prep_res['chunk']['gbs']} GB/s)")
-    for p_ in (k_in, v_in, gam):
-        hip_rt.free(p_)
+    prep_res = prep_bench()
 
     log("[bench] gemv")
     gemv_res = gemv_bench(nh, hip_rt, kv, stream, timed)

@@ -24,6 +24,8 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace nnchip
 {
 	namespace
@@ -31,10 +33,12 @@ namespace nnchip
 		constexpr int kWaves = 4; // wavefronts per work-group
 		constexpr int kMaxHd = 512; // head_dim bound (the reference's RoPE table holds 256 pairs)
 
-		constexpr int kRowsPerWave = 4; // head rows per wavefront, loaded together
-		constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
+		// Head rows per wavefront, loaded together (RPW): 4 for long batches
+		// (fewer, fuller work-groups), 1 for up to 16 tokens, where a row's
+		// exact-order norm chain is the latency and rows side by side in their
+		// own wavefronts finish sooner (one Qwen3-4B decode token: 6.9 -> 3.5 us).
 
-		// Work-group (g, t): head rows 16 g .. 16 g + 15 of token t, where rows
+		// Work-group (g, t): head rows 4 RPW g .. 4 RPW g + 4 RPW - 1 of token t, where rows
 		// 0 .. n_head - 1 are Q heads (updated in place), then n_kv K heads and
 		// n_kv V heads (appended to row (pos0 + t) % rows).
 		// NJ = head_dim / 64, rounded up: values per lane in a row; FULL: head_dim
@@ -104,9 +108,10 @@ namespace nnchip
 			}
 		}
 
-		template <int NJ, bool FULL>
+		template <int NJ, bool FULL, int RPW>
 		__global__ __launch_bounds__(64 * kWaves) void prep_kernel(const prep_params p)
 		{
+			constexpr int kRowsPerWave = RPW, kRowsPerGroup = kWaves * RPW;
 			__shared__ float s_x[kWaves][kMaxHd];
 			const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 			const int t = blockIdx.y;
@@ -322,26 +327,34 @@ namespace nnchip
 	bool launch_prep(const prep_params& p, int n_tok, hipStream_t stream)
 	{
 		if (p.head_dim <= 0 || p.head_dim > kMaxHd || p.n_rot / 2 > kPrepMaxPairs) return false;
-		const int rows = p.n_head + 2 * p.n_kv;
-		const dim3 grid((rows + kRowsPerGroup - 1) / kRowsPerGroup, n_tok);
-		const dim3 block(64 * kWaves);
-		switch (p.head_dim)
+		auto go = [&](auto rpw_tag)
 		{
-		case 64: prep_kernel<1, true><<<grid, block, 0, stream>>>(p); return true;
-		case 128: prep_kernel<2, true><<<grid, block, 0, stream>>>(p); return true;
-		case 256: prep_kernel<4, true><<<grid, block, 0, stream>>>(p); return true;
-		case 512: prep_kernel<8, true><<<grid, block, 0, stream>>>(p); return true;
-		default: break;
-		}
-		const int nj = (p.head_dim + 63) / 64;
-		if (nj <= 1)
-			prep_kernel<1, false><<<grid, block, 0, stream>>>(p);
-		else if (nj <= 2)
-			prep_kernel<2, false><<<grid, block, 0, stream>>>(p);
-		else if (nj <= 4)
-			prep_kernel<4, false><<<grid, block, 0, stream>>>(p);
+			constexpr int RPW = decltype(rpw_tag)::value;
+			const int rows = p.n_head + 2 * p.n_kv;
+			const dim3 grid((rows + kWaves * RPW - 1) / (kWaves * RPW), n_tok);
+			const dim3 block(64 * kWaves);
+			switch (p.head_dim)
+			{
+			case 64: prep_kernel<1, true, RPW><<<grid, block, 0, stream>>>(p); return;
+			case 128: prep_kernel<2, true, RPW><<<grid, block, 0, stream>>>(p); return;
+			case 256: prep_kernel<4, true, RPW><<<grid, block, 0, stream>>>(p); return;
+			case 512: prep_kernel<8, true, RPW><<<grid, block, 0, stream>>>(p); return;
+			default: break;
+			}
+			const int nj = (p.head_dim + 63) / 64;
+			if (nj <= 1)
+				prep_kernel<1, false, RPW><<<grid, block, 0, stream>>>(p);
+			else if (nj <= 2)
+				prep_kernel<2, false, RPW><<<grid, block, 0, stream>>>(p);
+			else if (nj <= 4)
+				prep_kernel<4, false, RPW><<<grid, block, 0, stream>>>(p);
+			else
+				prep_kernel<8, false, RPW><<<grid, block, 0, stream>>>(p);
+		};
+		if (n_tok <= 16)
+			go(std::integral_constant<int, 1>{});
 		else
-			prep_kernel<8, false><<<grid, block, 0, stream>>>(p);
+			go(std::integral_constant<int, 4>{});
 		return true;
 	}
 }
