@@ -318,6 +318,125 @@ namespace nnchip
 			float sc, bi; // the block's scale (Q8_0, Q4_S) and bias (Q4_S)
 		};
 
+		// The lane's dot product of one item (16 bytes of a row at columns
+		// c0 ..) with x in LDS.
+		template <int F>
+		__device__ __forceinline__ float vec_dot(const vec_item<F>& it, int c0, const float* s_x, int cols)
+		{
+			if (c0 >= cols) return 0.0f;
+			if constexpr (F == kGemvBf16)
+			{
+				const float4 x0 = *reinterpret_cast<const float4*>(s_x + c0);
+				const float4 x1 = *reinterpret_cast<const float4*>(s_x + c0 + 4);
+				float d = 0.0f;
+				d = fmaf(bf16_lo(it.w[0]), x0.x, d);
+				d = fmaf(bf16_hi(it.w[0]), x0.y, d);
+				d = fmaf(bf16_lo(it.w[1]), x0.z, d);
+				d = fmaf(bf16_hi(it.w[1]), x0.w, d);
+				d = fmaf(bf16_lo(it.w[2]), x1.x, d);
+				d = fmaf(bf16_hi(it.w[2]), x1.y, d);
+				d = fmaf(bf16_lo(it.w[3]), x1.z, d);
+				d = fmaf(bf16_hi(it.w[3]), x1.w, d);
+				return d;
+			}
+			else if constexpr (F == kGemvQ8_0)
+			{
+				float d = 0.0f;
+#pragma unroll
+				for (int u = 0; u < 4; ++u)
+				{
+					const float4 x = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
+					const uint32_t b = it.w[u] ^ 0x80808080u; // q + 128 per byte
+					d = fmaf(static_cast<float>(b & 0xffu) - 128.0f, x.x, d);
+					d = fmaf(static_cast<float>((b >> 8) & 0xffu) - 128.0f, x.y, d);
+					d = fmaf(static_cast<float>((b >> 16) & 0xffu) - 128.0f, x.z, d);
+					d = fmaf(static_cast<float>(b >> 24) - 128.0f, x.w, d);
+				}
+				return it.sc * d;
+			}
+			else
+			{
+				// Byte i of the block: element i (low nibble), i + 16 (high).
+				float d = 0.0f;
+#pragma unroll
+				for (int u = 0; u < 4; ++u)
+				{
+					const float4 xl = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
+					const float4 xh = *reinterpret_cast<const float4*>(s_x + c0 + 16 + 4 * u);
+					const uint32_t b = it.w[u];
+					d = fmaf(static_cast<float>(b & 0xfu), xl.x, d);
+					d = fmaf(static_cast<float>((b >> 8) & 0xfu), xl.y, d);
+					d = fmaf(static_cast<float>((b >> 16) & 0xfu), xl.z, d);
+					d = fmaf(static_cast<float>((b >> 24) & 0xfu), xl.w, d);
+					d = fmaf(static_cast<float>((b >> 4) & 0xfu), xh.x, d);
+					d = fmaf(static_cast<float>((b >> 12) & 0xfu), xh.y, d);
+					d = fmaf(static_cast<float>((b >> 20) & 0xfu), xh.z, d);
+					d = fmaf(static_cast<float>(b >> 28), xh.w, d);
+				}
+				return fmaf(it.bi, s_x[cols + c0 / 32], it.sc * d);
+			}
+		}
+
+		// 16 bytes of row r of matrix m at columns c0 .. (lanes past the row's
+		// end re-read its last bytes; their sums are not used), with the
+		// block's scale and bias.
+		template <int F>
+		__device__ __forceinline__ vec_item<F> vec_load(const gemv_mat& m, int r, int c0, int cols)
+		{
+			constexpr int CPL = vec_shape<F>::CPL;
+			const int cc = min(c0, cols - CPL);
+			vec_item<F> it;
+			const size_t off = static_cast<size_t>(r) * cols + cc;
+			if constexpr (F == kGemvBf16)
+				it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(m.w) + off);
+			else if constexpr (F == kGemvQ8_0)
+				it.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(m.w) + off);
+			else
+				it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(m.w) + off / 2);
+			if constexpr (F != kGemvBf16)
+			{
+				const size_t si = static_cast<size_t>(r) * (cols / 32) + cc / 32;
+				it.sc = bf16_bits_to_f32(m.scales[si]);
+				if constexpr (F == kGemvQ4S) it.bi = bf16_bits_to_f32(m.biases[si]);
+			}
+			return it;
+		}
+
+		// x into LDS (s_x[0 .. cols)), and for Q4_S its block sums after it;
+		// the caller's barrier follows. Thread t takes elements 4 t .. 4 t + 3
+		// of each 1024. Q4_S without the caller's block sums: the eight threads
+		// of a block hold its quarters q = t % 8, and three lane exchanges add
+		// them in the reference's order (reference nn_ops.cpp:1305-1316 under
+		// its -ffast-math build: l_j = (x_j + x_8+j) + (x_16+j + x_24+j), then
+		// ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7))), so x is read once.
+		template <int F>
+		__device__ __forceinline__ void vec_stage_x(const gemv_params& p, float* s_x)
+		{
+			const int nb_all = p.cols / 32;
+			const bool own_sums = F == kGemvQ4S && p.xsum == nullptr; // uniform
+			for (int i0 = 0; i0 < p.cols; i0 += 1024)
+			{
+				const int i = i0 + 4 * threadIdx.x;
+				const bool ok = i < p.cols; // a block's eight threads agree (cols % 32 == 0)
+				const float4 v = ok ? *reinterpret_cast<const float4*>(p.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				if (ok) *reinterpret_cast<float4*>(s_x + i) = v;
+				if (own_sums)
+				{
+					auto add_from = [](const float4& a, int m) __attribute__((always_inline)) -> float4
+					{
+						return make_float4(a.x + __shfl_xor(a.x, m), a.y + __shfl_xor(a.y, m), a.z + __shfl_xor(a.z, m),
+						                   a.w + __shfl_xor(a.w, m));
+					};
+					const float4 a = add_from(v, 2); // q = 0: x_j + x_8+j; q = 4: x_16+j + x_24+j (j < 4)
+					const float4 l = add_from(a, 4); // q = 0: l_0..3; q = 1: l_4..7
+					const float4 u = add_from(l, 1); // q = 0: l_k + l_k+4
+					if (ok && (threadIdx.x & 7) == 0) s_x[p.cols + i / 32] = (u.x + u.y) + (u.z + u.w);
+				}
+			}
+			if (F == kGemvQ4S && !own_sums)
+				for (int b = threadIdx.x; b < nb_all; b += 256) s_x[p.cols + b] = p.xsum[b];
+		}
+
 		// The argmax order: (v, r) beats (bv, br) when v is above -inf (NaN never
 		// is) and larger, or equal with a smaller row; br = -1 is "none". The
 		// smallest row of the largest value wins whatever order rows are met in.
@@ -337,7 +456,6 @@ namespace nnchip
 			extern __shared__ __attribute__((aligned(16))) float s_x[]; // x, then (Q4_S) its block sums
 			// (wave uniform: every row index below, and the matrix lookup, stays scalar)
 			const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-			const int nb_all = p.cols / 32;
 
 			// Items: for each of this wavefront's row pairs, chunk c of row 0,
 			// then of row 1, for every chunk c of CW columns. Two cursors walk
@@ -369,23 +487,7 @@ namespace nnchip
 			{
 				const bool past = l_pi >= my_pairs;
 				const int rem = past ? per_pair - 1 : l_rem;
-				const int r = l_r0 + ((rem & 1) & l_two);
-				const int c0 = (rem >> 1) * CW + lane * CPL;
-				const int cc = min(c0, p.cols - CPL); // lanes past the row's end re-read its last bytes (not used)
-				vec_item<F> it;
-				const size_t off = static_cast<size_t>(r) * p.cols + cc;
-				if constexpr (F == kGemvBf16)
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(l_m.w) + off);
-				else if constexpr (F == kGemvQ8_0)
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(l_m.w) + off);
-				else
-					it.w = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(l_m.w) + off / 2);
-				if constexpr (F != kGemvBf16)
-				{
-					const size_t si = static_cast<size_t>(r) * nb_all + cc / 32;
-					it.sc = bf16_bits_to_f32(l_m.scales[si]);
-					if constexpr (F == kGemvQ4S) it.bi = bf16_bits_to_f32(l_m.biases[si]);
-				}
+				const vec_item<F> it = vec_load<F>(l_m, l_r0 + ((rem & 1) & l_two), (rem >> 1) * CW + lane * CPL, p.cols);
 				if (!past && ++l_rem == per_pair)
 				{
 					l_rem = 0;
@@ -394,61 +496,9 @@ namespace nnchip
 				}
 				return it;
 			};
-			// The lane's dot product of one item with x.
 			auto dot = [&](const vec_item<F>& it, int c0) __attribute__((always_inline)) -> float
 			{
-				if (c0 >= p.cols) return 0.0f;
-				if constexpr (F == kGemvBf16)
-				{
-					const float4 x0 = *reinterpret_cast<const float4*>(s_x + c0);
-					const float4 x1 = *reinterpret_cast<const float4*>(s_x + c0 + 4);
-					float d = 0.0f;
-					d = fmaf(bf16_lo(it.w[0]), x0.x, d);
-					d = fmaf(bf16_hi(it.w[0]), x0.y, d);
-					d = fmaf(bf16_lo(it.w[1]), x0.z, d);
-					d = fmaf(bf16_hi(it.w[1]), x0.w, d);
-					d = fmaf(bf16_lo(it.w[2]), x1.x, d);
-					d = fmaf(bf16_hi(it.w[2]), x1.y, d);
-					d = fmaf(bf16_lo(it.w[3]), x1.z, d);
-					d = fmaf(bf16_hi(it.w[3]), x1.w, d);
-					return d;
-				}
-				else if constexpr (F == kGemvQ8_0)
-				{
-					float d = 0.0f;
-#pragma unroll
-					for (int u = 0; u < 4; ++u)
-					{
-						const float4 x = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
-						const uint32_t b = it.w[u] ^ 0x80808080u; // q + 128 per byte
-						d = fmaf(static_cast<float>(b & 0xffu) - 128.0f, x.x, d);
-						d = fmaf(static_cast<float>((b >> 8) & 0xffu) - 128.0f, x.y, d);
-						d = fmaf(static_cast<float>((b >> 16) & 0xffu) - 128.0f, x.z, d);
-						d = fmaf(static_cast<float>(b >> 24) - 128.0f, x.w, d);
-					}
-					return it.sc * d;
-				}
-				else
-				{
-					// Byte i of the block: element i (low nibble), i + 16 (high).
-					float d = 0.0f;
-#pragma unroll
-					for (int u = 0; u < 4; ++u)
-					{
-						const float4 xl = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
-						const float4 xh = *reinterpret_cast<const float4*>(s_x + c0 + 16 + 4 * u);
-						const uint32_t b = it.w[u];
-						d = fmaf(static_cast<float>(b & 0xfu), xl.x, d);
-						d = fmaf(static_cast<float>((b >> 8) & 0xfu), xl.y, d);
-						d = fmaf(static_cast<float>((b >> 16) & 0xfu), xl.z, d);
-						d = fmaf(static_cast<float>((b >> 24) & 0xfu), xl.w, d);
-						d = fmaf(static_cast<float>((b >> 4) & 0xfu), xh.x, d);
-						d = fmaf(static_cast<float>((b >> 12) & 0xfu), xh.y, d);
-						d = fmaf(static_cast<float>((b >> 20) & 0xfu), xh.z, d);
-						d = fmaf(static_cast<float>(b >> 28), xh.w, d);
-					}
-					return fmaf(it.bi, s_x[p.cols + c0 / 32], it.sc * d);
-				}
+				return vec_dot<F>(it, c0, s_x, p.cols);
 			};
 
 			// The first loads go out before x is staged.
@@ -456,35 +506,7 @@ namespace nnchip
 #pragma unroll
 			for (int j = 0; j < NA; ++j) ring[j] = load();
 
-			// x into LDS, thread t taking elements 4 t .. 4 t + 3 of each 1024.
-			// Q4_S without the caller's block sums: the eight threads of a block
-			// hold its quarters q = t % 8, and three lane exchanges add them in
-			// the reference's order (reference nn_ops.cpp:1305-1316 under its
-			// -ffast-math build: l_j = (x_j + x_8+j) + (x_16+j + x_24+j), then
-			// ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7))), so x is read
-			// once.
-			const bool own_sums = F == kGemvQ4S && p.xsum == nullptr; // uniform
-			for (int i0 = 0; i0 < p.cols; i0 += 1024)
-			{
-				const int i = i0 + 4 * threadIdx.x;
-				const bool ok = i < p.cols; // a block's eight threads agree (cols % 32 == 0)
-				const float4 v = ok ? *reinterpret_cast<const float4*>(p.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-				if (ok) *reinterpret_cast<float4*>(s_x + i) = v;
-				if (own_sums)
-				{
-					auto add_from = [](const float4& a, int m) __attribute__((always_inline)) -> float4
-					{
-						return make_float4(a.x + __shfl_xor(a.x, m), a.y + __shfl_xor(a.y, m), a.z + __shfl_xor(a.z, m),
-						                   a.w + __shfl_xor(a.w, m));
-					};
-					const float4 a = add_from(v, 2); // q = 0: x_j + x_8+j; q = 4: x_16+j + x_24+j (j < 4)
-					const float4 l = add_from(a, 4); // q = 0: l_0..3; q = 1: l_4..7
-					const float4 u = add_from(l, 1); // q = 0: l_k + l_k+4
-					if (ok && (threadIdx.x & 7) == 0) s_x[p.cols + i / 32] = (u.x + u.y) + (u.z + u.w);
-				}
-			}
-			if (F == kGemvQ4S && !own_sums)
-				for (int b = threadIdx.x; b < nb_all; b += 256) s_x[p.cols + b] = p.xsum[b];
+			vec_stage_x<F>(p, s_x);
 			__syncthreads();
 
 			float acc[2] = {0.0f, 0.0f};
