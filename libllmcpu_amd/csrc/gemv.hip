@@ -318,16 +318,40 @@ namespace nnchip
 			float sc, bi; // the block's scale (Q8_0, Q4_S) and bias (Q4_S)
 		};
 
+		// x in LDS for the one-vector kernels. Q4_S (a lane's 32 columns per
+		// load, its reads 128 bytes apart in column order: 8-way bank
+		// conflicts) keeps it in the order the lanes read it: the four
+		// consecutive columns 4 g .. 4 g + 3 of lane l's CPL columns of a
+		// CW-column chunk sit at chunk * CW + 256 g + 4 l, so each of a
+		// wavefront's 16-byte LDS reads covers 1 KB of consecutive addresses
+		// (Qwen3-4B layer, one vector: 58.3 -> 51.6 us), the chunks padded to
+		// CW columns and the block sums after them. BF16 and Q8_0 keep column
+		// order (the same layout measured no faster for BF16, 6 % slower for
+		// Q8_0).
+		template <int F>
+		constexpr bool kVecLaneOrder = F == kGemvQ4S;
+
+		template <int F>
+		__host__ __device__ constexpr int vec_x_floats(int cols)
+		{
+			return kVecLaneOrder<F> ? (cols + vec_shape<F>::CW - 1) / vec_shape<F>::CW * vec_shape<F>::CW : cols;
+		}
+
 		// The lane's dot product of one item (16 bytes of a row at columns
 		// c0 ..) with x in LDS.
 		template <int F>
 		__device__ __forceinline__ float vec_dot(const vec_item<F>& it, int c0, const float* s_x, int cols)
 		{
+			constexpr int CPL = vec_shape<F>::CPL;
 			if (c0 >= cols) return 0.0f;
+			const int lane = threadIdx.x & 63;
+			// columns c0 + 4 g .. + 3 at xq + GS g
+			constexpr int GS = kVecLaneOrder<F> ? 256 : 4;
+			const float* xq = kVecLaneOrder<F> ? s_x + (c0 - lane * CPL) + 4 * lane : s_x + c0;
 			if constexpr (F == kGemvBf16)
 			{
-				const float4 x0 = *reinterpret_cast<const float4*>(s_x + c0);
-				const float4 x1 = *reinterpret_cast<const float4*>(s_x + c0 + 4);
+				const float4 x0 = *reinterpret_cast<const float4*>(xq);
+				const float4 x1 = *reinterpret_cast<const float4*>(xq + GS);
 				float d = 0.0f;
 				d = fmaf(bf16_lo(it.w[0]), x0.x, d);
 				d = fmaf(bf16_hi(it.w[0]), x0.y, d);
@@ -345,7 +369,7 @@ namespace nnchip
 #pragma unroll
 				for (int u = 0; u < 4; ++u)
 				{
-					const float4 x = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
+					const float4 x = *reinterpret_cast<const float4*>(xq + GS * u);
 					const uint32_t b = it.w[u] ^ 0x80808080u; // q + 128 per byte
 					d = fmaf(static_cast<float>(b & 0xffu) - 128.0f, x.x, d);
 					d = fmaf(static_cast<float>((b >> 8) & 0xffu) - 128.0f, x.y, d);
@@ -361,8 +385,8 @@ namespace nnchip
 #pragma unroll
 				for (int u = 0; u < 4; ++u)
 				{
-					const float4 xl = *reinterpret_cast<const float4*>(s_x + c0 + 4 * u);
-					const float4 xh = *reinterpret_cast<const float4*>(s_x + c0 + 16 + 4 * u);
+					const float4 xl = *reinterpret_cast<const float4*>(xq + GS * u); // columns 4 u ..
+					const float4 xh = *reinterpret_cast<const float4*>(xq + GS * (4 + u)); // columns 16 + 4 u ..
 					const uint32_t b = it.w[u];
 					d = fmaf(static_cast<float>(b & 0xfu), xl.x, d);
 					d = fmaf(static_cast<float>((b >> 8) & 0xfu), xl.y, d);
@@ -373,7 +397,7 @@ namespace nnchip
 					d = fmaf(static_cast<float>((b >> 20) & 0xfu), xh.z, d);
 					d = fmaf(static_cast<float>(b >> 28), xh.w, d);
 				}
-				return fmaf(it.bi, s_x[cols + c0 / 32], it.sc * d);
+				return fmaf(it.bi, s_x[vec_x_floats<F>(cols) + c0 / 32], it.sc * d);
 			}
 		}
 
@@ -402,8 +426,8 @@ namespace nnchip
 			return it;
 		}
 
-		// x into LDS (s_x[0 .. cols)), and for Q4_S its block sums after it;
-		// the caller's barrier follows. Thread t takes elements 4 t .. 4 t + 3
+		// x into LDS (in the lanes' order for Q4_S, vec_x_floats), and for Q4_S
+		// its block sums after it; the caller's barrier follows. Thread t takes elements 4 t .. 4 t + 3
 		// of each 1024. Q4_S without the caller's block sums: the eight threads
 		// of a block hold its quarters q = t % 8, and three lane exchanges add
 		// them in the reference's order (reference nn_ops.cpp:1305-1316 under
@@ -412,14 +436,18 @@ namespace nnchip
 		template <int F>
 		__device__ __forceinline__ void vec_stage_x(const gemv_params& p, float* s_x)
 		{
+			constexpr int CW = vec_shape<F>::CW, CPL = vec_shape<F>::CPL;
 			const int nb_all = p.cols / 32;
+			const int xs = vec_x_floats<F>(p.cols); // the block sums' offset
 			const bool own_sums = F == kGemvQ4S && p.xsum == nullptr; // uniform
 			for (int i0 = 0; i0 < p.cols; i0 += 1024)
 			{
 				const int i = i0 + 4 * threadIdx.x;
 				const bool ok = i < p.cols; // a block's eight threads agree (cols % 32 == 0)
 				const float4 v = ok ? *reinterpret_cast<const float4*>(p.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-				if (ok) *reinterpret_cast<float4*>(s_x + i) = v;
+				const int rem = i % CW; // lane rem / CPL, group (rem % CPL) / 4 of chunk i / CW
+				const int dst = kVecLaneOrder<F> ? (i - rem) + 256 * ((rem % CPL) / 4) + 4 * (rem / CPL) : i;
+				if (ok) *reinterpret_cast<float4*>(s_x + dst) = v;
 				if (own_sums)
 				{
 					auto add_from = [](const float4& a, int m) __attribute__((always_inline)) -> float4
@@ -430,11 +458,11 @@ namespace nnchip
 					const float4 a = add_from(v, 2); // q = 0: x_j + x_8+j; q = 4: x_16+j + x_24+j (j < 4)
 					const float4 l = add_from(a, 4); // q = 0: l_0..3; q = 1: l_4..7
 					const float4 u = add_from(l, 1); // q = 0: l_k + l_k+4
-					if (ok && (threadIdx.x & 7) == 0) s_x[p.cols + i / 32] = (u.x + u.y) + (u.z + u.w);
+					if (ok && (threadIdx.x & 7) == 0) s_x[xs + i / 32] = (u.x + u.y) + (u.z + u.w);
 				}
 			}
 			if (F == kGemvQ4S && !own_sums)
-				for (int b = threadIdx.x; b < nb_all; b += 256) s_x[p.cols + b] = p.xsum[b];
+				for (int b = threadIdx.x; b < nb_all; b += 256) s_x[xs + b] = p.xsum[b];
 		}
 
 		// The argmax order: (v, r) beats (bv, br) when v is above -inf (NaN never
@@ -562,7 +590,7 @@ namespace nnchip
 			{
 				// The work-group's best: the four wavefronts' (lane 0's), after x
 				// in LDS, then one (value, row) pair per work-group.
-				float* s_best = s_x + p.cols;
+				float* s_best = s_x + vec_x_floats<F>(p.cols);
 				if (lane == 0)
 				{
 					s_best[2 * wave] = best_v;
@@ -699,16 +727,26 @@ namespace nnchip
 		return std::max(1, std::min((n_pairs + 3) / 4, 512));
 	}
 
-	bool gemv_vec_fits(int cols, int n_batch)
+	// LDS of the one-vector kernel: x in the lanes' order (padded to whole
+	// chunks), then Q4_S's block sums, or the argmax's eight floats.
+	static size_t gemv_vec_lds(int cols, int format)
 	{
-		return n_batch == 1 && static_cast<size_t>(cols + cols / 32) * 4 <= kGemvLdsBudget;
+		const int xf = format == kGemvBf16   ? vec_x_floats<kGemvBf16>(cols)
+		               : format == kGemvQ8_0 ? vec_x_floats<kGemvQ8_0>(cols)
+		                                     : vec_x_floats<kGemvQ4S>(cols);
+		return static_cast<size_t>(xf + std::max(cols / 32, 8)) * 4;
+	}
+
+	bool gemv_vec_fits(int cols, int n_batch, int format)
+	{
+		return n_batch == 1 && gemv_vec_lds(cols, format) <= kGemvLdsBudget;
 	}
 
 	bool launch_gemv(const gemv_params& p, hipStream_t stream)
 	{
-		if (gemv_vec_fits(p.cols, p.n_batch))
+		if (gemv_vec_fits(p.cols, p.n_batch, p.format))
 		{
-			const size_t lds = static_cast<size_t>(p.cols + p.cols / 32) * 4;
+			const size_t lds = gemv_vec_lds(p.cols, p.format);
 			const dim3 grid(gemv_vec_groups(p.rows));
 			switch (p.format)
 			{
@@ -738,9 +776,9 @@ namespace nnchip
 
 	bool launch_gemv_argmax(const gemv_params& p, hipStream_t stream)
 	{
-		if (p.format != kGemvBf16 || !gemv_vec_fits(p.cols, 1)) return false;
+		if (p.format != kGemvBf16 || !gemv_vec_fits(p.cols, 1, kGemvBf16)) return false;
 		const int groups = gemv_vec_groups(p.rows);
-		const size_t lds = (static_cast<size_t>(p.cols) + 8) * 4; // x, then the wavefronts' best pairs
+		const size_t lds = gemv_vec_lds(p.cols, kGemvBf16); // x, then the wavefronts' best pairs
 		gemv_vec_kernel<kGemvBf16, true><<<groups, 256, lds, stream>>>(p);
 		gemv_argmax_final_kernel<<<1, 256, 0, stream>>>(p, groups);
 		return true;

@@ -170,11 +170,11 @@ namespace nnchip
 	// best pairs launch_gemv_argmax writes), and whether a gemv of `cols`
 	// columns and n_batch vectors runs on it.
 	int gemv_vec_groups(int rows);
-	bool gemv_vec_fits(int cols, int n_batch);
+	bool gemv_vec_fits(int cols, int n_batch, int format);
 
 	// argmax_r y[r] for a BF16 gemv of one vector (p.best, p.argmax set):
 	// the smallest row of the largest value above -inf, NaN never chosen, 0
-	// when there is none. Needs gemv_vec_fits(p.cols, 1).
+	// when there is none. Needs gemv_vec_fits(p.cols, 1, kGemvBf16).
 	bool launch_gemv_argmax(const gemv_params& p, hipStream_t stream);
 
 	// The same argmax over a float vector y of p.rows elements (p.y read, p.best

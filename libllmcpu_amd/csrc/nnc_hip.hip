@@ -980,7 +980,7 @@ nnc_status nnc_hip_gemv_bf16_argmax(nnc_hip_kv* kv, const void* W, const float* 
 		return NNC_OK;
 	}
 	if (rows > 0x7fffffffu || cols > 0x7fffffffu) return fail(NNC_ERR_INVALID_ARGUMENT, "gemv of %u x %u", rows, cols);
-	if (cols % 32 != 0 || !nnchip::gemv_vec_fits(static_cast<int>(cols), 1))
+	if (cols % 32 != 0 || !nnchip::gemv_vec_fits(static_cast<int>(cols), 1, nnchip::kGemvBf16))
 		return fail(NNC_ERR_UNSUPPORTED_MODEL, "argmax gemv with %u columns (a multiple of 32, at most 15872)", cols);
 	if ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(x)) & 15)
 		return fail(NNC_ERR_INVALID_ARGUMENT, "weights and x must be 16-byte aligned");
