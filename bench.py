@@ -74,13 +74,24 @@ BOX_CPU_SHARE = 16  # host CPUs one GPU's jobs may use on the GPU boxes
 
 
 def cpu_model() -> str:
+    """/proc/cpuinfo's model name with its family, model and stepping (a VM
+    may report only "AMD EPYC"; family 26 is AMD's Zen 5 generation)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping", "flags") and k not in info:
+                info[k] = v.strip()
+            if len(info) == 5:
+                break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    extra = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    flags = info.get("flags", "").split()
+    tags = [t for t in ("avx512f", "avx512_bf16", "hypervisor") if t in flags]
+    return f"{name} ({extra}{'; ' + ' '.join(tags) if tags else ''})" if extra else name
 
 
 def cpu_baseline(kv, target_s: float) -> dict:
