@@ -382,7 +382,7 @@ namespace nnchip
 		template <int HD, int G>
 		__global__ __launch_bounds__(256) void f32_decode_kernel(const decode_params p)
 		{
-			constexpr int W = 4, kWaves = W, kThreads = 64 * W;
+			constexpr int W = 4, kWaves = W;
 			using S = f32_shape<HD>;
 			constexpr int CH = S::CH, NT = S::NT, KK = S::KK, VEC = S::VEC, LPK = S::LPK, KPL = S::KPL, NV = S::NV;
 			constexpr int PW = part_pitch<HD>();

@@ -137,14 +137,6 @@ namespace nnchip
 			return HD == 64 ? (row >> 1) & 7 : row & 15;
 		}
 
-		// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land
-		// at lds + 16 l (the LDS address is uniform over the wavefront).
-		__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voffset)
-		{
-			typedef __attribute__((address_space(3))) void* lds_ptr;
-			__builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr)lds, 16, voffset, 0, 0, 0);
-		}
-
 		// DMA j of a tile: 16 bytes per lane from buffer offset voffset into
 		// the tile at byte 1024 j + 16 l. The instruction offset (1024 (j % 4))
 		// is added to both the buffer offset (and its range check) and the LDS

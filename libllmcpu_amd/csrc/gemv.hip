@@ -638,7 +638,7 @@ namespace nnchip
 			__syncthreads();
 			for (int h = 128; h > 0; h >>= 1)
 			{
-				if (threadIdx.x < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
+				if (static_cast<int>(threadIdx.x) < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
 				                                     s_r[threadIdx.x]))
 				{
 					s_v[threadIdx.x] = s_v[threadIdx.x + h];
@@ -672,7 +672,7 @@ namespace nnchip
 			__syncthreads();
 			for (int h = 128; h > 0; h >>= 1)
 			{
-				if (threadIdx.x < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
+				if (static_cast<int>(threadIdx.x) < h && argmax_better(s_v[threadIdx.x + h], s_r[threadIdx.x + h], s_v[threadIdx.x],
 				                                     s_r[threadIdx.x]))
 				{
 					s_v[threadIdx.x] = s_v[threadIdx.x + h];

@@ -131,7 +131,6 @@ namespace
 	std::mutex g_scratch_mu;
 	void* g_scratch_ptr[kMaxDevices] = {};
 
-	constexpr int kAttnBlock = 256; // reference model.h:229
 	constexpr int32_t kDecodeChunk = 1024; // tokens per split-K launch
 	// Most tokens one forward pass of an nnc session carries
 	// (MODEL_PREFILL_BATCH, reference model.h:330; session.cpp:340), its MTP
@@ -223,16 +222,6 @@ namespace
 		return NNC_OK;
 	}
 
-	// Host rows -> device memory through the pinned staging (asynchronous on
-	// the cache's stream; the host rows are free on return).
-	nnc_status upload(nnc_hip_kv* kv, void* dst, const void* src, size_t bytes, const char* what)
-	{
-		if (nnc_status s = reserve_pinned(kv, bytes, what)) return s;
-		std::memcpy(kv->pinned.ptr, src, bytes);
-		NNC_HIP_TRY(hipMemcpyAsync(dst, kv->pinned.ptr, bytes, hipMemcpyHostToDevice, kv->stream), what);
-		NNC_HIP_TRY(hipEventRecord(kv->pinned.free, kv->stream), what);
-		return NNC_OK;
-	}
 
 	// The cos/sin of every RoPE angle of tokens pos0 .. pos0 + n_tok - 1 on the
 	// device, computed on the host the way the reference computes them
