@@ -263,6 +263,59 @@ def test_hip_gemv_group_equals_single_calls(orc, rows, cols, n):
 
 
 @pytest.mark.gpu
+def test_hip_gemv_group_strides_and_block_sums(orc):
+    """A group with y_stride past each matrix's rows (the gap untouched) and X
+    rows x_stride apart, and for Q4_S the caller's block sums: each Y equals its
+    single-matrix call's bits."""
+    import libllmcpu_amd as nh
+    from libllmcpu_amd import hip_rt
+
+    rows, cols, n = (64, 32), 256, 3
+    xs = cols + 64
+    rng = np.random.default_rng(77)
+    wfs = [(rng.standard_normal((r, cols)) * 0.05).astype(np.float32) for r in rows]
+    x = (rng.standard_normal((n, cols)) * 2).astype(np.float32)
+    xp = np.zeros((n, xs), np.float32)
+    xp[:, :cols] = x
+    sums = orc.block_sums(x).astype(np.float32)
+    with nh.KVCache([16], [64]) as kv:
+        for fmt in ("bf16", "q8_0", "q4_s"):
+            print(f"case gemv group strides {fmt}", flush=True)
+            wls = [layouts(orc, wf)[fmt] for wf in wfs]
+            dev = []
+            try:
+                def up(a):
+                    a = np.ascontiguousarray(a)
+                    d = hip_rt.malloc(max(a.nbytes, 16))
+                    dev.append(d)
+                    hip_rt.to_device(d, a)
+                    return d
+
+                w_dev = [tuple(up(a) for a in wl) for wl in wls]
+                x_dev, s_dev = up(xp), up(sums)
+                ys = [r + 8 for r in rows]
+                y_grp = [up(np.full((n, y), 7.0, np.float32)) for y in ys]
+                y_one = [up(np.full((n, y), 7.0, np.float32)) for y in ys]
+                q4 = fmt == "q4_s"
+                kv.gemv_group_device(fmt, [(w, y, r, st) for w, y, r, st in zip(w_dev, y_grp, rows, ys)], x_dev,
+                                     cols=cols, n_batch=n, x_stride=xs, xsum_dev=s_dev if q4 else 0,
+                                     xsum_stride=cols // 32)
+                for w, y, r, st in zip(w_dev, y_one, rows, ys):
+                    kv.gemv_device(fmt, w, x_dev, y, rows=r, cols=cols, n_batch=n, x_stride=xs, y_stride=st,
+                                   xsum_dev=s_dev if q4 else 0, xsum_stride=cols // 32)
+                kv.sync()
+                for m, (r, st) in enumerate(zip(rows, ys)):
+                    got = hip_rt.to_host(np.empty((n, st), np.float32), y_grp[m])
+                    one = hip_rt.to_host(np.empty((n, st), np.float32), y_one[m])
+                    assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), (fmt, m)
+                    assert np.all(got[:, r:] == 7.0)  # the gap between output rows is untouched
+                    assert np.all(np.abs(got[:, :r] - oracle_gemv(orc, fmt, wls[m], x)) <= bound(fmt, wls[m], x))
+            finally:
+                for d in dev:
+                    hip_rt.free(d)
+
+
+@pytest.mark.gpu
 def test_hip_gemv_group_errors():
     import libllmcpu_amd as nh
 
