@@ -1139,12 +1139,13 @@ namespace nnchip
 						vta[c][db] = u32x4{lo.x, lo.y, hi.x, hi.y};
 					}
 
-				// One tile at a time: its scores (the hi and lo products in their
-				// own chains, added once: the operations of scores_hilo), then its
-				// softmax and P.V. The next chunk's K and V rows load once the
-				// last tile's scores no longer need the K registers.
-#pragma unroll
-				for (int tl = 0; tl < NTL; ++tl)
+				// A tile's scores (the hi and lo products in their own chains,
+				// added once: the operations of scores_hilo), then its softmax and
+				// P.V. The last two tiles' scores come first, then the next chunk's
+				// K rows load (two tiles of work to land in), and its V rows before
+				// the last tile's softmax (all four tiles' scores at once, or the V
+				// rows a tile earlier, would not fit the registers).
+				auto tile_scores = [&](int tl, f32x4 (&out)[NT]) __attribute__((always_inline))
 				{
 					// (the lo chain accumulates in sc, the hi chain in sh)
 					f32x4 sc[NT], sh[NT];
@@ -1164,13 +1165,10 @@ namespace nnchip
 						}
 					}
 #pragma unroll
-					for (int t = 0; t < NT; ++t) sc[t] = sh[t] + sc[t];
-					if (tl == NTL - 1)
-					{
-						load_k(cw + LPH);
-						load_v(cw + LPH);
-					}
-
+					for (int t = 0; t < NT; ++t) out[t] = sh[t] + sc[t];
+				};
+				auto tile_softmax_pv = [&](int tl, f32x4 (&sc)[NT]) __attribute__((always_inline))
+				{
 					const bool real = (16 * tl + col) / G < n_tt;
 					const float m_loc = softmax_mask_max<NT>(sc, cbase, col_s0[tl], col_s1[tl], real, CH);
 					const float m_new = lazy_offset(m_run[tl], m_loc);
@@ -1200,7 +1198,21 @@ namespace nnchip
 					for (int c = 0; c < NC; ++c)
 #pragma unroll
 						for (int db = 0; db < DB; ++db) pv_mfma(acc_o[tl][db], vta[c][db], pb[c]);
+				};
+#pragma unroll
+				for (int tl = 0; tl < NTL - 2; ++tl)
+				{
+					f32x4 sc[NT];
+					tile_scores(tl, sc);
+					tile_softmax_pv(tl, sc);
 				}
+				f32x4 sa[NT], sb[NT];
+				tile_scores(NTL - 2, sa);
+				tile_scores(NTL - 1, sb);
+				load_k(cw + LPH);
+				tile_softmax_pv(NTL - 2, sa);
+				load_v(cw + LPH);
+				tile_softmax_pv(NTL - 1, sb);
 				wave_sync(); // V is read before the next chunk overwrites it
 			};
 			for (int i = 0; i < n_wchunks; ++i, c_wave += LPH) chunk(c_wave);
