@@ -13,10 +13,11 @@
 // quantised block's product starts from zero and is scaled into the row's sum
 // with the block's scale; Q4_S adds bias * (block sum of x) in a second sum.
 //
-// Grid: (row groups of 64, K splits). A work-group of 4 wavefronts stages its
-// K range of X^T (hi, lo, and for Q4_S the block sums) in LDS once; each
-// wavefront then streams the weights of its own 16 rows block by block over
-// the whole range, kAhead blocks of loads in flight. With one K split the rows go straight to Y; with
+// Grid: (row groups of kGemvRows = 128, K splits). A work-group of 8
+// wavefronts (two work-groups per CU) stages its K range of X^T (hi, lo, and
+// for Q4_S the block sums) in LDS once; each wavefront then streams the
+// weights of its own 16 rows block by block over the whole range, kAhead
+// blocks of loads in flight. With one K split the rows go straight to Y; with
 // several, each split writes a partial and a second kernel adds the splits in
 // split order, so results are the same run to run.
 #include "device_common.h"
@@ -123,7 +124,7 @@ namespace nnchip
 		}
 
 		template <int F>
-		__global__ __launch_bounds__(256) void gemv_kernel(const gemv_params p)
+		__global__ __launch_bounds__(4 * kGemvRows) void gemv_kernel(const gemv_params p)
 		{
 			// Dynamic LDS: X^T hi and lo [block][token][32 slots] (bf16), the 16
 			// rows' scales (and biases) [block][16], and the wavefronts' sums.
@@ -137,13 +138,13 @@ namespace nnchip
 			uint16_t* s_xh = reinterpret_cast<uint16_t*>(s_raw);
 			uint16_t* s_xl = s_xh + static_cast<size_t>(p.split_blocks) * nt * 32;
 			uint16_t* s_sc = s_xl + static_cast<size_t>(p.split_blocks) * nt * 32;
-			uint16_t* s_bi = s_sc + p.split_blocks * 64;
-			float* s_xs = reinterpret_cast<float*>(s_bi + p.split_blocks * 64); // Q4_S: [block][token] sums of x
+			uint16_t* s_bi = s_sc + p.split_blocks * kGemvRows;
+			float* s_xs = reinterpret_cast<float*>(s_bi + p.split_blocks * kGemvRows); // Q4_S: [block][token] sums of x
 
-			// The work-group's 64 rows; wavefront w takes rows 16 w .. 16 w + 15
+			// The work-group's kGemvRows rows; wavefront w takes rows 16 w .. 16 w + 15
 			// over every block of the range, kAhead blocks in flight, the first
 			// ones while X^T is staged.
-			const int row0 = blockIdx.x * 64 + 16 * wave;
+			const int row0 = blockIdx.x * kGemvRows + 16 * wave;
 			// The tile's matrix (one for all 16 rows) and its rows in it (a tile
 			// past the last row has none and only helps stage X^T).
 			const int m_rows = max(0, min(16, p.rows - row0)); // (only the last matrix's last tile is short)
@@ -158,13 +159,13 @@ namespace nnchip
 			// X^T of the range, four columns per piece (consecutive threads read
 			// consecutive 16 bytes of a token's row), loads issued eight at a time.
 			const int n_pieces = nblk * nt * 8;
-			for (int i0 = 0; i0 < n_pieces; i0 += 256 * 8)
+			for (int i0 = 0; i0 < n_pieces; i0 += 4 * kGemvRows * 8)
 			{
 				float4 xv[8];
 #pragma unroll
 				for (int u = 0; u < 8; ++u)
 				{
-					const int i = i0 + threadIdx.x + 256 * u;
+					const int i = i0 + threadIdx.x + 4 * kGemvRows * u;
 					const int q = i & 7, b = (i >> 3) % nblk, t = (i >> 3) / nblk;
 					xv[u] = i < n_pieces ? *reinterpret_cast<const float4*>(p.x + t * p.x_stride + 32 * (b0 + b) + 4 * q)
 					                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -172,7 +173,7 @@ namespace nnchip
 #pragma unroll
 				for (int u = 0; u < 8; ++u)
 				{
-					const int i = i0 + threadIdx.x + 256 * u;
+					const int i = i0 + threadIdx.x + 4 * kGemvRows * u;
 					if (i >= n_pieces) continue;
 					const int q = i & 7, b = (i >> 3) % nblk, t = (i >> 3) / nblk;
 					// The piece's first k-slot; its four columns take four consecutive slots.
@@ -192,7 +193,7 @@ namespace nnchip
 				// (reference nn_ops.cpp:1305-1316 under its -ffast-math build:
 				// lane j = (x[j] + x[8 + j]) + (x[16 + j] + x[24 + j]), then the
 				// lanes pairwise).
-				for (int i = threadIdx.x; i < nblk * nt; i += 256)
+				for (int i = threadIdx.x; i < nblk * nt; i += 4 * kGemvRows)
 				{
 					const int b = i % nblk, t = i / nblk;
 					float sum;
@@ -221,16 +222,16 @@ namespace nnchip
 			}
 			if constexpr (F != kGemvBf16)
 			{
-				// The 64 rows' scales (and biases) of the range, [block][row], so
+				// The work-group's rows' scales (and biases) of the range, [block][row], so
 				// a lane reads its four rows with one 8-byte read.
-				for (int i = threadIdx.x; i < nblk * 64; i += 256)
+				for (int i = threadIdx.x; i < nblk * kGemvRows; i += 4 * kGemvRows)
 				{
 					const int r = i / nblk, b = i % nblk;
-					const int sr = min(blockIdx.x * 64 + r, p.rows - 1); // stacked row (clamped; not used past the end)
+					const int sr = min(blockIdx.x * kGemvRows + r, p.rows - 1); // stacked row (clamped; not used past the end)
 					const mat_row sm = locate(p, sr);
 					const size_t src = static_cast<size_t>(sm.r) * nb_all + b0 + b;
-					s_sc[b * 64 + r] = sm.m.scales[src];
-					if constexpr (F == kGemvQ4S) s_bi[b * 64 + r] = sm.m.biases[src];
+					s_sc[b * kGemvRows + r] = sm.m.scales[src];
+					if constexpr (F == kGemvQ4S) s_bi[b * kGemvRows + r] = sm.m.biases[src];
 				}
 			}
 			__syncthreads();
@@ -263,7 +264,7 @@ namespace nnchip
 							f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 							d = mfma16x16x32(a, xh, d);
 							d = mfma16x16x32(a, xl, d);
-							const u32x2 sc = *reinterpret_cast<const u32x2*>(s_sc + bl * 64 + 16 * wave + 4 * grp);
+							const u32x2 sc = *reinterpret_cast<const u32x2*>(s_sc + bl * kGemvRows + 16 * wave + 4 * grp);
 							acc[0] = fmaf(bf16_lo(sc.x), d[0], acc[0]);
 							acc[1] = fmaf(bf16_hi(sc.x), d[1], acc[1]);
 							acc[2] = fmaf(bf16_lo(sc.y), d[2], acc[2]);
@@ -271,7 +272,7 @@ namespace nnchip
 							if constexpr (F == kGemvQ4S)
 							{
 								// The bias term: bias * (block sum of x).
-								const u32x2 bi = *reinterpret_cast<const u32x2*>(s_bi + bl * 64 + 16 * wave + 4 * grp);
+								const u32x2 bi = *reinterpret_cast<const u32x2*>(s_bi + bl * kGemvRows + 16 * wave + 4 * grp);
 								const float xs = col < nt ? s_xs[bl * nt + col] : 0.0f;
 								acc_b[0] = fmaf(bf16_lo(bi.x), xs, acc_b[0]);
 								acc_b[1] = fmaf(bf16_hi(bi.x), xs, acc_b[1]);
@@ -716,7 +717,7 @@ namespace nnchip
 		// As few K splits as the LDS copy of X^T allows (one for a single
 		// vector at every nnc shape), the splits equal in size.
 		int max_blocks = 1;
-		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= kGemvLdsBudget) ++max_blocks;
+		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= kGemvBatchLds) ++max_blocks;
 		n_split = (nb + max_blocks - 1) / max_blocks;
 		split_blocks = (nb + n_split - 1) / n_split;
 	}
@@ -756,13 +757,13 @@ namespace nnchip
 			default: return false;
 			}
 		}
-		const dim3 grid((p.rows + 63) / 64, p.n_split);
+		const dim3 grid((p.rows + kGemvRows - 1) / kGemvRows, p.n_split);
 		const size_t lds = gemv_lds_bytes(p.split_blocks, p.n_batch);
 		switch (p.format)
 		{
-		case kGemvBf16: gemv_kernel<kGemvBf16><<<grid, 256, lds, stream>>>(p); break;
-		case kGemvQ8_0: gemv_kernel<kGemvQ8_0><<<grid, 256, lds, stream>>>(p); break;
-		case kGemvQ4S: gemv_kernel<kGemvQ4S><<<grid, 256, lds, stream>>>(p); break;
+		case kGemvBf16: gemv_kernel<kGemvBf16><<<grid, 4 * kGemvRows, lds, stream>>>(p); break;
+		case kGemvQ8_0: gemv_kernel<kGemvQ8_0><<<grid, 4 * kGemvRows, lds, stream>>>(p); break;
+		case kGemvQ4S: gemv_kernel<kGemvQ4S><<<grid, 4 * kGemvRows, lds, stream>>>(p); break;
 		default: return false;
 		}
 		if (p.n_split > 1)
