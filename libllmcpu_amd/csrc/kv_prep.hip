@@ -211,7 +211,16 @@ namespace nnchip
 					const int body = hd & ~7;
 					float chain = 0.0f;
 					if (lane < 8)
-						for (int i = lane; i < body; i += 8) chain = __builtin_fmaf(xs[i], xs[i], chain);
+					{
+						if constexpr (FULL)
+						{
+							// (head_dim = 64 NJ: a chain of 8 NJ, its reads all issued first)
+#pragma unroll
+							for (int k = 0; k < 8 * NJ; ++k) chain = __builtin_fmaf(xs[lane + 8 * k], xs[lane + 8 * k], chain);
+						}
+						else
+							for (int i = lane; i < body; i += 8) chain = __builtin_fmaf(xs[i], xs[i], chain);
+					}
 					float c8[8];
 #pragma unroll
 					for (int l = 0; l < 8; ++l) c8[l] = __shfl(chain, l);
