@@ -710,14 +710,14 @@ namespace nnchip
 		}
 	}
 
-	void gemv_plan(int rows, int cols, int n_batch, int& n_split, int& split_blocks)
+	void gemv_plan(int rows, int cols, int n_batch, int format, int& n_split, int& split_blocks)
 	{
 		(void)rows;
 		const int nb = cols / 32;
 		// As few K splits as the LDS copy of X^T allows (one for a single
 		// vector at every nnc shape), the splits equal in size.
 		int max_blocks = 1;
-		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= kGemvBatchLds) ++max_blocks;
+		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= gemv_batch_lds(format)) ++max_blocks;
 		n_split = (nb + max_blocks - 1) / max_blocks;
 		split_blocks = (nb + n_split - 1) / n_split;
 	}

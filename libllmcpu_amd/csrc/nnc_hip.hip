@@ -931,7 +931,7 @@ namespace
 			p.format = format;
 			stack_rows(p, rows, n_mat);
 			int n_split = 1, split_blocks = 1;
-			nnchip::gemv_plan(p.rows, static_cast<int>(cols), nb, n_split, split_blocks);
+			nnchip::gemv_plan(p.rows, static_cast<int>(cols), nb, format, n_split, split_blocks);
 			if (n_split > 1)
 				if (nnc_status s = reserve(kv, kv->gemv_part,
 				                           static_cast<size_t>(n_split) * nb * static_cast<size_t>(p.rows) * sizeof(float),
