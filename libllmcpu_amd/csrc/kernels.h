@@ -117,14 +117,15 @@ namespace nnchip
 	constexpr int kGemvMaxBatch = 16;
 	constexpr size_t kGemvLdsBudget = 64 << 10; // dynamic LDS per one-vector gemv work-group
 	// The batch kernel: weight rows per work-group (16 per wavefront) and its
-	// dynamic LDS budget per weight layout (two work-groups per CU), which sets
-	// the K splits. Measured against 64 rows and 64 KiB (a 16-vector Qwen3-4B
-	// layer, us): BF16 94.4 -> 91.6 (80 KiB; 98.0 at 64 KiB), Q8_0 114.2 ->
-	// 105.3, Q4_S 122.1 -> 104.8 (64 KiB; 110.6 at 80 KiB: the nibble kernel
-	// gains from the extra work-groups of more splits); the X^T staged per
-	// weight byte halves.
+	// dynamic LDS budget per weight layout (at most two work-groups per CU),
+	// which sets the K splits. Measured against 64 rows and 64 KiB (a 16-vector
+	// Qwen3-4B layer, us): BF16 94.4 -> 91.6 (80 KiB; 98.0 at 64, 93.3 at 96),
+	// Q8_0 114.2 -> 97.0 and Q4_S 122.1 -> 96.6 (48 KiB; at 32 / 40 / 56 / 64 /
+	// 80 KiB Q8_0 107.1 / 98.4 / 107.4 / 105.6 / 105.5, Q4_S 105.3 / 102.4 /
+	// 106.9 / 105.0 / 110.6: the quantised kernels, slower per byte, gain from
+	// the work-groups of more splits); the X^T staged per weight byte halves.
 	constexpr int kGemvRows = 128;
-	constexpr size_t gemv_batch_lds(int format) { return format == kGemvBf16 ? 80 << 10 : 64 << 10; }
+	constexpr size_t gemv_batch_lds(int format) { return format == kGemvBf16 ? 80 << 10 : 48 << 10; }
 
 	// LDS of a gemv work-group over `blocks` 32-column blocks and n_batch
 	// tokens: X^T hi and lo (bf16), the kGemvRows rows' scales and biases, and
