@@ -6,10 +6,10 @@
 // runtime.h:106-113) or F32. Q is updated in place, ready for the attention
 // call; the K/V inputs are left as they are.
 //
-// A work-group takes 16 head rows of one token, 4 per wavefront, all loaded at
-// once; a head's head_dim values are held 64 lanes wide (coalesced loads and
-// stores) and meet through the wavefront's LDS row. Every result has the
-// reference's bits:
+// A work-group takes 8 head rows of one token, 2 per wavefront, all loaded at
+// once (4 rows, one per wavefront, for up to 16 tokens); a head's head_dim
+// values are held 64 lanes wide (coalesced loads and stores) and meet through
+// the wavefront's LDS row. Every result has the reference's bits:
 //   RMSNorm  the sum of squares as the reference's AVX2 loop takes it: eight
 //            fp32 fused multiply-add chains over x[l], x[l + 8], ... (lanes
 //            0..7, from the LDS row), summed in hsum_ymm's order, the tail in
@@ -33,10 +33,11 @@ namespace nnchip
 		constexpr int kWaves = 4; // wavefronts per work-group
 		constexpr int kMaxHd = 512; // head_dim bound (the reference's RoPE table holds 256 pairs)
 
-		// Head rows per wavefront, loaded together (RPW): 4 for long batches
-		// (fewer, fuller work-groups), 1 for up to 16 tokens, where a row's
-		// exact-order norm chain is the latency and rows side by side in their
-		// own wavefronts finish sooner (one Qwen3-4B decode token: 6.9 -> 3.5 us).
+		// Head rows per wavefront, loaded together (RPW): 2 for long batches
+		// (a Qwen3-4B 512-token layer: 12.2 us at 4, 11.6 at 2, 11.9 at 1), 1 for
+		// up to 16 tokens, where a row's exact-order norm chain is the latency
+		// and rows side by side in their own wavefronts finish sooner (one
+		// Qwen3-4B decode token: 6.9 -> 3.5 us).
 
 		// Work-group (g, t): head rows 4 RPW g .. 4 RPW g + 4 RPW - 1 of token t, where rows
 		// 0 .. n_head - 1 are Q heads (updated in place), then n_kv K heads and
@@ -363,7 +364,7 @@ namespace nnchip
 		if (n_tok <= 16)
 			go(std::integral_constant<int, 1>{});
 		else
-			go(std::integral_constant<int, 4>{});
+			go(std::integral_constant<int, 2>{});
 		return true;
 	}
 }
