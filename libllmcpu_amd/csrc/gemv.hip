@@ -16,7 +16,7 @@
 // Grid: (row groups of kGemvRows = 128, K splits). A work-group of 8
 // wavefronts (two work-groups per CU) stages its K range of X^T (hi, lo, and
 // for Q4_S the block sums) in LDS once; each wavefront then streams the
-// weights of its own 16 rows block by block over the whole range, kAhead
+// weights of its own 16 rows block by block over the whole range, kAhead<F>
 // blocks of loads in flight. With one K split the rows go straight to Y; with
 // several, each split writes a partial and a second kernel adds the splits in
 // split order, so results are the same run to run.
@@ -29,7 +29,12 @@ namespace nnchip
 {
 	namespace
 	{
-		constexpr int kAhead = 8; // blocks of weights in flight per wavefront (batch kernel)
+		// Blocks of weights in flight per wavefront of the batch kernel, per
+		// layout (a 16-vector Qwen3-4B layer, us, at 8 / 4 / 3 / 2: BF16 91.6 /
+		// 87.5 / 87.6 / 89.6, Q8_0 97.6 / 88.9 / 89.5 / 85.7, Q4_S 96.5 / 90.2 /
+		// 90.3 / 87.7; 12 was slower still than 8).
+		template <int F>
+		constexpr int kAhead = F == kGemvBf16 ? 4 : 2;
 		constexpr int kVecAhead = 8; // 16-byte loads in flight per lane (one-vector kernel)
 
 		// The matrix holding stacked row `row` and the row's index in it (row
@@ -152,9 +157,9 @@ namespace nnchip
 			const int ra = mr.r + min(col, max(m_rows - 1, 0)); // this lane's A row in the matrix (clamped; not stored)
 			const int n_mine = m_rows > 0 ? nblk : 0; // blocks of this wavefront
 			auto my_block = [&](int i) { return b0 + min(i, max(n_mine - 1, 0)); };
-			a_block<F> ab[kAhead];
+			a_block<F> ab[kAhead<F>];
 #pragma unroll
-			for (int j = 0; j < kAhead; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
+			for (int j = 0; j < kAhead<F>; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
 
 			// X^T of the range, four columns per piece (consecutive threads read
 			// consecutive 16 bytes of a token's row), loads issued eight at a time.
@@ -238,17 +243,17 @@ namespace nnchip
 
 			f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc_b = {0.0f, 0.0f, 0.0f, 0.0f};
 			const bf16x8 zero8 = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
-			for (int i0 = 0; i0 < n_mine; i0 += kAhead)
+			for (int i0 = 0; i0 < n_mine; i0 += kAhead<F>)
 			{
 #pragma unroll
-				for (int j = 0; j < kAhead; ++j)
+				for (int j = 0; j < kAhead<F>; ++j)
 				{
 					const int i = i0 + j;
 					const int bl = my_block(i) - b0; // block within the range
 					const bf16x8 a = a_operand<F>(ab[j]);
 					// The next load into this slot, kAhead blocks on (clamped: a
 					// load is never under a branch).
-					ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(i + kAhead), nb_all - 1), grp);
+					ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(i + kAhead<F>), nb_all - 1), grp);
 					if (i < n_mine) // uniform
 					{
 						const size_t at = (static_cast<size_t>(bl) * nt + col) * 32 + 8 * grp;
