@@ -35,7 +35,11 @@ namespace nnchip
 		// 90.3 / 87.7; 12 was slower still than 8).
 		template <int F>
 		constexpr int kAhead = F == kGemvBf16 ? 4 : 2;
-		constexpr int kVecAhead = 8; // 16-byte loads in flight per lane (one-vector kernel)
+		// 16-byte loads in flight per lane of the one-vector kernel, per layout
+		// (a one-vector Qwen3-4B layer, us, at 8 / 6 / 4: BF16 55.7 / 56.1 /
+		// 59.2, Q8_0 48.7 / 48.9 / 48.4, Q4_S 51.5 / 50.9 / 48.4; 16 slower).
+		template <int F>
+		constexpr int kVecAhead = F == kGemvQ4S ? 4 : 8;
 
 		// The matrix holding stacked row `row` and the row's index in it (row
 		// uniform over the caller's rows: a row pair or a 16-row tile).
@@ -308,7 +312,7 @@ namespace nnchip
 		// One activation vector (the decode gemv) on the VALU: every load is 16
 		// contiguous bytes of a weight row (a wavefront reads 1 KB of one row
 		// per instruction), x sits in LDS, and each wavefront streams pairs of
-		// rows with kVecAhead loads in flight across row boundaries; a row's
+		// rows with kVecAhead<F> loads in flight across row boundaries; a row's
 		// lane sums meet through DPP and lane swaps.
 		template <int F>
 		struct vec_shape
@@ -486,14 +490,14 @@ namespace nnchip
 		{
 			static_assert(!ARGMAX || F == kGemvBf16, "argmax of a BF16 gemv only");
 			using V = vec_shape<F>;
-			constexpr int CPL = V::CPL, CW = V::CW, NA = kVecAhead;
+			constexpr int CPL = V::CPL, CW = V::CW, NA = kVecAhead<F>;
 			extern __shared__ __attribute__((aligned(16))) float s_x[]; // x, then (Q4_S) its block sums
 			// (wave uniform: every row index below, and the matrix lookup, stays scalar)
 			const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
 			// Items: for each of this wavefront's row pairs, chunk c of row 0,
 			// then of row 1, for every chunk c of CW columns. Two cursors walk
-			// them, the loads' (kVecAhead ahead) and the sums': (pair, item within
+			// them, the loads' (kVecAhead<F> ahead) and the sums': (pair, item within
 			// the pair), stepped by one item at a time (no division per item);
 			// a pair's matrix is looked up when the load cursor enters it.
 			const int nch = (p.cols + CW - 1) / CW;
