@@ -36,9 +36,12 @@
 //                      offset), so the scores come out already shifted.
 //                      Meanwhile V^T is read back transposed
 //                      (ds_read_b64_tr_b16) into registers;
-//   softmax            in fp32 and log2 units. The offset m is raised only
-//                      when a row's scores exceed it by more than 8, so
-//                      weights stay in (0, 256] and the O rescale is rare; the
+//   softmax            in fp32 and log2 units, weights exp2(s - m) with the
+//                      row's offset m set 8 below its largest score so far:
+//                      m is raised only when a score passes it by more than
+//                      15, so weights stay in (0, 2^15] (fp16's range) and the
+//                      O rescale is rare, and the row sum is at least 2^8, so
+//                      fp16's subnormal steps (2^-24) are negligible in it; the
 //                      two halves of a row's 32 scores meet through
 //                      v_permlane32_swap;
 //   O^T += V^T . P^T   P as the B operand straight from the score registers
@@ -66,7 +69,8 @@ namespace nnchip
 		constexpr int kKG = 4; // key groups: the key quarters of a step
 		constexpr int kWK = 32; // keys per wavefront per step (one MFMA tile)
 		constexpr int kStep = kKG * kWK; // keys per work-group step
-		constexpr float kLazy = 8.0f; // max growth of a row's scores over its offset, log2 units
+		constexpr float kBias = 8.0f; // a raised offset sits this far below the row's max (log2 units)
+		constexpr float kLazy = 15.0f; // max growth of a row's scores over its offset (weights up to 2^15)
 		constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3: raw 32-bit data
 
 		// A work-group is RG row groups of 32 rows times kKG key groups, one
@@ -461,7 +465,7 @@ namespace nnchip
 				if (__builtin_amdgcn_ballot_w64(grow) != 0) // uniform
 				{
 					const bool fresh = m_off == -INFINITY;
-					const float d = grow ? mx : 0.0f;
+					const float d = grow ? mx - kBias : 0.0f;
 					const float alpha = fresh ? 0.0f : fast_exp2(-d); // 1 when the row does not grow
 					if (grow) m_off = (fresh ? 0.0f : m_off) + d;
 					const float ci = m_off == -INFINITY ? 0.0f : -m_off;

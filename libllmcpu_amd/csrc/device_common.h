@@ -166,17 +166,21 @@ namespace nnchip
 
 	// The fp16 copy of a BF16 V element kept for the prefill kernel (RNE;
 	// exact for every bf16 from 2^-14 up to fp16's range, within 2^-25 below).
-	// The prefill kernel multiplies it by P rounded to fp16, whose error in an
-	// output is up to 2^-11 of the spread of the V values it weighs (measured
-	// with sharply peaked scores: about 1.2e-4 of max |V|). So only values up
-	// to kF16CopyMax in magnitude are kept; a larger (or non-finite) one is
-	// stored as kF16Bad, a NaN pattern that no conversion of a bf16 value
-	// produces (its lowest mantissa bit is set, where bf16's 7 mantissa bits
-	// fill only fp16's top 7), so the copy itself records which of its
-	// elements are unusable, and a buffer holding one runs the exact bf16
-	// path until such rows are overwritten.
+	// The prefill kernel multiplies it by P rounded to fp16 (relative error at
+	// most u = 2^-11 per weight) and takes the row sum from the same rounded
+	// weights, so an output is a weighted mean of V whose weights moved by a
+	// factor (1 + e_k), |e_k| <= u. Its error is sum_k w_k e_k (V_k - out),
+	// at most u times the mean absolute deviation of V about the output,
+	// which is at most half the range of V: u * max |V|. The BF16 tolerance
+	// is 5e-3; kF16CopyMax = 8 bounds this term by 2^-8 = 3.9e-3 and leaves
+	// the rest for the near-fp32 scores and the fp32 sums. A larger (or
+	// non-finite) value is stored as kF16Bad, a NaN pattern that no
+	// conversion of a bf16 value produces (its lowest mantissa bit is set,
+	// where bf16's 7 mantissa bits fill only fp16's top 7), so the copy
+	// itself records which of its elements are unusable, and a buffer
+	// holding one runs the exact bf16 path until such rows are overwritten.
 	constexpr uint16_t kF16Bad = 0x7e01;
-	constexpr float kF16CopyMax = 32.0f;
+	constexpr float kF16CopyMax = 8.0f;
 
 	__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint32_t b)
 	{

@@ -156,10 +156,10 @@ def test_prefill_odd_batches(orc):
 
 def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
     """BF16 caches keep an fp16 copy of V for the prefill kernel (P in fp16,
-    one MFMA per P . V product) holding values up to 32 in magnitude. A V
-    value beyond that (40, or 1e5 past fp16's range) sends the prefill through
+    one MFMA per P . V product) holding values up to 8 in magnitude. A V
+    value beyond that (10, or 1e5 past fp16's range) sends the prefill through
     the bf16 path (P as bf16 hi + lo against the exact bf16 V), bit for bit
-    what a cache without the copy (NNC_HIP_F16_SHADOW=0) gives; a value of 30
+    what a cache without the copies (NNC_HIP_F16_SHADOW=0) gives; a value of 6
     keeps the fp16 path. K is read as bf16 with Q as hi + lo on both paths, so
     large K or Q values need no fallback. Every variant stays within the BF16
     bound of the oracle, and within 5e-3 * (1 + |ref|) where a V of 1e5 makes
@@ -194,7 +194,7 @@ def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
 
     base, plain = bits(K, V, "fp16 shadow")
     assert not np.array_equal(base, plain)  # the two paths round differently
-    for val, copy_used in ((30.0, True), (40.0, False)):  # the copy's limit is 32
+    for val, copy_used in ((6.0, True), (10.0, False)):  # the copy's limit is 8
         V3 = V.copy()
         V3[200, 9] = nh.bf16_round(np.array([val], np.float32))[0]
         a, b = bits(K, V3, f"cache V value {val:g}")

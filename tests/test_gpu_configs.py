@@ -165,17 +165,19 @@ def test_peaked_scores(orc, n_tok):
     assert d.max() <= cfg.tol
 
 
-@pytest.mark.parametrize("n_tok,v_mul", ((1, 100.0), (16, 100.0), (200, 100.0), (200, 5.0)))
+@pytest.mark.parametrize("n_tok,v_mul", ((1, 100.0), (16, 100.0), (200, 100.0), (200, 1.4)))
 def test_large_values(orc, n_tok, v_mul):
     """V scaled up and Q by 6 (peaked weights, scores up to ~90 in log2 units).
     With V x100 (|V| up to about 550) outputs reach a few hundred; there a
     score's own fp32 rounding moves a weight by ~1e-5 and an output by ~1e-3
-    in any fp32 implementation, the reference's included, so the bound is the
-    relative one, 5e-3 (1 + |ref|) per element, for decode and a session
-    batch (split-K kernels, P as bf16 hi + lo) and for the prefill kernel
-    (values beyond 32 keep it off V's fp16 copy, so it also takes P as bf16
-    hi + lo). With V x5 (|V| below 32) the prefill kernel reads the fp16 copy
-    with P rounded to fp16, whose error grows with |V|: both bounds hold."""
+    in any fp32 implementation, the reference's included, so the bound is
+    relative to 1 + |ref| per element: 2.5e-3 for decode and a session batch
+    (split-K kernels, every product near-fp32; measured 9.8e-4, while P
+    rounded to bf16 alone would give about 8e-3), 5e-3 for the prefill kernel
+    (values beyond 8 keep it off V's fp16 copy, so it takes P as bf16 hi +
+    lo). With V x1.4 (|V| below 8) the prefill kernel reads the fp16 copy
+    with P rounded to fp16, whose error grows with |V|: both of its bounds
+    hold."""
     cfg = synth.CONFIGS["D"]
     n_seq = 8192
     K, V = synth.cache_buffer(cfg, 2, n_seq, n_seq)
@@ -191,8 +193,9 @@ def test_large_values(orc, n_tok, v_mul):
     d = np.abs(got.astype(np.float64) - want)
     say(f"  max-abs {d.max():.3e}; max of d / (1 + |ref|) {(d / (1 + np.abs(want))).max():.3e}; "
         f"max |ref| {np.abs(want).max():.1f}")
-    assert np.all(d <= cfg.tol * (1.0 + np.abs(want)))
-    if v_mul < 32.0 / 6.0:
+    rel = 2.5e-3 if n_tok <= 16 else cfg.tol
+    assert np.all(d <= rel * (1.0 + np.abs(want)))
+    if np.abs(nh.bf16_to_f32(V)).max() <= 8.0:
         assert d.max() <= cfg.tol
 
 
