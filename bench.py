@@ -15,13 +15,17 @@ prefill TFLOP/s (4 * head_dim * n_head * sum of span lengths) rides in
 `prefill`. `roofline` is the decode kernel's (HBM bound),
 `prefill.roofline` the prefill kernel's (MFMA bound, dense fp16/bf16 peak),
 both from HIP events on the op's stream; their `traffic` comes from the
-counter summaries in profiles/. Beside them: a 16-token session batch, the
-pre-attention step, the weight gemvs, one decode layer through the
-host-buffer entry point, the other benchmark configurations (A, B, C, D at
-4096 keys, E; each step replayed from a HIP graph) and `cpu_baseline`, nnc's
-own CPU attention (oracle/_ref: the reference's kernels and worker pool) on a
-bounded sample of the same workload on this host at the reference's two
-thread settings.
+counter summaries in profiles/. Beside them: chunk 7 of the prompt in exact
+mode (every token with its one-token bits) against the prefill kernel, a
+16-token session batch, the pre-attention step, the weight gemvs, one decode
+layer through the host-buffer entry point (C-side cost beside the device
+form), the other benchmark configurations (A, B, C, D at 4096 keys, E; each
+step replayed from a HIP graph) and `cpu_baseline`, nnc's own CPU attention
+(oracle/_ref: the reference's kernels and worker pool) on bounded samples of
+the same work on this host (decode at the reference's two thread settings,
+a prefill chunk, B at 16384 keys, C's decode step), whose leg also gives the
+`parity` block: max-abs and max-rel (|d| / (1 + |ref|)) of the timed GPU
+outputs against the reference on the same inputs.
 """
 from __future__ import annotations
 
@@ -94,52 +98,112 @@ def cpu_model() -> str:
     return f"{name} ({extra}{'; ' + ' '.join(tags) if tags else ''})" if extra else name
 
 
-def cpu_baseline(kv, target_s: float) -> dict:
-    """nnc's CPU attention on this host: one Qwen3-4B layer at 32768 keys,
-    repeated for about target_s seconds per setting, at the reference's two
-    thread settings: min(8, nproc) (its default, reference nn_ops.cpp:865-879)
-    and nproc capped at 64 (nn_ops.cpp:786), the latter also held to the
-    CPUs this process may use. The first is the reported value."""
+def parity_of(got: np.ndarray, ref: np.ndarray) -> dict:
+    """max-abs and max-rel, rel = |d| / (1 + |ref|), of the GPU output against the reference's."""
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    return {"max_abs": float(d.max()), "max_rel": float((d / (1.0 + np.abs(ref))).max())}
+
+
+def cpu_baseline(cache_l0, target_s: float, samples: dict) -> dict:
+    """nnc's CPU attention on this host (oracle/_ref: the reference's own
+    kernels and worker pool, or the oracle's port where it was not built),
+    on bounded samples of the benchmark's work, and the parity of the timed
+    GPU outputs against it on the same inputs.
+
+    Decode: one Qwen3-4B layer at 32768 keys (layer 0 of the timed step: its
+    q and the GPU's output), repeated for about target_s seconds per setting,
+    at the reference's two thread settings: min(8, nproc) (its default,
+    reference nn_ops.cpp:865-879) and nproc capped at 64 (nn_ops.cpp:786),
+    the latter also held to the CPUs this process may use. The first is the
+    reported value. Prefill: chunk 7 of layer 0 (512 tokens at keys 0 ..
+    4095), the GPU's output of the same call. B decode at 16384 keys and C's
+    26-layer decode step at 8192 (22 windowed local layers, 4 global), on
+    synthetic rows of their shapes, at the default setting."""
     import oracle
 
-    K, V = kv.read(0, 0, CTX)
-    rng = np.random.default_rng(0)
-    q = rng.standard_normal((1, N_HEAD * HD)).astype(np.float32)
-    q /= np.sqrt((q.reshape(N_HEAD, HD) ** 2).mean(axis=1)).repeat(HD)[None, :]
+    K, V = cache_l0
     nproc = os.cpu_count() or 1
     usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
-    kw = dict(kv_bf16=True, rows=CTX, pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
     ref = oracle.reference_available()
     lib = oracle.Reference() if ref else oracle.Oracle()
     kind = "reference" if ref else "port"
 
-    def timed_run(threads):
+    def attend(threads, q, Kb, Vb, **kw):
         if ref:
             lib.set_threads(threads)
-            run = lambda: lib.attend_layer(q, K, V, **kw)  # noqa: E731
-        else:
-            run = lambda: lib.attend_layer(q, K, V, threads=threads, **kw)  # noqa: E731
-        run()
-        n, t0 = 0, time.perf_counter()
-        best = float("inf")
-        while time.perf_counter() - t0 < target_s:
+            return lib.attend_layer(q, Kb, Vb, **kw)
+        return lib.attend_layer(q, Kb, Vb, threads=threads, **kw)
+
+    def best_of(threads, seconds, q, Kb, Vb, **kw):
+        out = attend(threads, q, Kb, Vb, **kw)
+        n, t0, best = 0, time.perf_counter(), float("inf")
+        while n < 2 or time.perf_counter() - t0 < seconds:
             t = time.perf_counter()
-            run()
+            attend(threads, q, Kb, Vb, **kw)
             best = min(best, time.perf_counter() - t)
             n += 1
-        return decode_bytes(CTX) / best / 1e9, n
+        return out, best, n
 
     t_default = min(8, nproc)
     t_all = min(64, nproc, usable, BOX_CPU_SHARE)
-    gbs, n = timed_run(t_default)
-    gbs_all, n_all = timed_run(t_all)
+    dec = dict(kv_bf16=True, rows=CTX, pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+    q0 = samples["decode_q"]
+    ref_dec, best, n = best_of(t_default, target_s, q0, K, V, **dec)
+    _, best_all, n_all = best_of(t_all, target_s, q0, K, V, **dec)
+    gbs, gbs_all = decode_bytes(CTX) / best / 1e9, decode_bytes(CTX) / best_all / 1e9
+
+    # prefill: chunk 7 of layer 0
+    c0 = (PROMPT // CHUNK - 1) * CHUNK
+    pre = dict(kv_bf16=True, rows=PROMPT, pos0=c0, n_seq=c0 + CHUNK, n_head=N_HEAD, n_kv=N_KV, head_dim=HD,
+               scale=SCALE)
+    ref_pre, best_pre, n_pre = best_of(t_default, 2.0, samples["prefill_q"], K[:PROMPT], V[:PROMPT], **pre)
+    pre_tflops = prefill_flops(c0, CHUNK) / best_pre / 1e12
+
+    # B decode at 16384 keys and C's decode step, on synthetic rows of their shapes
+    from libllmcpu_amd import synth
+    rng = np.random.default_rng(5)
+
+    def decode_layer_s(cfg, rows, window, span_keys):
+        Kb = nh_bf16(rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32))
+        Vb = nh_bf16(rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32))
+        q = rng.standard_normal((1, cfg.n_head * cfg.head_dim)).astype(np.float32)
+        kw = dict(kv_bf16=True, rows=rows, pos0=span_keys - 1, n_seq=span_keys, window=window, n_head=cfg.n_head,
+                  n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+        return best_of(t_default, 1.0, q, Kb, Vb, **kw)[1]
+
+    B, Cc = synth.CONFIGS["B"], synth.CONFIGS["C"]
+    b_s = decode_layer_s(B, 16384, 0, 16384)
+    b_bytes = decode_layer_bytes(16384, B.n_kv, B.head_dim, B.n_head, 2)
+    n_local = sum(1 for li in range(Cc.n_layer) if Cc.layer_window(li) > 0)
+    c_local = decode_layer_s(Cc, Cc.layer_rows(0, 8192, 2048), Cc.window, 8192)
+    c_global = decode_layer_s(Cc, 8192, 0, 8192)
+    c_step = n_local * c_local + (Cc.n_layer - n_local) * c_global
+    c_bytes = sum(decode_layer_bytes(int(layer_spans(Cc, li, 8191, 1)[0]), Cc.n_kv, Cc.head_dim, Cc.n_head, 2)
+                  for li in range(Cc.n_layer))
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": t_default, "kind": kind,
-            "sample": f"decode of one Qwen3-4B layer at {CTX} keys, best of {n} runs over {target_s:.0f} s "
-                      f"(the reference's kernels and worker pool)",
+            "sample": f"decode of one Qwen3-4B layer at {CTX} keys (layer 0 of the timed step), best of {n} runs "
+                      f"over {target_s:.0f} s (the reference's kernels and worker pool)",
             "cpu": cpu_model(), "nproc": nproc, "usable_cpus": usable,
             "all_cores": {"value": round(gbs_all, 2), "cores": t_all, "runs": n_all,
                           "threads_rule": f"min(64, nproc) held to the usable CPUs and the box's "
-                                          f"{BOX_CPU_SHARE}-CPU share per GPU"}}
+                                          f"{BOX_CPU_SHARE}-CPU share per GPU"},
+            "prefill": {"value": round(pre_tflops, 4), "unit": "TFLOP/s", "cores": t_default, "runs": n_pre,
+                        "sample": f"chunk 7 of layer 0 (512 tokens at keys 0 .. 4095), {best_pre * 1e3:.1f} ms"},
+            "B_decode_16384": {"value": round(b_bytes / b_s / 1e9, 2), "unit": "GB/s", "cores": t_default,
+                               "sample": "one Llama-3.2-1B layer at 16384 keys, synthetic rows"},
+            "C_decode_8192": {"value": round(c_bytes / c_step / 1e9, 2), "unit": "GB/s", "cores": t_default,
+                              "ms_per_step": round(c_step * 1e3, 3),
+                              "sample": f"{n_local} local (window {Cc.window}) and {Cc.n_layer - n_local} global "
+                                        f"Gemma-3-1B layers at 8192, synthetic rows"},
+            "parity": {"against": kind, "rel": "|d| / (1 + |ref|)",
+                       "decode_layer0_32768": parity_of(samples["decode_out"], ref_dec),
+                       "prefill_layer0_chunk7": parity_of(samples["prefill_out"], ref_pre),
+                       "bound": 5e-3}}
+
+
+def nh_bf16(x: np.ndarray) -> np.ndarray:
+    from libllmcpu_amd import bf16_round
+    return bf16_round(x)
 
 
 def pmc_summary(fetch_csv: str, write_csv: str, kind: str = "decode") -> dict:
@@ -418,13 +482,15 @@ def configs_bench(nh, hip_rt, synth) -> dict:
                       "replay_equals_eager": same}
         log(f"[bench] {label}: {ms:.3f} ms/step, {tf:.0f} TFLOP/s")
 
-    A, B, Cc, E = (synth.CONFIGS[k] for k in "ABCE")
+    A, B, Cc, D, E = (synth.CONFIGS[k] for k in "ABCDE")
     kv = build(A, 1024, 1)
     decode_entry(A, "A_decode_1024", kv, 1024, reps=50)
     out["A_decode_1024"]["note"] = "18 x 2 MB of K/V stay in the 256 MB Infinity Cache: not an HBM rate"
     kv = build(B, 16384, 1)
     for ctx in (512, 4096, 16384):
         decode_entry(B, f"B_decode_{ctx}", kv, ctx)
+    kv = build(D, 4096, 1)
+    decode_entry(D, "D_decode_4096", kv, 4096)
     kv = build(Cc, 8192, 2048)
     decode_entry(Cc, "C_decode_8192", kv, 8192)
     prefill_entry(Cc, "C_prefill_8192", kv, 8192, 2048)
@@ -448,25 +514,53 @@ def configs_bench(nh, hip_rt, synth) -> dict:
     return out
 
 
-def host_path_bench(nh, kv) -> dict:
+def host_path_bench(nh, kv, q_dev: int, o_dev: int) -> dict:
     """One decode layer through nnc_hip_attend (q and out in host memory, the
     call synchronous), as a drop-in caller at reference model.cpp:1693-1757
-    would make it; wall time per call, ctypes overhead included."""
+    would make it, beside the device form made synchronous
+    (nnc_hip_attend_device + nnc_hip_kv_sync). Both through raw ctypes calls;
+    the C-side cost per call is the wall time less the cost of a ctypes call
+    that returns at once (nnc_hip_kv_bytes), measured the same way."""
+    import ctypes as C
+
+    lib = nh.load_library()
     rng = np.random.default_rng(3)
     q = rng.standard_normal((1, N_HEAD * HD)).astype(np.float32)
-    kw = dict(pos0=CTX - 1, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
-    for li in range(N_LAYER):
-        kv.attend(li, q, **kw)
-    n = 0
-    t0 = time.perf_counter()
-    for _ in range(5):
+    out = np.empty_like(q)
+    qp, op, h = C.c_void_p(q.ctypes.data), C.c_void_p(out.ctypes.data), kv.handle
+    args = (1, CTX - 1, CTX, 0, True, N_HEAD, N_KV, HD, SCALE)
+    reps = 5
+
+    def per_call(fn):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) * 1e6 / (reps * N_LAYER)
+
+    def host():
         for li in range(N_LAYER):
-            kv.attend(li, q, **kw)
-            n += 1
-    us = (time.perf_counter() - t0) * 1e6 / n
-    return {"what": "one Qwen3-4B decode layer at 32768 keys through nnc_hip_attend: q staged through pinned "
-                    "memory, out copied back, the call synchronous (Python ctypes call included)",
-            "us_per_call": round(us, 2), "gbs": round(decode_bytes(CTX) / (us * 1e-6) / 1e9, 1)}
+            lib.nnc_hip_attend(h, li, qp, op, *args)
+
+    def device():
+        for li in range(N_LAYER):
+            lib.nnc_hip_attend_device(h, li, C.c_void_p(q_dev + li * N_HEAD * HD * 4),
+                                      C.c_void_p(o_dev + li * N_HEAD * HD * 4), *args)
+            lib.nnc_hip_kv_sync(h)
+
+    def floor():
+        for _ in range(N_LAYER):
+            lib.nnc_hip_kv_bytes(h)
+
+    host_us, dev_us, floor_us = per_call(host), per_call(device), per_call(floor)
+    c_host, c_dev = host_us - floor_us, dev_us - 2 * floor_us
+    return {"what": "one Qwen3-4B decode layer at 32768 keys through nnc_hip_attend: q copied into pinned memory "
+                    "and read by a copy kernel, out written by the kernels into pinned memory, the call "
+                    "synchronous; beside nnc_hip_attend_device + nnc_hip_kv_sync on the same layers",
+            "us_per_call": round(host_us, 2), "c_side_us": round(c_host, 2),
+            "device_form_c_side_us": round(c_dev, 2), "ratio_to_device_form": round(c_host / c_dev, 3),
+            "ctypes_call_us": round(floor_us, 3),
+            "gbs": round(decode_bytes(CTX) / (c_host * 1e-6) / 1e9, 1)}
 
 
 def main() -> int:
@@ -477,7 +571,7 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations (A, B, C, E)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations (A, B, C, D at 4096, E)")
     ap.add_argument("--only", choices=["decode", "prefill", "batch", "prep", "gemv", "configs"], default=None,
                     help="time one mode only (profiling runs); the JSON line needs both")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_traffic.json"),
@@ -667,6 +761,48 @@ def main() -> int:
     pre_launch_us = pre_ms * 1e3 / (args.prefill_steps * pre_launches)
     pre_launch_tflops = (pre_flops / pre_launches) / (pre_launch_us * 1e-6) / 1e12
 
+    # nnc's "same bits whatever batch" (exact mode: every token on the split-K
+    # kernel, bit-identical to its one-token call) for chunk 7 of every layer,
+    # beside the prefill kernel on the same chunk.
+    c7 = PROMPT // CHUNK - 1
+
+    def chunk_step():
+        for li in range(N_LAYER):
+            qb = q_pre + li * PROMPT * N_HEAD * HD * 4
+            kv.attend_device(li, qb + c7 * CHUNK * N_HEAD * HD * 4, o_pre + c7 * CHUNK * N_HEAD * HD * 4,
+                             n_tok=CHUNK, pos0=c7 * CHUNK, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+
+    log("[bench] chunk 7: prefill kernel, then exact mode")
+    chunk_step()
+    hip_rt.sync()
+    fast_ms, _ = timed(chunk_step, 3)
+    lib.nnc_hip_kv_set_exact_batches(kv.handle, True)
+    chunk_step()
+    hip_rt.sync()
+    exact_ms, _ = timed(chunk_step, 3)
+    lib.nnc_hip_kv_set_exact_batches(kv.handle, False)
+    exact_res = {"what": f"chunk {c7} of the {PROMPT}-token prompt ({CHUNK} tokens at keys 0 .. {PROMPT - 1}) "
+                         "through every layer: the prefill kernel, and exact mode (nnc_hip_kv_set_exact_batches: "
+                         "every token on the split-K kernel with its one-token bits)",
+                 "prefill_kernel_us_per_layer": round(fast_ms * 1e3 / (3 * N_LAYER), 2),
+                 "exact_us_per_layer": round(exact_ms * 1e3 / (3 * N_LAYER), 2),
+                 "exact_over_prefill": round(exact_ms / fast_ms, 2),
+                 "exact_tflops": round(prefill_flops(c7 * CHUNK, CHUNK) * 3 * N_LAYER / (exact_ms * 1e-3) / 1e12, 1)}
+    log(f"[bench] exact mode {json.dumps(exact_res)}")
+
+    # Parity samples, taken before the pre-attention benchmark rewrites q and
+    # cache rows: layer 0's q and output of the timed decode step, and chunk 7
+    # of layer 0 through the prefill kernel.
+    width = N_HEAD * HD
+    kv.attend_device(0, q_pre + c7 * CHUNK * width * 4, o_pre + c7 * CHUNK * width * 4, n_tok=CHUNK,
+                     pos0=c7 * CHUNK, n_head=N_HEAD, n_kv=N_KV, head_dim=HD, scale=SCALE)
+    kv.sync()
+    samples = {"decode_q": hip_rt.to_host(np.empty((1, width), np.float32), q_dec),
+               "decode_out": hip_rt.to_host(np.empty((1, width), np.float32), o_dec),
+               "prefill_q": hip_rt.to_host(np.empty((CHUNK, width), np.float32), q_pre + c7 * CHUNK * width * 4),
+               "prefill_out": hip_rt.to_host(np.empty((CHUNK, width), np.float32), o_pre + c7 * CHUNK * width * 4)}
+    cache_l0 = kv.read(0, 0, CTX)
+
     log("[bench] session batch")
     batch_step()
     hip_rt.sync()
@@ -694,13 +830,13 @@ def main() -> int:
     pre_traffic = traffic_of(args.prefill_traffic)
 
     log("[bench] host-buffer decode path")
-    host_res = host_path_bench(nh, kv)
+    host_res = host_path_bench(nh, kv, q_dec, o_dec)
     log(f"[bench] host path {host_res['us_per_call']} us/call")
 
     cpu = None
     if not args.no_cpu:
         log(f"[bench] cpu baseline ~{args.cpu_seconds:.0f} s per setting")
-        cpu = cpu_baseline(kv, args.cpu_seconds)
+        cpu = cpu_baseline(cache_l0, args.cpu_seconds, samples)
 
     configs = None
     if not args.no_configs:
@@ -753,6 +889,8 @@ def main() -> int:
                               "kernel": "prep_kernel (512-token chunk)"}},
         "gemv": gemv_res,
         "host_path": host_res,
+        "exact_mode": exact_res,
+        "parity": cpu["parity"] if cpu else None,
         "configs": configs,
         "cpu_baseline": cpu,
         "device": {"cu": n_cu, "clock_mhz": clock_mhz},

@@ -58,6 +58,25 @@ typedef enum nnc_status
 } nnc_status;
 #endif
 
+/* Log levels, the values of nnc_log_level (reference nnc.h:83-89). */
+#define NNC_HIP_LOG_DEBUG 0
+#define NNC_HIP_LOG_INFO 1
+#define NNC_HIP_LOG_WARN 2
+#define NNC_HIP_LOG_ERROR 3
+
+/* Receives one complete message without a trailing newline; the signature
+ * of nnc_log_callback (reference nnc.h:91-92), so nnc's own callback can be
+ * passed straight through. */
+typedef void (*nnc_hip_log_callback)(int level, const char* message, void* user);
+
+/* Routes the bridge's diagnostics to `callback`; NULL restores the default,
+ * which writes warnings and errors to stderr (reference nnc.h:94-98,
+ * nnc_set_log_callback). Failures are still reported through return values
+ * and nnc_hip_last_error(). nnc_hip_kv_create logs, at INFO, the device and
+ * the device memory the cache holds (the counterpart of nnc's context line,
+ * reference session.cpp:341-343). */
+void nnc_hip_set_log_callback(nnc_hip_log_callback callback, void* user);
+
 /* A session's K/V cache in device memory: one buffer per cache-owning layer,
  * as in model_kv_cache::bufs (reference model.h:252-326). */
 typedef struct nnc_hip_kv nnc_hip_kv;
@@ -216,10 +235,15 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
  * (no hipMalloc, hipFree or allocating library routine): the decode kernels'
  * partials go to a fixed array of NNC_HIP_NOALLOC_SCRATCH_BYTES in each
  * device's memory, which the library holds until the process ends. Every
- * call on a GPU shares that GPU's array, so calls that overlap on one GPU
- * (caches driven from different threads at once) race on it; calls on one
- * cache are ordered on its stream and do not. The first call on a device
- * looks up the array's device address (no allocation).
+ * call on a GPU shares that GPU's array, and the calls are asynchronous: two
+ * no-alloc calls on different caches of one GPU (each cache has its own
+ * stream) overlap on the GPU and race on the array, even when one thread
+ * issues them one after the other, so the caller must order them (wait for
+ * the first, or make the second cache's stream wait on it); calls on one
+ * cache are ordered on its stream and do not race. The array's device
+ * address is looked up when the first cache on a device is created, so the
+ * call itself loads nothing. Every launch of a call is planned before the
+ * first is enqueued, so a refused call changes nothing.
  * NNC_ERR_INVALID_ARGUMENT: as nnc_hip_attend_device, and when the call's
  * partials would exceed the array (the message gives both sizes); one
  * decode token of Qwen3-4B at 32k context needs about 1 MiB, a 16-token

@@ -16,4 +16,5 @@ from .nnc_hip import (  # noqa: F401
     kv_rows,
     load_library,
     max_rewind,
+    set_log_callback,
 )

@@ -194,6 +194,10 @@ namespace nnchip
 
 	bool launch_zero(float* dst, size_t n, hipStream_t stream);
 
+	// n floats from src (device memory or pinned host memory, 16-byte
+	// aligned) to dst (device memory), on the stream.
+	bool launch_copy(float* dst, const float* src, size_t n, hipStream_t stream);
+
 	// The span of keys position `pos` attends to (reference model.cpp:2300-2316).
 	__host__ __device__ inline void attn_span(int causal, int window, int pos, int n_seq, int& first, int& last)
 	{

@@ -136,6 +136,17 @@ namespace nnchip
 			}
 		}
 
+		// dst[i] = src[i]; src may be pinned host memory (read once, over the
+		// bus), dst device memory.
+		__global__ void copy_kernel(float* dst, const float* src, size_t n)
+		{
+			const size_t n4 = n / 4;
+			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n4;
+			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
+				reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(src)[i];
+			if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) dst[4 * n4 + threadIdx.x] = src[4 * n4 + threadIdx.x];
+		}
+
 		__global__ void zero_kernel(float* dst, size_t n)
 		{
 			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
@@ -183,6 +194,12 @@ namespace nnchip
 		shadow_rows_kernel<<<grid_for(n, 256), 256, 0, stream>>>(static_cast<const uint16_t*>(V),
 		                                                         static_cast<uint16_t*>(V16), n_bad, rows, kv_dim,
 		                                                         pos0, n_tok);
+		return true;
+	}
+
+	bool launch_copy(float* dst, const float* src, size_t n, hipStream_t stream)
+	{
+		copy_kernel<<<grid_for((n + 3) / 4, 256), 256, 0, stream>>>(dst, src, n);
 		return true;
 	}
 

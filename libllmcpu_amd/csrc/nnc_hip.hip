@@ -34,6 +34,28 @@ namespace
 {
 	thread_local std::string g_last_error = "";
 
+	// The log callback (nnc's own, in a drop-in build) and its user pointer;
+	// none: warnings and errors go to stderr, as nnc's default does.
+	std::mutex g_log_mu;
+	nnc_hip_log_callback g_log_cb = nullptr;
+	void* g_log_user = nullptr;
+
+	void log_msg(int level, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+	void log_msg(int level, const char* fmt, ...)
+	{
+		char buf[512];
+		va_list ap;
+		va_start(ap, fmt);
+		std::vsnprintf(buf, sizeof buf, fmt, ap);
+		va_end(ap);
+		std::lock_guard<std::mutex> lock(g_log_mu);
+		if (g_log_cb)
+			g_log_cb(level, buf, g_log_user);
+		else if (level >= NNC_HIP_LOG_WARN)
+			std::fprintf(stderr, "nnc_hip: %s\n", buf);
+	}
+
 	nnc_status fail(nnc_status status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
 	nnc_status fail(nnc_status status, const char* fmt, ...)
@@ -93,10 +115,12 @@ namespace
 		size_t bytes = 0;
 	};
 
-	// Pinned host memory (hipHostMalloc) through which the host-buffer entry
-	// points move rows, so every copy is a DMA from page-locked memory and the
-	// caller's buffers are free on return. `free` is recorded after the last
-	// copy that reads the buffer; the host waits on it before writing again.
+	// Pinned host memory (hipHostMalloc, coherent) through which the
+	// host-buffer entry points move rows: appended rows and RoPE tables go to
+	// the device by DMA, q is read once by a copy kernel, and the kernels
+	// write out straight into it, so the caller's buffers are free on return.
+	// `free` is recorded after the last device access of the buffer; the host
+	// waits on it before writing again.
 	struct host_staging
 	{
 		void* ptr = nullptr;
@@ -158,8 +182,7 @@ struct nnc_hip_kv
 	std::vector<kv_buffer> bufs;
 	uint64_t bytes = 0;
 	dev_scratch part; // decode partials
-	dev_scratch q; // device copies of host q / gate / out and append rows
-	dev_scratch out;
+	dev_scratch q; // device copies of host q / gate and append rows
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
 	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now marked kF16Bad (device)
@@ -182,7 +205,7 @@ namespace
 				if (ptr) (void)hipFree(ptr);
 		}
 		if (kv->n_bad) (void)hipFree(kv->n_bad);
-		for (dev_scratch* s : {&kv->part, &kv->q, &kv->out, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v,
+		for (dev_scratch* s : {&kv->part, &kv->q, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v,
 		                       &kv->rope[0].dev, &kv->rope[1].dev})
 			if (s->ptr) (void)hipFree(s->ptr);
 		if (kv->pinned.ptr) (void)hipHostFree(kv->pinned.ptr);
@@ -217,7 +240,7 @@ namespace
 		h.ptr = nullptr;
 		h.bytes = 0;
 		const size_t n = (std::max<size_t>(bytes, 64 << 10) + 4095) & ~static_cast<size_t>(4095);
-		NNC_HIP_TRY(hipHostMalloc(&h.ptr, n, hipHostMallocDefault), what);
+		NNC_HIP_TRY(hipHostMalloc(&h.ptr, n, hipHostMallocCoherent), what);
 		h.bytes = n;
 		return NNC_OK;
 	}
@@ -353,35 +376,57 @@ namespace
 		return static_cast<int>(sk);
 	}
 
+	// One split-K launch: tokens t0 .. t0 + n - 1 of a call on the absolute
+	// split grid of sk keys.
+	struct decode_plan
+	{
+		int32_t t0, n;
+		int sk;
+	};
+
+	// The split grid of one launch over tokens pos0 .. pos0 + n_tok - 1:
+	// the first split's first key, the number of splits and the bytes of
+	// partials it writes (none for one split); n_split 0 when no token sees a
+	// key.
+	struct launch_geometry
+	{
+		int split_base = 0, n_split = 0;
+		size_t part_bytes = 0;
+	};
+
+	launch_geometry geometry_of(int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
+	                            int32_t n_kv, int32_t head_dim, int split_keys)
+	{
+		launch_geometry g;
+		int kmin, kmax, unused;
+		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, kmin, unused);
+		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, unused, kmax);
+		if (kmax < kmin) return g;
+		g.split_base = (kmin / split_keys) * split_keys;
+		g.n_split = kmax / split_keys - kmin / split_keys + 1;
+		if (g.n_split > 1)
+			g.part_bytes = static_cast<size_t>(n_tok) * n_kv * g.n_split * (n_head / n_kv) * (head_dim + 4) * sizeof(float);
+		return g;
+	}
+
 	// One split-K launch (and its merge) over tokens pos0 .. pos0 + n_tok - 1
-	// on the absolute split grid of split_keys keys.
+	// on the absolute split grid of split_keys keys. The partials go to
+	// src (already checked to hold them) or to the cache's scratch.
 	nnc_status decode_launch(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
 	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
 	                         int32_t head_dim, float scale, int split_keys, const part_source& src)
 	{
 		const int group = n_head / n_kv;
-		int kmin, kmax, unused;
-		nnchip::attn_span(causal ? 1 : 0, window, pos0, n_seq, kmin, unused);
-		nnchip::attn_span(causal ? 1 : 0, window, pos0 + n_tok - 1, n_seq, unused, kmax);
-		if (kmax < kmin)
+		const launch_geometry g = geometry_of(n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, split_keys);
+		if (g.n_split == 0)
 			return nnchip::launch_zero(out, static_cast<size_t>(n_tok) * n_head * head_dim, kv->stream) ? NNC_OK
 			                                                                                             : NNC_ERR_IO;
-		const int split_base = (kmin / split_keys) * split_keys;
-		const int n_split = kmax / split_keys - kmin / split_keys + 1;
-		if (n_split > nnchip::kDecodeMaxSplits)
-			return fail(NNC_ERR_IO, "decode split grid of %d splits (at most %d)", n_split, nnchip::kDecodeMaxSplits);
-		const size_t part_bytes = static_cast<size_t>(n_tok) * n_kv * n_split * group * (head_dim + 4) * sizeof(float);
+		if (g.n_split > nnchip::kDecodeMaxSplits)
+			return fail(NNC_ERR_IO, "decode split grid of %d splits (at most %d)", g.n_split, nnchip::kDecodeMaxSplits);
 		float* part = src.ptr;
-		if (part)
+		if (!part)
 		{
-			if (n_split > 1 && part_bytes > src.bytes) // (one split writes no partials)
-				return fail(NNC_ERR_INVALID_ARGUMENT,
-				            "%d tokens over %d splits need %zu bytes of decode partials; the fixed scratch holds %zu",
-				            n_tok, n_split, part_bytes, src.bytes);
-		}
-		else
-		{
-			if (nnc_status s = reserve(kv, kv->part, part_bytes, "decode scratch")) return s;
+			if (nnc_status s = reserve(kv, kv->part, g.part_bytes, "decode scratch")) return s;
 			part = static_cast<float*>(kv->part.ptr);
 		}
 
@@ -401,9 +446,9 @@ namespace
 		p.window = window;
 		p.causal = causal ? 1 : 0;
 		p.n_tok = n_tok;
-		p.split_base = split_base;
+		p.split_base = g.split_base;
 		p.split_keys = split_keys;
-		p.n_split = n_split;
+		p.n_split = g.n_split;
 		p.qscale = scale * 1.4426950408889634f;
 		if (!nnchip::launch_decode(p, n_tok, head_dim, group, kv->bf16, kv->stream))
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no decode kernel for head_dim %d, group %d", head_dim, group);
@@ -411,14 +456,13 @@ namespace
 		return NNC_OK;
 	}
 
-	// A session-sized batch: each token on the split grid a one-token call
-	// gives it (the split size of its own span over n_kv pairs). Consecutive
-	// tokens with the same split size share a launch; a token's result does
-	// not depend on the rest of its launch, so it matches the one-token call
-	// bit for bit.
-	nnc_status decode_tokens(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
-	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
-	                         int32_t head_dim, float scale, const part_source& src)
+	// The launches of a session-sized batch: each token on the split grid a
+	// one-token call gives it (the split size of its own span over the head
+	// groups). Consecutive tokens with the same split size share a launch; a
+	// token's result does not depend on the rest of its launch, so it
+	// matches the one-token call bit for bit.
+	void plan_tokens(const nnc_hip_kv* kv, int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+	                 int32_t n_kv, int32_t head_dim, std::vector<decode_plan>& plan)
 	{
 		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv);
 		const int groups = nnchip::decode_groups(n_kv, kv->bf16);
@@ -430,7 +474,6 @@ namespace
 			span_of(t, first, last);
 			return split_keys_for(kv, first, last, groups, wgk);
 		};
-		const size_t tok_floats = static_cast<size_t>(n_head) * head_dim;
 		for (int32_t t = 0; t < n_tok;)
 		{
 			const int sk = own_split(t);
@@ -443,13 +486,27 @@ namespace
 				span_of(u, fu, lu);
 				if (lu / sk - f0 / sk + 1 > nnchip::kDecodeMaxSplits) break; // the launch's split grid stays mergeable
 			}
-			if (nnc_status s = decode_launch(kv, b, q + t * tok_floats, out + t * tok_floats,
-			                                 gate ? gate + t * tok_floats : nullptr, u - t, pos0 + t, n_seq,
-			                                 window, causal, n_head, n_kv, head_dim, scale, sk, src))
-				return s;
+			plan.push_back({t, u - t, sk});
 			t = u;
 		}
-		return NNC_OK;
+	}
+
+	// The launches of an F32 batch of more than a session's tokens: chunks of
+	// at most kDecodeChunk tokens (a grid z-extent and a scratch size that
+	// stay small), each on the split grid of its own span.
+	void plan_f32_chunks(const nnc_hip_kv* kv, int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+	                     int32_t n_kv, int32_t head_dim, std::vector<decode_plan>& plan)
+	{
+		for (int32_t t0 = 0; t0 < n_tok; t0 += kDecodeChunk)
+		{
+			const int32_t nt = std::min(kDecodeChunk, n_tok - t0);
+			int kmin, kmax, unused;
+			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0, n_seq, kmin, unused);
+			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
+			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, kv->bf16),
+			                              nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv));
+			plan.push_back({t0, nt, sk});
+		}
 	}
 
 	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, const float* gate, int32_t n_tok, int32_t pos0,
@@ -471,11 +528,12 @@ namespace
 
 		// Decode and session-sized batches (and every batch in exact mode):
 		// the split-K kernel, each token on its own split grid. Larger
-		// batches: the prefill kernel for BF16, the split-K kernel over the
-		// batch's span for F32 (exact fp32 products against F32 K/V).
+		// batches: the prefill kernel for BF16, the split-K kernel over each
+		// chunk's span for F32 (exact fp32 products against F32 K/V).
+		std::vector<decode_plan> plan;
 		if (n_tok <= kSessionBatch || kv->exact_batches)
-			return decode_tokens(kv, b, q, out, gate, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale, src);
-		if (bf16)
+			plan_tokens(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, plan);
+		else if (bf16)
 		{
 			nnchip::prefill_params p{};
 			p.q = q;
@@ -500,20 +558,27 @@ namespace
 			NNC_HIP_TRY(hipGetLastError(), "prefill launch");
 			return NNC_OK;
 		}
+		else
+			plan_f32_chunks(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, plan);
 
-		// The split-K kernel, over chunks of at most kDecodeChunk tokens (a
-		// grid z-extent and a scratch size that stay small).
-		for (int32_t t0 = 0; t0 < n_tok; t0 += kDecodeChunk)
+		// Every launch is planned before the first is enqueued: a call whose
+		// partials do not fit the fixed scratch is refused whole.
+		if (src.ptr)
+			for (const decode_plan& d : plan)
+			{
+				const launch_geometry g =
+					geometry_of(d.n, pos0 + d.t0, n_seq, window, causal, n_head, n_kv, head_dim, d.sk);
+				if (g.part_bytes > src.bytes)
+					return fail(NNC_ERR_INVALID_ARGUMENT,
+					            "%d tokens over %d splits need %zu bytes of decode partials; the fixed scratch holds %zu",
+					            d.n, g.n_split, g.part_bytes, src.bytes);
+			}
+		const size_t tok_floats = static_cast<size_t>(n_head) * head_dim;
+		for (const decode_plan& d : plan)
 		{
-			const int32_t nt = std::min(kDecodeChunk, n_tok - t0);
-			const size_t off = static_cast<size_t>(t0) * n_head * head_dim;
-			int kmin, kmax, unused;
-			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0, n_seq, kmin, unused);
-			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
-			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, bf16),
-			                              nnchip::decode_wg_keys(head_dim, bf16, n_kv));
-			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, nt, pos0 + t0, n_seq, window, causal, n_head,
-			                                 n_kv, head_dim, scale, sk, src))
+			const size_t off = static_cast<size_t>(d.t0) * tok_floats;
+			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, d.n, pos0 + d.t0, n_seq,
+			                                 window, causal, n_head, n_kv, head_dim, scale, d.sk, src))
 				return s;
 		}
 		return NNC_OK;
@@ -553,6 +618,29 @@ namespace
 		(void)last0;
 		if (static_cast<long long>(n_seq) - first0 > b.rows)
 			return fail(NNC_ERR_CONTEXT_FULL, "keys %d .. %d do not fit a buffer of %d rows", first0, n_seq - 1, b.rows);
+		return NNC_OK;
+	}
+	// The device address of `scratch` on `device`: looked up once per device,
+	// with that device current, when the first cache on it is created (the
+	// library's set-up; a later no-alloc call only reads the table).
+	nnc_status noalloc_scratch(int device, void** out)
+	{
+		if (device < 0 || device >= kMaxDevices)
+			return fail(NNC_ERR_UNSUPPORTED_CPU, "device %d is past the library's %d-device table", device, kMaxDevices);
+		std::lock_guard<std::mutex> lock(g_scratch_mu);
+		if (!g_scratch_ptr[device])
+		{
+			int cur = 0;
+			NNC_HIP_TRY(hipGetDevice(&cur), "scratch lookup");
+			if (cur != device) NNC_HIP_TRY(hipSetDevice(device), "scratch lookup");
+			void* ptr = nullptr;
+			const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+			if (cur != device) (void)hipSetDevice(cur);
+			if (e != hipSuccess) return hip_fail(e, "scratch lookup");
+			if (!ptr) return fail(NNC_ERR_IO, "scratch lookup: no device address");
+			g_scratch_ptr[device] = ptr;
+		}
+		*out = g_scratch_ptr[device];
 		return NNC_OK;
 	}
 }
@@ -617,11 +705,26 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 	}
 	e = hipStreamSynchronize(kv->stream);
 	if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
+	void* fixed = nullptr;
+	if (nnc_status s = noalloc_scratch(kv->device, &fixed)) return bail(s);
+	// The counterpart of nnc's context line (reference session.cpp:341-343).
+	hipDeviceProp_t prop;
+	const bool named = hipGetDeviceProperties(&prop, kv->device) == hipSuccess;
+	log_msg(NNC_HIP_LOG_INFO, "device %d (%s, %d CUs): %d K/V buffers, %.1f MB of %s K/V%s in device memory",
+	        kv->device, named ? prop.name : "unknown", kv->n_cu, n_buf, static_cast<double>(kv->bytes) / 1e6,
+	        bf16 ? "BF16" : "F32", shadow ? " (with V's fp16 copy)" : "");
 	*out = kv;
 	return NNC_OK;
 }
 
 void nnc_hip_kv_free(nnc_hip_kv* kv) { release(kv); }
+
+void nnc_hip_set_log_callback(nnc_hip_log_callback callback, void* user)
+{
+	std::lock_guard<std::mutex> lock(g_log_mu);
+	g_log_cb = callback;
+	g_log_user = user;
+}
 
 uint64_t nnc_hip_kv_bytes(const nnc_hip_kv* kv) { return kv ? kv->bytes : 0; }
 
@@ -759,31 +862,33 @@ namespace
 		if (nnc_status s = check_attend(kv, buf, q ? aligned_probe : nullptr, out ? aligned_probe : nullptr, n_tok,
 		                                pos0, n_seq, window, causal, n_head, n_kv, head_dim))
 			return s;
-		const size_t bytes = static_cast<size_t>(n_tok) * n_head * head_dim * sizeof(float);
+		const size_t n = static_cast<size_t>(n_tok) * n_head * head_dim, bytes = n * sizeof(float);
+		const size_t slot = (bytes + 255) & ~static_cast<size_t>(255);
 		if (nnc_status s = reserve(kv, kv->q, bytes, "q staging")) return s;
-		if (nnc_status s = reserve(kv, kv->out, bytes, "out staging")) return s;
 		if (gate)
 			if (nnc_status s = reserve(kv, kv->gate, bytes, "gate staging")) return s;
-		// pinned: q, then gate; out comes back over q once the call is done
-		if (nnc_status s = reserve_pinned(kv, gate ? 2 * bytes : bytes, "q staging")) return s;
+		// pinned: q, gate, then out (written by the kernels themselves)
+		if (nnc_status s = reserve_pinned(kv, 3 * slot, "q staging")) return s;
 		char* pq = static_cast<char*>(kv->pinned.ptr);
+		float* pout = reinterpret_cast<float*>(pq + 2 * slot);
 		std::memcpy(pq, q, bytes);
-		NNC_HIP_TRY(hipMemcpyAsync(kv->q.ptr, pq, bytes, hipMemcpyHostToDevice, kv->stream), "q upload");
+		nnchip::launch_copy(static_cast<float*>(kv->q.ptr), reinterpret_cast<const float*>(pq), n, kv->stream);
 		if (gate)
 		{
-			std::memcpy(pq + bytes, gate, bytes);
-			NNC_HIP_TRY(hipMemcpyAsync(kv->gate.ptr, pq + bytes, bytes, hipMemcpyHostToDevice, kv->stream), "gate upload");
+			std::memcpy(pq + slot, gate, bytes);
+			nnchip::launch_copy(static_cast<float*>(kv->gate.ptr), reinterpret_cast<const float*>(pq + slot), n,
+			                    kv->stream);
 		}
-		if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), static_cast<float*>(kv->out.ptr),
+		NNC_HIP_TRY(hipGetLastError(), "q upload");
+		if (nnc_status s = attend_impl(kv, buf, static_cast<const float*>(kv->q.ptr), pout,
 		                               gate ? static_cast<const float*>(kv->gate.ptr) : nullptr, n_tok, pos0, n_seq,
 		                               window, causal, n_head, n_kv, head_dim, scale))
 		{
 			(void)hipStreamSynchronize(kv->stream); // the staging is read until the uploads finish
 			return s;
 		}
-		NNC_HIP_TRY(hipMemcpyAsync(pq, kv->out.ptr, bytes, hipMemcpyDeviceToHost, kv->stream), "out download");
 		NNC_HIP_TRY(hipStreamSynchronize(kv->stream), "attention");
-		std::memcpy(out, pq, bytes);
+		std::memcpy(out, pout, bytes);
 		return NNC_OK;
 	}
 }
@@ -804,32 +909,6 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
 	return attend_impl(kv, buf, q, out, nullptr, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim, scale);
 }
 
-namespace
-{
-	// The device address of `scratch` on the cache's device: looked up once
-	// per device, on its first no-alloc call, with that device current.
-	static nnc_status noalloc_scratch(const nnc_hip_kv* kv, void** out)
-	{
-		if (kv->device < 0 || kv->device >= kMaxDevices)
-			return fail(NNC_ERR_UNSUPPORTED_CPU, "device %d is past the library's %d-device table", kv->device, kMaxDevices);
-		std::lock_guard<std::mutex> lock(g_scratch_mu);
-		if (!g_scratch_ptr[kv->device])
-		{
-			int cur = 0;
-			NNC_HIP_TRY(hipGetDevice(&cur), "scratch lookup");
-			if (cur != kv->device) NNC_HIP_TRY(hipSetDevice(kv->device), "scratch lookup");
-			void* ptr = nullptr;
-			const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-			if (cur != kv->device) (void)hipSetDevice(cur);
-			if (e != hipSuccess) return hip_fail(e, "scratch lookup");
-			if (!ptr) return fail(NNC_ERR_IO, "scratch lookup: no device address");
-			g_scratch_ptr[kv->device] = ptr;
-		}
-		*out = g_scratch_ptr[kv->device];
-		return NNC_OK;
-	}
-}
-
 nnc_status nnc_hip_attend_device_noalloc(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok,
                                          int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
                                          int32_t n_kv, int32_t head_dim, float scale)
@@ -837,7 +916,7 @@ nnc_status nnc_hip_attend_device_noalloc(nnc_hip_kv* kv, int32_t buf, const floa
 	if (nnc_status s = check_attend(kv, buf, q, out, n_tok, pos0, n_seq, window, causal, n_head, n_kv, head_dim))
 		return s;
 	void* ptr = nullptr;
-	if (nnc_status s = noalloc_scratch(kv, &ptr)) return s;
+	if (nnc_status s = noalloc_scratch(kv->device, &ptr)) return s;
 	part_source src;
 	src.ptr = static_cast<float*>(ptr);
 	src.bytes = NNC_HIP_NOALLOC_SCRATCH_BYTES;

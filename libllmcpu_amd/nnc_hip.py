@@ -78,8 +78,12 @@ class NncHipPrep(C.Structure):
                 ("freq_factors", _P)]
 
 
+# nnc_hip_log_callback: (level, message, user)
+LOG_CALLBACK = C.CFUNCTYPE(None, C.c_int, C.c_char_p, C.c_void_p)
+
 # name: (restype, argtypes) for every function include/nnc_hip.h declares.
 SIGNATURES = {
+    "nnc_hip_set_log_callback": (None, [LOG_CALLBACK, _P]),
     "nnc_hip_kv_create": (C.c_int, [_I, C.POINTER(_I), C.POINTER(_I), _B, C.POINTER(_P)]),
     "nnc_hip_kv_free": (None, [_P]),
     "nnc_hip_kv_bytes": (_U64, [_P]),
@@ -130,6 +134,23 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
     if path is None:
         _lib = lib
     return lib
+
+
+_log_keep = None  # the installed callback object (ctypes needs it alive)
+
+
+def set_log_callback(fn) -> None:
+    """Routes the bridge's log lines to fn(level, message) (levels as nnc's:
+    0 debug, 1 info, 2 warn, 3 error); None restores the default (warnings
+    and errors to stderr)."""
+    global _log_keep
+    lib = load_library()
+    if fn is None:
+        _log_keep = None
+        lib.nnc_hip_set_log_callback(LOG_CALLBACK(), None)
+        return
+    _log_keep = LOG_CALLBACK(lambda level, msg, user: fn(int(level), msg.decode("utf-8", "replace")))
+    lib.nnc_hip_set_log_callback(_log_keep, None)
 
 
 def _check(status: int) -> None:

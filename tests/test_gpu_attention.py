@@ -154,6 +154,47 @@ def test_prefill_odd_batches(orc):
         assert errors(got, want)[0] <= 5e-3, w
 
 
+@pytest.mark.parametrize("shape,n,w", (("A", 700, 256), ("D", 300, 0), ("D", 1300, 64)))
+def test_f32_embedding_batch(orc, shape, n, w):
+    """nnc_embed's attention (reference model.cpp:2368, spans :2308-2315): an
+    F32 cache of the whole sequence, every token in one bidirectional batch,
+    with a symmetric window or none; F32 bound of the oracle. 1300 tokens
+    take two launches (1024 tokens each at most)."""
+    base = synth.CONFIGS[shape]
+    cfg = synth.AttnConfig(9, f"embed {shape}", base.n_head, base.n_kv, base.head_dim, 1, kv_bf16=False,
+                           qk_norm=base.qk_norm)
+    K, V = synth.cache_buffer(cfg, 0, n, n)
+    q = synth.qk_rows(cfg, 0, 0, np.arange(n), cfg.n_head)
+    kw = dict(window=w, causal=False, n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim,
+              scale=cfg.attn_scale)
+    say(f"case F32 embedding {shape}: {n} tokens, window {w}")
+    with nh.KVCache([n], [cfg.kv_dim], bf16=False) as kv:
+        kv.append(0, 0, K, V)
+        got = kv.attend(0, q, pos0=0, n_seq=n, **kw)
+    want = orc.attend_layer(q, K, V, kv_bf16=False, rows=n, pos0=0, n_seq=n, **kw)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= 1e-3
+
+
+def test_cache_creation_logs_device_and_bytes():
+    """nnc_hip_kv_create reports the device and the device memory it holds at
+    INFO through the log callback (the counterpart of nnc's context line)."""
+    lines = []
+    nh.set_log_callback(lambda level, msg: lines.append((level, msg)))
+    try:
+        say("case creation log line")
+        with nh.KVCache([1024, 512], [1024, 1024]) as kv:
+            nbytes = kv.nbytes
+    finally:
+        nh.set_log_callback(None)
+    info = [m for level, m in lines if level == 1]
+    say(f"  {info}")
+    assert len(info) == 1
+    assert "2 K/V buffers" in info[0] and "BF16 K/V" in info[0]
+    assert f"{nbytes / 1e6:.1f} MB" in info[0]
+
+
 def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
     """BF16 caches keep an fp16 copy of V for the prefill kernel (P in fp16,
     one MFMA per P . V product) holding values up to 8 in magnitude. A V
