@@ -1313,8 +1313,9 @@ namespace nnchip
 		}
 	}
 
-	int decode_wg_keys(int head_dim, bool bf16, int n_kv)
+	int decode_wg_keys(int head_dim, int group, bool bf16, int n_kv)
 	{
+		if (!mfma_shape(head_dim, group)) return 256;
 		const int lanes = bf16 ? 4 / bf16_heads_per_wg(n_kv) : 4; // wavefronts per KV head
 		switch (head_dim)
 		{
@@ -1325,10 +1326,14 @@ namespace nnchip
 		}
 	}
 
-	int decode_groups(int n_kv, bool bf16) { return bf16 ? n_kv / bf16_heads_per_wg(n_kv) : n_kv; }
+	int decode_groups(int n_kv, bool bf16, int head_dim, int group)
+	{
+		return bf16 && mfma_shape(head_dim, group) ? n_kv / bf16_heads_per_wg(n_kv) : n_kv;
+	}
 
 	bool launch_decode(const decode_params& p, int n_tok, int head_dim, int group, bool bf16, hipStream_t stream)
 	{
+		if (!mfma_shape(head_dim, group)) return launch_decode_generic(p, n_tok, head_dim, group, bf16, stream);
 		switch (head_dim)
 		{
 		case 64:

@@ -36,11 +36,28 @@ namespace nnchip
 	// what keeps a token's bits independent of the kernel that computes it.
 	inline int bf16_heads_per_wg(int n_kv) { return n_kv % 2 == 0 ? 2 : 1; }
 
+	// The head shapes of the MFMA kernels: head_dim 64, 128 or 256 with 1, 2,
+	// 4 or 8 query heads per KV head. Every other shape nnc runs (an even
+	// head_dim up to 512, group * head_dim up to kGenMaxGroupDim) takes the
+	// generic split-K kernels, for every batch size.
+	constexpr int kGenMaxGroup = 16, kGenMaxGroupDim = 8192;
+	__host__ __device__ inline bool mfma_shape(int head_dim, int group)
+	{
+		return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+		       (group == 1 || group == 2 || group == 4 || group == 8);
+	}
+	__host__ __device__ inline bool generic_shape_ok(int head_dim, int group)
+	{
+		return head_dim > 0 && head_dim % 2 == 0 && head_dim <= 512 && group >= 1 && group <= kGenMaxGroup &&
+		       group * head_dim <= kGenMaxGroupDim;
+	}
+
 	// Work-groups per split (head groups) and the keys one work-group
-	// consumes per iteration, for a head size, element type and n_kv;
-	// split_keys must be a multiple of the latter.
-	int decode_groups(int n_kv, bool bf16);
-	int decode_wg_keys(int head_dim, bool bf16, int n_kv);
+	// consumes per iteration, for a head shape, element type and n_kv;
+	// split_keys must be a multiple of the latter (256, nnc's block, for the
+	// generic kernels).
+	int decode_groups(int n_kv, bool bf16, int head_dim, int group);
+	int decode_wg_keys(int head_dim, int group, bool bf16, int n_kv);
 
 	// Launches the decode kernel over an (n_split, head groups, token groups)
 	// grid, then (n_split > 1) the split merge over (n_kv * group * slices, n_tok);
@@ -49,6 +66,11 @@ namespace nnchip
 	// (split_keys and the absolute split boundaries), not on the other tokens
 	// of the launch.
 	bool launch_decode(const decode_params& p, int n_tok, int head_dim, int group, bool bf16, hipStream_t stream);
+
+	// The generic split-K kernels (and their ordered merge) for a shape
+	// outside mfma_shape; false when generic_shape_ok fails.
+	bool launch_decode_generic(const decode_params& p, int n_tok, int head_dim, int group, bool bf16,
+	                           hipStream_t stream);
 
 	// Tiled MFMA attention for a batch of query tokens.
 	struct prefill_params

@@ -462,10 +462,10 @@ namespace
 	// token's result does not depend on the rest of its launch, so it
 	// matches the one-token call bit for bit.
 	void plan_tokens(const nnc_hip_kv* kv, int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
-	                 int32_t n_kv, int32_t head_dim, std::vector<decode_plan>& plan)
+	                 int32_t n_kv, int32_t head_dim, int group, std::vector<decode_plan>& plan)
 	{
-		const int wgk = nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv);
-		const int groups = nnchip::decode_groups(n_kv, kv->bf16);
+		const int wgk = nnchip::decode_wg_keys(head_dim, group, kv->bf16, n_kv);
+		const int groups = nnchip::decode_groups(n_kv, kv->bf16, head_dim, group);
 		auto span_of = [&](int32_t t, int& first, int& last)
 		{ nnchip::attn_span(causal ? 1 : 0, window, pos0 + t, n_seq, first, last); };
 		auto own_split = [&](int32_t t)
@@ -495,7 +495,7 @@ namespace
 	// at most kDecodeChunk tokens (a grid z-extent and a scratch size that
 	// stay small), each on the split grid of its own span.
 	void plan_f32_chunks(const nnc_hip_kv* kv, int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
-	                     int32_t n_kv, int32_t head_dim, std::vector<decode_plan>& plan)
+	                     int32_t n_kv, int32_t head_dim, int group, std::vector<decode_plan>& plan)
 	{
 		for (int32_t t0 = 0; t0 < n_tok; t0 += kDecodeChunk)
 		{
@@ -503,8 +503,9 @@ namespace
 			int kmin, kmax, unused;
 			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0, n_seq, kmin, unused);
 			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
-			const int sk = split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, kv->bf16),
-			                              nnchip::decode_wg_keys(head_dim, kv->bf16, n_kv));
+			const int sk =
+				split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, kv->bf16, head_dim, group),
+				               nnchip::decode_wg_keys(head_dim, group, kv->bf16, n_kv));
 			plan.push_back({t0, nt, sk});
 		}
 	}
@@ -526,13 +527,14 @@ namespace
 		const int kmin = first0, kmax = last1;
 		if (kmax < kmin) return nnchip::launch_zero(out, q_floats, kv->stream) ? NNC_OK : NNC_ERR_IO;
 
-		// Decode and session-sized batches (and every batch in exact mode):
-		// the split-K kernel, each token on its own split grid. Larger
-		// batches: the prefill kernel for BF16, the split-K kernel over each
-		// chunk's span for F32 (exact fp32 products against F32 K/V).
+		// Decode and session-sized batches (and every batch in exact mode, and
+		// every batch of a head shape the MFMA kernels do not take): the
+		// split-K kernel, each token on its own split grid. Larger batches:
+		// the prefill kernel for BF16, the split-K kernel over each chunk's
+		// span for F32 (exact fp32 products against F32 K/V).
 		std::vector<decode_plan> plan;
-		if (n_tok <= kSessionBatch || kv->exact_batches)
-			plan_tokens(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, plan);
+		if (n_tok <= kSessionBatch || kv->exact_batches || (bf16 && !nnchip::mfma_shape(head_dim, group)))
+			plan_tokens(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, group, plan);
 		else if (bf16)
 		{
 			nnchip::prefill_params p{};
@@ -559,7 +561,7 @@ namespace
 			return NNC_OK;
 		}
 		else
-			plan_f32_chunks(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, plan);
+			plan_f32_chunks(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, group, plan);
 
 		// Every launch is planned before the first is enqueued: a call whose
 		// partials do not fit the fixed scratch is refused whole.
@@ -601,10 +603,11 @@ namespace
 			return fail(NNC_ERR_INVALID_ARGUMENT, "%d KV heads of %d do not make the buffer's kv_dim %d", n_kv, head_dim,
 			            b.kv_dim);
 		const int group = n_head / n_kv;
-		if ((head_dim != 64 && head_dim != 128 && head_dim != 256) ||
-		    (group != 1 && group != 2 && group != 4 && group != 8))
-			return fail(NNC_ERR_UNSUPPORTED_MODEL, "head_dim %d with group %d is not supported on the GPU", head_dim,
-			            group);
+		if (!nnchip::mfma_shape(head_dim, group) && !nnchip::generic_shape_ok(head_dim, group))
+			return fail(NNC_ERR_UNSUPPORTED_MODEL,
+			            "head_dim %d with group %d is not supported on the GPU (an even head_dim up to 512, group up to "
+			            "%d, group * head_dim up to %d)",
+			            head_dim, group, nnchip::kGenMaxGroup, nnchip::kGenMaxGroupDim);
 		if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15)
 			return fail(NNC_ERR_INVALID_ARGUMENT, "q and out must be 16-byte aligned");
 		// The BF16 kernels address a buffer with 32-bit byte offsets.
