@@ -30,9 +30,12 @@
 // (o, m, l per head) goes to global scratch, and a second small kernel merges
 // the splits of each KV head in split order and writes o / l (0 when l == 0,
 // reference nn_ops.cpp:492). The order is fixed, so results are the same run
-// to run. (A single-kernel "last work-group merges" scheme needs an
-// agent-scope release in every work-group, which on this multi-XCD part
-// writes back the XCD's L2: measured 1.7x slower at 32k keys.)
+// to run. A one-token launch over at most kFuseMaxSplits splits merges in
+// the split launch instead (fused_merge): the last work-group of each head
+// group to finish runs the merge kernel's operations. (An agent-scope
+// release in every work-group writes back the XCD's L2: that form measured
+// 1.7x slower at 32k keys; the fused merge uses scoped stores and loads
+// instead of fences.)
 #include "device_common.h"
 #include "kernels.h"
 
@@ -178,6 +181,165 @@ namespace nnchip
 			return sh + sl;
 		}
 
+		// Device-coherent access to the partials of a fused merge, through a
+		// buffer descriptor over the launch's partials. The cache-policy
+		// argument 16 sets the sc1 scope bit (device scope): a store with it
+		// is written through the XCD's L2 and acknowledged once every XCD can
+		// see it, and a load with it bypasses the CU's vector cache and is
+		// served from the device-coherent level, never from a stale copy in
+		// another XCD's L2.
+		constexpr int kAuxDevice = 16;
+
+		__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const decode_params& p, int group_pitch)
+		{
+			const uint32_t bytes = static_cast<uint32_t>(p.n_tok) * p.n_kv * p.n_split * group_pitch * 4u;
+			return __builtin_amdgcn_make_buffer_rsrc(p.part, 0, static_cast<int>(bytes), 0x00020000);
+		}
+
+		__device__ __forceinline__ void store_device(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v)
+		{
+			__builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kAuxDevice);
+		}
+
+		__device__ __forceinline__ void store_device(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 v)
+		{
+			__builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, kAuxDevice);
+		}
+
+		__device__ __forceinline__ f32x4 load_device4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+		{
+			return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxDevice));
+		}
+
+		__device__ __forceinline__ float2 load_device2(__amdgpu_buffer_rsrc_t r, uint32_t off)
+		{
+			return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kAuxDevice));
+		}
+
+		// The fused merge of head group hg's splits (one-token launches,
+		// fused_merge_on). Each thread has stored its share of the
+		// work-group's partial with device-scope stores; it waits until they
+		// are acknowledged (s_waitcnt vmcnt(0): on gfx9 stores count there),
+		// so after the barrier the whole partial is visible on every XCD.
+		// One thread then counts the work-group in with a device-scope atomic
+		// add; the work-group that brings the count to n_split is the last of
+		// its group, every other partial is then visible, and it resets the
+		// count to zero for the next launch and merges. Each thread of the
+		// last work-group takes float4 columns of the group's (KV head, query
+		// head) outputs, loads the column of every split at once and
+		// repeats merge_splits' operations:
+		// per part (splits with (absolute split number) % PARTS == part) the
+		// largest m, then the ascending-split sums against it, then the parts
+		// in order against the largest of all. A token therefore gets the
+		// same bits from either merge.
+		template <int HD, int G, int W, int HPW>
+		__device__ __forceinline__ void fused_merge(const decode_params& p, __amdgpu_buffer_rsrc_t rs, int tok, int hg)
+		{
+			__shared__ int s_last;
+			asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+			__syncthreads();
+			if (threadIdx.x == 0)
+			{
+				unsigned* c = p.counts + hg;
+				const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+				const bool last = prev == static_cast<unsigned>(p.n_split - 1);
+				if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+				s_last = last ? 1 : 0;
+			}
+			__syncthreads();
+			if (!s_last) return;
+
+			// F register slots: the splits, and at least one per part (a
+			// part's result is kept in the slot of its first split; a part
+			// past the last split has none and keeps m = -inf, o = l = 0).
+			constexpr int PL = part_pitch<HD>(), Q4 = HD / 4, PARTS = 1024 / HD;
+			constexpr int F = PARTS > kFuseMaxSplits ? PARTS : kFuseMaxSplits;
+			const int ns = p.n_split, a0 = p.split_base / p.split_keys;
+			const uint32_t sstride = G * PL * 4u;
+			for (int idx = threadIdx.x; idx < HPW * G * Q4; idx += 64 * W)
+			{
+				const int hh = idx / (G * Q4), h = (idx / Q4) % G, d4 = idx % Q4;
+				const int kvh = head_of<HPW>(hg, hh, p.n_kv);
+				const uint32_t base = ((static_cast<uint32_t>(tok) * p.n_kv + kvh) * ns * G + h) * PL * 4u;
+				f32x4 o[F];
+				float2 ml[F];
+#pragma unroll
+				for (int u = 0; u < F; ++u)
+				{
+					if (u < ns)
+					{
+						const uint32_t sp = base + static_cast<uint32_t>(u) * sstride;
+						o[u] = load_device4(rs, sp + 16u * d4);
+						ml[u] = load_device2(rs, sp + 4u * HD);
+					}
+				}
+				// Split u belongs to class u % PARTS, and class k to part
+				// (a0 + k) % PARTS: the classes are the parts, with each
+				// class's splits at fixed register indices. Per class: its
+				// largest m, then its ascending-split sums against it, kept in
+				// slot k (its first split, already consumed).
+#pragma unroll
+				for (int k = 0; k < PARTS; ++k)
+				{
+					float mk = -INFINITY;
+#pragma unroll
+					for (int u = k; u < F; u += PARTS)
+						if (u < ns) mk = fmaxf(mk, ml[u].x);
+					const float m_use = mk == -INFINITY ? 0.0f : mk;
+					f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+					float L = 0.0f;
+#pragma unroll
+					for (int u = k; u < F; u += PARTS)
+					{
+						if (u < ns)
+						{
+							const float f = fast_exp2(ml[u].x - m_use);
+							acc.x = fmaf(o[u].x, f, acc.x);
+							acc.y = fmaf(o[u].y, f, acc.y);
+							acc.z = fmaf(o[u].z, f, acc.z);
+							acc.w = fmaf(o[u].w, f, acc.w);
+							L = fmaf(ml[u].y, f, L);
+						}
+					}
+					o[k] = acc;
+					ml[k] = make_float2(mk, L);
+				}
+				float M = -INFINITY;
+#pragma unroll
+				for (int k = 0; k < PARTS; ++k) M = fmaxf(M, ml[k].x);
+				const float M_use = M == -INFINITY ? 0.0f : M;
+				// Then the parts in order 0, 1, ...: part j is class
+				// (j + c) % PARTS, so the classes go c, c + 1, ..., then 0 ..
+				// c - 1 (c is uniform).
+				const int c = (PARTS - a0 % PARTS) % PARTS;
+				float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+				float lt = 0.0f;
+				auto add_part = [&](int k) __attribute__((always_inline))
+				{
+					const float f = fast_exp2(ml[k].x - M_use);
+					r.x = fmaf(o[k].x, f, r.x);
+					r.y = fmaf(o[k].y, f, r.y);
+					r.z = fmaf(o[k].z, f, r.z);
+					r.w = fmaf(o[k].w, f, r.w);
+					lt = fmaf(ml[k].y, f, lt);
+				};
+#pragma unroll
+				for (int k = 0; k < PARTS; ++k)
+					if (k >= c) add_part(k);
+#pragma unroll
+				for (int k = 0; k < PARTS; ++k)
+					if (k < c) add_part(k);
+				const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+				const size_t oi = (static_cast<size_t>(tok) * p.n_head + kvh * G + h) * HD + 4 * d4;
+				float4 out;
+				out.x = gated(r.x * inv, p.gate, oi);
+				out.y = gated(r.y * inv, p.gate, oi + 1);
+				out.z = gated(r.z * inv, p.gate, oi + 2);
+				out.w = gated(r.w * inv, p.gate, oi + 3);
+				*reinterpret_cast<float4*>(p.out + oi) = out;
+			}
+		}
+
 		// The work-group's result from its wavefronts' partials in s_wpart
 		// (o[head_dim], m, l per column, per wavefront). The work-group holds
 		// the HPW KV heads of head group hg (head_of); wavefront w works for
@@ -189,12 +351,13 @@ namespace nnchip
 		// gets the same bits either way. Each thread takes four consecutive
 		// elements of one column. (Wavefront w's partial of column c starts at
 		// s_wpart + w * wstride + c * part_pitch<HD>().)
-		template <int HD, int G, int W, int HPW>
+		template <int HD, int G, int W, int HPW, bool FUSE = true>
 		__device__ __forceinline__ void write_wg_result(const decode_params& p, const float* s_wpart, int wstride,
 		                                                int tok0, int n_cols, int split, int hg)
 		{
 			constexpr int PL = part_pitch<HD>(), LPH = W / HPW, kThreads = 64 * W, Q4 = HD / 4;
-			const bool single = p.n_split == 1;
+			const bool single = p.n_split == 1, fused = FUSE && fused_merge_on(p);
+			const __amdgpu_buffer_rsrc_t rs = part_rsrc(p, G * PL);
 			for (int idx = threadIdx.x; idx < HPW * n_cols * Q4; idx += kThreads)
 			{
 				const int hh = idx / (n_cols * Q4), c = (idx / Q4) % n_cols, d = 4 * (idx % Q4);
@@ -223,7 +386,14 @@ namespace nnchip
 					r.w = fmaf(v.w, f[l], r.w);
 					l_sum = fmaf(wp[HD + 1], f[l], l_sum);
 				}
-				if (!single)
+				if (fused)
+				{
+					const uint32_t off =
+						(((static_cast<uint32_t>(tok) * p.n_kv + kvh) * p.n_split + split) * G * PL + h * PL) * 4u;
+					store_device(rs, off + 4u * d, r);
+					if (d == 0) store_device(rs, off + 4u * HD, make_float2(m, l_sum));
+				}
+				else if (!single)
 				{
 					float* gpart = p.part + ((static_cast<size_t>(tok) * p.n_kv + kvh) * p.n_split + split) * G * PL + h * PL;
 					*reinterpret_cast<float4*>(gpart + d) = r;
@@ -241,6 +411,7 @@ namespace nnchip
 					*reinterpret_cast<float4*>(p.out + oi) = o;
 				}
 			}
+			if (fused) fused_merge<HD, G, W, HPW>(p, rs, tok0, hg);
 		}
 
 		// A merge work-group takes 1 / SLICES of one (token, query head)'s
@@ -1239,7 +1410,8 @@ namespace nnchip
 					}
 				}
 				__syncthreads();
-				if (n_cols > 0) write_wg_result<HD, G, W, HPW>(p, s_wpart, kTileFloats, tok0 + 16 * tl / G, n_cols, split, hg);
+				if (n_cols > 0)
+					write_wg_result<HD, G, W, HPW, false>(p, s_wpart, kTileFloats, tok0 + 16 * tl / G, n_cols, split, hg);
 				__syncthreads(); // the partials are read before the next tile overwrites them
 			}
 		}
@@ -1292,6 +1464,8 @@ namespace nnchip
 				f32_decode_kernel<HD, G><<<dim3(p.n_split, p.n_kv, n_tok), 256, 0, stream>>>(p);
 			// The merge: a quarter head per work-group while that makes at most
 			// 256 work-groups, else whole heads.
+			if (fused_merge_on(p))
+				return;
 			if (p.n_split > 1 && p.n_kv * G * n_tok <= 64)
 				decode_merge_kernel<HD, G, 4>
 					<<<dim3(p.n_kv * G * 4, n_tok), merge_lds<HD, 4>::THREADS, 0, stream>>>(p);

@@ -25,9 +25,25 @@ namespace nnchip
 		int split_keys; // keys per work-group, a multiple of decode_wg_keys()
 		int n_split; // work-groups per (token, KV head), at most kDecodeMaxSplits
 		float qscale; // scale * log2(e)
+		// Per head group arrival counts for the fused merge (all zero
+		// between launches), or null: then a separate merge launch follows.
+		unsigned* counts;
 	};
 
 	constexpr int kDecodeMaxSplits = 256;
+
+	// The fused merge: a one-token launch of the MFMA kernels over at most
+	// kFuseMaxSplits splits merges inside the split launch. Each work-group
+	// writes its partial device-coherently and counts itself in; the last of
+	// a head group to arrive merges the group's splits with the operations of
+	// the merge kernel, so the bits do not depend on which path ran. The
+	// short spans of decode (a sliding window, a small context) are where a
+	// second launch costs as much as the split itself.
+	constexpr int kFuseMaxSplits = 8, kFuseCounts = 4096;
+	__host__ __device__ inline bool fused_merge_on(const decode_params& p)
+	{
+		return p.counts != nullptr && p.n_tok == 1 && p.n_split > 1 && p.n_split <= kFuseMaxSplits;
+	}
 
 	// KV heads per work-group of the BF16 kernels: two when n_kv is even (a
 	// work-group then reads runs of 2 * head_dim elements of each row, two

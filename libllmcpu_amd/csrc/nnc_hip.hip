@@ -186,6 +186,7 @@ struct nnc_hip_kv
 	dev_scratch gate;
 	dev_scratch gemv_part; // weight gemv partial sums over K splits
 	int* n_bad = nullptr; // per buffer: elements of V's fp16 copy now marked kF16Bad (device)
+	unsigned* counts = nullptr; // kFuseCounts arrival counts of the fused decode merge (device, zero between calls)
 	dev_scratch rows_k;
 	dev_scratch rows_v;
 	host_staging pinned; // host rows in and out (q, gate, out; K/V appends; RoPE tables)
@@ -205,6 +206,7 @@ namespace
 				if (ptr) (void)hipFree(ptr);
 		}
 		if (kv->n_bad) (void)hipFree(kv->n_bad);
+		if (kv->counts) (void)hipFree(kv->counts);
 		for (dev_scratch* s : {&kv->part, &kv->q, &kv->gate, &kv->gemv_part, &kv->rows_k, &kv->rows_v,
 		                       &kv->rope[0].dev, &kv->rope[1].dev})
 			if (s->ptr) (void)hipFree(s->ptr);
@@ -450,6 +452,9 @@ namespace
 		p.split_keys = split_keys;
 		p.n_split = g.n_split;
 		p.qscale = scale * 1.4426950408889634f;
+		// One-token launches of the MFMA kernels over a few splits merge in
+		// the split launch; the counts are the cache's, used in stream order.
+		if (nnchip::mfma_shape(head_dim, group) && n_kv <= nnchip::kFuseCounts) p.counts = kv->counts;
 		if (!nnchip::launch_decode(p, n_tok, head_dim, group, kv->bf16, kv->stream))
 			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no decode kernel for head_dim %d, group %d", head_dim, group);
 		NNC_HIP_TRY(hipGetLastError(), "decode launch");
@@ -706,7 +711,9 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 		kv->bytes += 2 * n;
 	}
-	e = hipStreamSynchronize(kv->stream);
+	e = hipMalloc(&kv->counts, sizeof(unsigned) * nnchip::kFuseCounts);
+	if (e == hipSuccess) e = hipMemsetAsync(kv->counts, 0, sizeof(unsigned) * nnchip::kFuseCounts, kv->stream);
+	if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
 	if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 	void* fixed = nullptr;
 	if (nnc_status s = noalloc_scratch(kv->device, &fixed)) return bail(s);

@@ -25,7 +25,8 @@ def say(msg: str) -> None:
 
 def test_noalloc_first_call_is_captured_and_replays(orc):
     """Fresh caches A and B with the same rows: A's first no-alloc calls (a
-    decode token and a 16-token session batch) are captured into a HIP graph
+    decode token, a 16-token session batch and a short-span decode token,
+    whose merge runs inside the split launch) are captured into a HIP graph
     (thread-local capture mode: a hipMalloc, hipFree or stream
     synchronisation inside the call would fail hipStreamEndCapture). B runs
     the same calls eagerly through nnc_hip_attend_device. Three replays, each
@@ -36,7 +37,7 @@ def test_noalloc_first_call_is_captured_and_replays(orc):
     K, V = synth.cache_buffer(cfg, 0, rows, rows)
     kw = dict(n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
     width = cfg.n_head * cfg.head_dim
-    calls = ((8191, 1, 0), (8176, 16, 1))  # (pos0, n_tok, first token slot)
+    calls = ((8191, 1, 0), (8176, 16, 1), (700, 1, 17))  # (pos0, n_tok, first token slot)
     q = np.concatenate([synth.qk_rows(cfg, 0, 0, np.arange(p, p + n), cfg.n_head) for p, n, _ in calls])
     with nh.KVCache([rows], [cfg.kv_dim]) as kv_a, nh.KVCache([rows], [cfg.kv_dim]) as kv_b:
         kv_a.append(0, 0, K, V)
