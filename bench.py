@@ -390,7 +390,8 @@ def layer_spans(cfg, layer: int, pos0: int, n_tok: int) -> np.ndarray:
 
 
 def configs_bench(nh, hip_rt, synth) -> dict:
-    """The benchmark's other configurations (A, B, C, D at 4096, E), each
+    """The benchmark's other configurations (A, B, C, D at 4096, E) and an
+    embedding call (EmbeddingGemma-300M's shape), each
     step replayed from a HIP graph of its attend calls so the small layers are
     timed by the GPU rather than by Python's launch rate. Inputs come from
     the device generator (K RMS-normed per head where the model normalises
@@ -424,7 +425,7 @@ def configs_bench(nh, hip_rt, synth) -> dict:
         kv.sync()
         return kv
 
-    def measure(kv, calls, n_tok_max, n_out, cfg, reps):
+    def measure(kv, calls, n_tok_max, n_out, cfg, reps, causal=True):
         """calls: (layer, out slot, pos0, n_tok) tuples of one step."""
         st = kv.stream
         width = cfg.n_head * cfg.head_dim
@@ -435,7 +436,7 @@ def configs_bench(nh, hip_rt, synth) -> dict:
         def step():
             for li, slot, pos0, n in calls:
                 kv.attend_device(li, q, o + 4 * slot * n_tok_max * width, n_tok=n, pos0=pos0,
-                                 window=cfg.layer_window(li), n_head=cfg.n_head, n_kv=cfg.n_kv,
+                                 window=cfg.layer_window(li), causal=causal, n_head=cfg.n_head, n_kv=cfg.n_kv,
                                  head_dim=cfg.head_dim, scale=cfg.attn_scale)
 
         step()  # eager: scratch grows here, never inside the capture
@@ -507,6 +508,28 @@ def configs_bench(nh, hip_rt, synth) -> dict:
                            "ms_per_step": round(ms / 256, 4), "bytes_per_step": nbytes // 256, "value": round(gbs, 1),
                            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "replay_equals_eager": same}
     log(f"[bench] E_decode_256: {ms / 256 * 1e3:.1f} us/step, {gbs:.0f} GB/s")
+    # nnc's embedding call (reference model.cpp:2355-2368): the whole input
+    # in one batch over an F32 cache, bidirectional (local layers see +-w/2
+    # keys, model.cpp:2308-2315), EmbeddingGemma-300M's attention shape.
+    emb = synth.AttnConfig(5, "embeddinggemma-300m embedding", 3, 1, 256, 24, kv_bf16=False, window=512,
+                           swa_period=6, tol=1e-3)
+    n_emb = 2048
+    kv = build(emb, n_emb, n_emb)
+    calls = [(li, li, 0, n_emb) for li in range(emb.n_layer)]
+    ms, same = measure(kv, calls, n_emb, emb.n_layer, emb, 3, causal=False)
+    pos = np.arange(n_emb, dtype=np.int64)
+    flops = 0
+    for li in range(emb.n_layer):
+        w = emb.layer_window(li)
+        spans = (np.minimum(n_emb - 1, pos + w // 2) - np.maximum(0, pos - w // 2) + 1) if w > 0 else \
+            np.full(n_emb, n_emb)
+        flops += int(4 * emb.head_dim * emb.n_head * spans.sum())
+    tf = flops / (ms * 1e-3) / 1e12
+    out["EMB_embed_2048"] = {"workload": f"{emb.name}: one {n_emb}-token input, F32 K/V, bidirectional, "
+                                         f"{emb.n_layer} layers (20 with a 512-key window)",
+                             "ms_per_step": round(ms, 3), "flops_per_step": flops, "value": round(tf, 2),
+                             "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "replay_equals_eager": same}
+    log(f"[bench] EMB_embed_2048: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
     for kv_, k_dev, v_dev in keep:
         kv_.close()
         hip_rt.free(k_dev)

@@ -30,16 +30,20 @@ from libllmcpu_amd import synth  # noqa: E402
 
 OUT = Path(__file__).resolve().parent / "reference_vectors.npz"
 
-# (name, config, layer, n_seq, pos0, n_tok, n_batch): a session that appended
-# positions 0 .. n_seq - 1, then attends tokens pos0 .. pos0 + n_tok - 1.
+# (name, config, layer, n_seq, pos0, n_tok, n_batch, stride): a session that
+# appended positions 0 .. n_seq - 1, then attends tokens pos0 .. pos0 + n_tok
+# - 1; the output rows of every stride-th token are stored.
 LAYER_CASES = [
-    ("A_decode", "A", 1, 1024, 1023, 1, 16),            # F32 K/V, hd 256
-    ("B_decode", "B", 0, 512, 511, 1, 16),              # hd 64, RoPE NORM
-    ("C_local_ring_decode", "C", 0, 3000, 2999, 1, 2048),  # ring of 2560 rows, window 512, wrapped
-    ("C_global_prefill", "C", 5, 640, 632, 8, 16),
-    ("D_decode", "D", 0, 2048, 2047, 1, 16),            # RMS-normed Q/K, hd 128
-    ("D_prefill", "D", 1, 512, 504, 8, 16),
-    ("E_local_prefill", "E", 0, 1400, 1392, 8, 1024),  # ring of 2048 rows, window 1024, g = 2
+    ("A_decode", "A", 1, 1024, 1023, 1, 16, 1),            # F32 K/V, hd 256
+    ("B_decode", "B", 0, 512, 511, 1, 16, 1),              # hd 64, RoPE NORM
+    ("C_local_ring_decode", "C", 0, 3000, 2999, 1, 2048, 1),  # ring of 2560 rows, window 512, wrapped
+    ("C_global_prefill", "C", 5, 640, 632, 8, 16, 1),
+    ("D_decode", "D", 0, 2048, 2047, 1, 16, 1),            # RMS-normed Q/K, hd 128
+    ("D_prefill", "D", 1, 512, 504, 8, 16, 1),
+    ("E_local_prefill", "E", 0, 1400, 1392, 8, 1024, 1),  # ring of 2048 rows, window 1024, g = 2
+    # chunks long enough for the MFMA prefill kernel: hd 128, and hd 256 on a global layer
+    ("D_prefill_chunk64", "D", 1, 2048, 1984, 64, 64, 4),
+    ("E_global_chunk64", "E", 5, 1600, 1536, 64, 64, 4),
 ]
 
 
@@ -105,11 +109,12 @@ def main() -> int:
     orc, ref = oracle.Oracle(), oracle.Reference()
     ref.set_threads(8)
     data: dict[str, np.ndarray] = {}
-    for name, key, layer, n_seq, pos0, n_tok, n_batch in LAYER_CASES:
+    for name, key, layer, n_seq, pos0, n_tok, n_batch, stride in LAYER_CASES:
         q, K, V, kw = layer_inputs(key, layer, n_seq, pos0, n_tok, n_batch)
-        data[f"layer/{name}/out"] = ref.attend_layer(q, K, V, **kw)
+        data[f"layer/{name}/out"] = np.ascontiguousarray(ref.attend_layer(q, K, V, **kw)[::stride])
         data[f"layer/{name}/sha256"] = np.array(sha(q, K, V))
         data[f"layer/{name}/case"] = np.array([layer, n_seq, pos0, n_tok, n_batch], dtype=np.int64)
+        data[f"layer/{name}/stride"] = np.array(stride, dtype=np.int64)
         data[f"layer/{name}/config"] = np.array(key)
         print(f"{name}: {data[f'layer/{name}/out'].shape}")
     for which in range(4):

@@ -48,8 +48,18 @@ def layer_case(gold, name):
     return cfg, q, K, V, kw, gold[f"layer/{name}/out"]
 
 
+def stored_rows(gold, name, out):
+    """The rows of `out` the file holds: every stride-th token."""
+    return out[::int(gold[f"layer/{name}/stride"])]
+
+
 def test_golden_file_holds_every_case(gold):
-    assert len(layer_names(gold)) == 7
+    """Decode tokens, 8-token batches, and two 64-token chunks (hd 128, and
+    hd 256 on a global layer) long enough for the MFMA prefill kernel."""
+    assert len(layer_names(gold)) == 9
+    for name in ("D_prefill_chunk64", "E_global_chunk64"):
+        assert int(gold[f"layer/{name}/case"][3]) >= 64
+        assert gold[f"layer/{name}/out"].shape[0] == 16
     assert {f"blocks/{w}/out" for w in range(4)} <= set(gold.files)
 
 
@@ -59,7 +69,7 @@ def test_oracle_layers_match_reference_vectors(orc, gold):
     differ only in exp's polynomial and summation order."""
     for name in layer_names(gold):
         cfg, q, K, V, kw, want = layer_case(gold, name)
-        got = orc.attend_layer(q, K, V, kv_bf16=cfg.kv_bf16, **kw)
+        got = stored_rows(gold, name, orc.attend_layer(q, K, V, kv_bf16=cfg.kv_bf16, **kw))
         assert np.all(np.abs(got - want) <= 1e-5 * (1.0 + np.abs(want))), name
 
 
@@ -112,13 +122,14 @@ def test_rope_and_rmsnorm_match_reference_vectors(orc, gold):
 @pytest.mark.gpu
 def test_hip_op_matches_reference_vectors(gold):
     """The HIP op through the C ABI against the reference's outputs (bounds:
-    1e-3 for F32 K/V, 5e-3 for BF16)."""
+    1e-3 for F32 K/V, 5e-3 for BF16): decode and 8-token batches through the
+    split-K kernels, the 64-token chunks through the MFMA prefill kernel."""
     for name in layer_names(gold):
         cfg, q, K, V, kw, want = layer_case(gold, name)
         print(f"case golden {name}: tokens {kw['pos0']}+{q.shape[0]} rows {kw['rows']}", flush=True)
         with nh.KVCache([kw["rows"]], [cfg.kv_dim], bf16=cfg.kv_bf16) as kv:
             kv.append(0, 0, K, V)
-            got = kv.attend(0, q, **{k: v for k, v in kw.items() if k != "rows"})
+            got = stored_rows(gold, name, kv.attend(0, q, **{k: v for k, v in kw.items() if k != "rows"}))
         err = float(np.abs(got.astype(np.float64) - want).max())
         print(f"  max-abs {err:.3e}", flush=True)
         assert err <= cfg.tol, (name, err)
