@@ -16,7 +16,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libnnc_hip.so"
-SOURCES = ["nnc_hip.hip", "attn_decode.hip", "attn_generic.hip", "attn_prefill.hip", "kv_ops.hip", "kv_prep.hip", "gemv.hip"]
+SOURCES = ["nnc_hip.hip", "attn_decode.hip", "attn_generic.hip", "attn_tiled.hip", "attn_prefill.hip", "kv_ops.hip", "kv_prep.hip", "gemv.hip"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [

@@ -214,8 +214,12 @@ namespace nnchip
 			decode_generic_kernel<true><<<grid, kGenThreads, 0, stream>>>(p, head_dim, group);
 		else
 			decode_generic_kernel<false><<<grid, kGenThreads, 0, stream>>>(p, head_dim, group);
-		if (p.n_split > 1)
-			merge_generic_kernel<<<dim3(p.n_kv * group, n_tok), kGenThreads, 0, stream>>>(p, head_dim, group);
+		if (p.n_split > 1) launch_merge_generic(p, n_tok, head_dim, group, stream);
 		return true;
+	}
+
+	void launch_merge_generic(const decode_params& p, int n_tok, int head_dim, int group, hipStream_t stream)
+	{
+		merge_generic_kernel<<<dim3(p.n_kv * group, n_tok), kGenThreads, 0, stream>>>(p, head_dim, group);
 	}
 }

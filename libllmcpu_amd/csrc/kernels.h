@@ -88,6 +88,21 @@ namespace nnchip
 	bool launch_decode_generic(const decode_params& p, int n_tok, int head_dim, int group, bool bf16,
 	                           hipStream_t stream);
 
+	// The ordered merge of the generic kernels' split partials (n_split > 1)
+	// over an (n_kv * group, n_tok) grid; writes o * (1 / l).
+	void launch_merge_generic(const decode_params& p, int n_tok, int head_dim, int group, hipStream_t stream);
+
+	// The tiled fp32-MFMA kernel for batches of F32 caches and of head shapes
+	// outside mfma_shape: head_dim a multiple of 16 up to 512, group up to 16.
+	// Grid (row blocks of 64, n_kv, n_split) over the absolute split grid of
+	// p.split_keys (a multiple of 16) keys, then (n_split > 1) the generic
+	// merge; false when tiled_shape_ok fails.
+	__host__ __device__ inline bool tiled_shape_ok(int head_dim, int group)
+	{
+		return head_dim > 0 && head_dim % 16 == 0 && head_dim <= 512 && group >= 1 && group <= kGenMaxGroup;
+	}
+	bool launch_tiled(const decode_params& p, int n_tok, int head_dim, int group, bool bf16, hipStream_t stream);
+
 	// Tiled MFMA attention for a batch of query tokens.
 	struct prefill_params
 	{

@@ -156,6 +156,7 @@ namespace
 	void* g_scratch_ptr[kMaxDevices] = {};
 
 	constexpr int32_t kDecodeChunk = 1024; // tokens per split-K launch
+	constexpr int32_t kTiledChunk = 2048; // tokens per tiled launch (rows / 64 blocks on the grid's x)
 	// Most tokens one forward pass of an nnc session carries
 	// (MODEL_PREFILL_BATCH, reference model.h:330; session.cpp:340), its MTP
 	// verification batches included (n_draft + 1, session.cpp:357, :516).
@@ -384,7 +385,16 @@ namespace
 	{
 		int32_t t0, n;
 		int sk;
+		bool tiled = false; // the tiled fp32-MFMA kernel instead of the per-token split-K kernels
+		int nz = 0; // tiled: splits of the row block with the most keys (sk keys each, from the block's first key)
 	};
+
+	// Bytes of the tiled kernel's partials for a plan entry (none for one split).
+	size_t tiled_part_bytes(const decode_plan& d, int32_t n_head, int32_t n_kv, int32_t head_dim)
+	{
+		if (d.nz <= 1) return 0;
+		return static_cast<size_t>(d.n) * n_kv * d.nz * (n_head / n_kv) * (head_dim + 4) * sizeof(float);
+	}
 
 	// The split grid of one launch over tokens pos0 .. pos0 + n_tok - 1:
 	// the first split's first key, the number of splits and the bytes of
@@ -414,6 +424,44 @@ namespace
 	// One split-K launch (and its merge) over tokens pos0 .. pos0 + n_tok - 1
 	// on the absolute split grid of split_keys keys. The partials go to
 	// src (already checked to hold them) or to the cache's scratch.
+	// One launch of the tiled kernel (plan entry d: its tokens, split size
+	// and split count), partials in src or the cache's scratch.
+	nnc_status tiled_launch(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate,
+	                        const decode_plan& d, int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
+	                        int32_t n_kv, int32_t head_dim, float scale, const part_source& src)
+	{
+		const size_t bytes = tiled_part_bytes(d, n_head, n_kv, head_dim);
+		float* part = src.ptr;
+		if (!part && bytes)
+		{
+			if (nnc_status s = reserve(kv, kv->part, bytes, "tiled scratch")) return s;
+			part = static_cast<float*>(kv->part.ptr);
+		}
+		nnchip::decode_params p{};
+		p.q = q;
+		p.out = out;
+		p.gate = gate;
+		p.K = b.k;
+		p.V = b.v;
+		p.part = part;
+		p.rows = b.rows;
+		p.kv_dim = b.kv_dim;
+		p.n_head = n_head;
+		p.n_kv = n_kv;
+		p.pos0 = pos0;
+		p.n_seq = n_seq;
+		p.window = window;
+		p.causal = causal ? 1 : 0;
+		p.n_tok = d.n;
+		p.split_keys = d.sk;
+		p.n_split = d.nz;
+		p.qscale = scale * 1.4426950408889634f;
+		if (!nnchip::launch_tiled(p, d.n, head_dim, n_head / n_kv, kv->bf16, kv->stream))
+			return fail(NNC_ERR_UNSUPPORTED_MODEL, "no tiled kernel for head_dim %d, group %d", head_dim, n_head / n_kv);
+		NNC_HIP_TRY(hipGetLastError(), "tiled launch");
+		return NNC_OK;
+	}
+
 	nnc_status decode_launch(nnc_hip_kv* kv, const kv_buffer& b, const float* q, float* out, const float* gate, int32_t n_tok,
 	                         int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
 	                         int32_t head_dim, float scale, int split_keys, const part_source& src)
@@ -515,6 +563,42 @@ namespace
 		}
 	}
 
+	// The tiled kernel's launches: chunks of at most kTiledChunk tokens. Each
+	// row block of 64 (token, head) rows splits its keys (the union of its
+	// rows' spans) into splits of sk keys from its first key; sk is chosen so
+	// that the work-groups of the launch about fill the part once (the
+	// kernel's resident work-groups per CU: 4 up to head_dim 128, 2 up to
+	// 256, else 1), at least 64 keys per split.
+	void plan_tiled(const nnc_hip_kv* kv, int32_t n_tok, int32_t pos0, int32_t n_seq, int32_t window, bool causal,
+	                int32_t n_kv, int32_t head_dim, int group, std::vector<decode_plan>& plan)
+	{
+		const int per_cu = head_dim <= 128 ? 4 : head_dim <= 256 ? 2 : 1;
+		for (int32_t t0 = 0; t0 < n_tok; t0 += kTiledChunk)
+		{
+			const int32_t nt = std::min(kTiledChunk, n_tok - t0);
+			const long long n_rows = static_cast<long long>(nt) * group, n_blk = (n_rows + 63) / 64;
+			std::vector<int> spans(static_cast<size_t>(n_blk));
+			int max_span = 1;
+			for (long long blk = 0; blk < n_blk; ++blk)
+			{
+				const long long r0 = 64 * blk, r1 = std::min(r0 + 64, n_rows) - 1;
+				int lo, hi, unused;
+				nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + static_cast<int32_t>(r0 / group), n_seq, lo, unused);
+				nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + static_cast<int32_t>(r1 / group), n_seq, unused, hi);
+				spans[static_cast<size_t>(blk)] = std::max(0, hi - lo + 1);
+				max_span = std::max(max_span, hi - lo + 1);
+			}
+			const long long want = std::max<long long>(1, 1LL * kv->n_cu * per_cu / (n_blk * n_kv));
+			long long sk = (max_span + want - 1) / want;
+			sk = std::max<long long>(64, (sk + 15) / 16 * 16);
+			int nz = 1;
+			for (int sp : spans)
+				if (sp > 0) nz = std::max(nz, static_cast<int>((sp - 1) / sk + 1));
+			decode_plan d{t0, nt, static_cast<int>(sk), true, nz};
+			plan.push_back(d);
+		}
+	}
+
 	nnc_status attend_impl(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, const float* gate, int32_t n_tok, int32_t pos0,
 	                       int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv, int32_t head_dim,
 	                       float scale, const part_source& src = part_source{})
@@ -532,15 +616,18 @@ namespace
 		const int kmin = first0, kmax = last1;
 		if (kmax < kmin) return nnchip::launch_zero(out, q_floats, kv->stream) ? NNC_OK : NNC_ERR_IO;
 
-		// Decode and session-sized batches (and every batch in exact mode, and
-		// every batch of a head shape the MFMA kernels do not take): the
-		// split-K kernel, each token on its own split grid. Larger batches:
-		// the prefill kernel for BF16, the split-K kernel over each chunk's
-		// span for F32 (exact fp32 products against F32 K/V).
+		// Decode and session-sized batches (and every batch in exact mode):
+		// the split-K kernels, each token on its own split grid. Larger
+		// batches: the MFMA prefill kernel for BF16 K/V of its head shapes;
+		// the tiled fp32-MFMA kernel for F32 K/V and the other head shapes
+		// with head_dim a multiple of 16 (exact fp32 products); otherwise the
+		// split-K kernels (BF16: each token on its own grid; F32: over each
+		// chunk's span).
 		std::vector<decode_plan> plan;
-		if (n_tok <= kSessionBatch || kv->exact_batches || (bf16 && !nnchip::mfma_shape(head_dim, group)))
+		const bool mfma = nnchip::mfma_shape(head_dim, group), tiled = nnchip::tiled_shape_ok(head_dim, group);
+		if (n_tok <= kSessionBatch || kv->exact_batches || (bf16 && !mfma && !tiled))
 			plan_tokens(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, group, plan);
-		else if (bf16)
+		else if (bf16 && mfma)
 		{
 			nnchip::prefill_params p{};
 			p.q = q;
@@ -565,6 +652,8 @@ namespace
 			NNC_HIP_TRY(hipGetLastError(), "prefill launch");
 			return NNC_OK;
 		}
+		else if (tiled)
+			plan_tiled(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, group, plan);
 		else
 			plan_f32_chunks(kv, n_tok, pos0, n_seq, window, causal, n_kv, head_dim, group, plan);
 
@@ -574,7 +663,8 @@ namespace
 			for (const decode_plan& d : plan)
 			{
 				const launch_geometry g =
-					geometry_of(d.n, pos0 + d.t0, n_seq, window, causal, n_head, n_kv, head_dim, d.sk);
+					d.tiled ? launch_geometry{0, d.nz, tiled_part_bytes(d, n_head, n_kv, head_dim)}
+					        : geometry_of(d.n, pos0 + d.t0, n_seq, window, causal, n_head, n_kv, head_dim, d.sk);
 				if (g.part_bytes > src.bytes)
 					return fail(NNC_ERR_INVALID_ARGUMENT,
 					            "%d tokens over %d splits need %zu bytes of decode partials; the fixed scratch holds %zu",
@@ -584,9 +674,11 @@ namespace
 		for (const decode_plan& d : plan)
 		{
 			const size_t off = static_cast<size_t>(d.t0) * tok_floats;
-			if (nnc_status s = decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, d.n, pos0 + d.t0, n_seq,
-			                                 window, causal, n_head, n_kv, head_dim, scale, d.sk, src))
-				return s;
+			nnc_status s = d.tiled ? tiled_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, d, pos0 + d.t0,
+			                                      n_seq, window, causal, n_head, n_kv, head_dim, scale, src)
+			                       : decode_launch(kv, b, q + off, out + off, gate ? gate + off : nullptr, d.n, pos0 + d.t0,
+			                                       n_seq, window, causal, n_head, n_kv, head_dim, scale, d.sk, src);
+			if (s) return s;
 		}
 		return NNC_OK;
 	}
