@@ -87,7 +87,8 @@ typedef struct nnc_hip_kv nnc_hip_kv;
  * model.cpp:1908-1957; rows come from the same rule: n_ctx, or a ring of
  * round_up(window + n_batch, 256) rows for a sliding layer). A BF16 cache
  * also keeps an fp16 copy of every V buffer, written by every append, for the
- * prefill kernel, which uses it while every value in it is within +-32 (1.5
+ * prefill kernel, which uses it while every value in it is within +-8, where
+ * P rounded to fp16 moves an output by at most 2^-11 * 8 = 3.9e-3 (1.5
  * times the device memory of K and V alone; NNC_HIP_F16_SHADOW=0 in the
  * environment at creation leaves it out, and prefill then runs slower). The
  * nnc-visible buffers stay BF16 in nnc's layout.
@@ -203,10 +204,13 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
  * reference model.h:330) run the split-K kernel with each token on the split
  * grid a one-token call gives it, so every token of such a batch gets the
  * bits of its one-token call (the decode == batch property of reference
- * tests.cpp:2631-2661 that MTP verification relies on). Larger BF16 batches
- * run the MFMA prefill kernel (within tolerance, not bit-identical); larger
- * F32 batches the split-K kernel over the batch's span. Supported shapes:
- * head_dim 64, 128 or 256; group n_head / n_kv in {1, 2, 4, 8}.
+ * tests.cpp:2631-2661 that MTP verification relies on). Larger batches run
+ * the MFMA prefill kernel (BF16, head_dim 64, 128 or 256 with a group of 1,
+ * 2, 4 or 8) or the tiled fp32-MFMA kernel (F32, and the other head shapes
+ * with head_dim a multiple of 16), within tolerance, not bit-identical;
+ * other shapes stay on the split-K kernels. Supported shapes: every even
+ * head_dim up to 512 (as nnc, reference model.cpp:714) with a group
+ * n_head / n_kv up to 16 and group * head_dim up to 8192.
  * NNC_ERR_INVALID_ARGUMENT: bad buffer index, NULL pointers, n_tok <= 0,
  * pos0 < 0, n_seq < 1, n_head not a multiple of n_kv, n_kv * head_dim not the
  * buffer's kv_dim.
@@ -214,7 +218,7 @@ nnc_status nnc_hip_kv_read(nnc_hip_kv* kv, int32_t buf, int32_t row0, int32_t n_
  * can hold (a full buffer with pos0 + n_tok > rows, or a ring too small for
  * the window plus the batch).
  * NNC_ERR_UNSUPPORTED_MODEL: a head_dim or group outside the supported set,
- * or a BF16 batch of more than 16 tokens over a buffer of 2 GiB or more. */
+ * or a BF16 buffer of 2 GiB or more. */
 nnc_status nnc_hip_attend(nnc_hip_kv* kv, int32_t buf, const float* q, float* out, int32_t n_tok, int32_t pos0,
                           int32_t n_seq, int32_t window, bool causal, int32_t n_head, int32_t n_kv,
                           int32_t head_dim, float scale);
@@ -225,14 +229,14 @@ nnc_status nnc_hip_attend_device(nnc_hip_kv* kv, int32_t buf, const float* q, fl
                                  int32_t pos0, int32_t n_seq, int32_t window, bool causal, int32_t n_head,
                                  int32_t n_kv, int32_t head_dim, float scale);
 
-/* Bytes of the fixed per-device decode scratch of
- * nnc_hip_attend_device_noalloc. */
+/* Bytes of the fixed per-device scratch of nnc_hip_attend_device_noalloc
+ * (split partials of decode and of tiled batches). */
 #define NNC_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* As nnc_hip_attend_device, for callers that cannot allocate device memory:
  * code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. No counterpart in the reference. The call allocates nothing
- * (no hipMalloc, hipFree or allocating library routine): the decode kernels'
+ * (no hipMalloc, hipFree or allocating library routine): the split kernels'
  * partials go to a fixed array of NNC_HIP_NOALLOC_SCRATCH_BYTES in each
  * device's memory, which the library holds until the process ends. Every
  * call on a GPU shares that GPU's array, and the calls are asynchronous: two

@@ -21,9 +21,9 @@
 // wavefront then keeps both halves of its B operand in registers (at
 // head_dim 256 it reads them from LDS). V comes from one of two copies:
 //   - an fp16 copy (exact copies of the bf16 values, kept beside the cache
-//     and used while every value in it is within +-32, kF16CopyMax, where
-//     P's rounding stays well inside the tolerance): P goes in fp16 rounded
-//     to nearest, one MFMA per product;
+//     and used while every value in it is within +-8, kF16CopyMax, where
+//     P's rounding moves an output by at most 2^-11 * 8): P goes in fp16
+//     rounded to nearest, one MFMA per product;
 //   - the bf16 V itself (no copy, or a larger value in it): P is split into
 //     bf16 hi + lo, two MFMAs per product, near-fp32.
 // Per step, a key group's 32 K rows and 32 V rows arrive in its LDS tiles

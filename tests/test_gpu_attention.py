@@ -253,6 +253,57 @@ def test_prefill_fp16_shadow_and_fallbacks(orc, monkeypatch):
     run(K, V, q2, "Q value past fp16 range", relative=True)
 
 
+def test_prefill_fp16_weights_within_their_bound(orc):
+    """The fp16 P . V path at its limit, closed form: every query row weighs
+    three keys only (unit K rows e0, e1, e2; every other key scores 60 log2
+    units lower and weighs 0), with V rows 0, +8 and -8 (the copy's limit),
+    scores 20, 20 - a and 20 - b in log2 units for random a, b in [0, 1).
+    The kernel's offset sits 8 below the row max, so the max key weighs
+    exactly 2^8 and the other two land anywhere in (2^7, 2^8], their fp16
+    roundings in either direction (relative error up to 2^-11, just above
+    2^7). With the row sum taken from the same rounded weights, an output
+    moves by sum_k w_k e_k (V_k - out), so each row must stay within
+    2^-11 * sum_k w_k |V_k - out| of the oracle (plus 2e-6 for the
+    near-fp32 scores): 1024 rows of a 256-token chunk (the prefill kernel),
+    many of them near the worst case."""
+    n_head, n_kv, hd, n_seq, n_tok = 4, 1, 128, 1024, 256
+    scale = 1.0 / np.sqrt(hd)
+    log2e = 1.4426950408889634
+    K = np.zeros((n_seq, hd), np.float32)
+    K[0, 0] = K[1, 1] = K[2, 2] = 1.0
+    K[3:, 3] = -1.0
+    V = np.zeros((n_seq, hd), np.float32)
+    V[1], V[2] = 8.0, -8.0
+    rng = np.random.default_rng(11)
+    a, b = rng.random((2, n_tok, n_head))
+    u = 1.0 / (scale * log2e)  # q component giving one log2 unit of score
+    q = np.zeros((n_tok, n_head, hd), np.float32)
+    q[..., 0] = 20.0 * u
+    q[..., 1] = (20.0 - a) * u
+    q[..., 2] = (20.0 - b) * u
+    q[..., 3] = 40.0 * u
+    q = q.reshape(n_tok, n_head * hd)
+    Kb, Vb = nh.bf16_round(K), nh.bf16_round(V)
+    pos0 = n_seq - n_tok
+    kw = dict(n_head=n_head, n_kv=n_kv, head_dim=hd, scale=scale)
+    say("case prefill fp16 weights at the copy's limit (V +-8), 256 tokens")
+    with nh.KVCache([n_seq], [hd]) as kv:
+        kv.append(0, 0, Kb, Vb)
+        got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+    want = orc.attend_layer(q, Kb, Vb, kv_bf16=True, rows=n_seq, pos0=pos0, n_seq=n_seq, **kw)
+    # the three weights per row (exact softmax of the exact scores) and the bound
+    qs = q.reshape(n_tok, n_head, hd).astype(np.float64)
+    s = scale * log2e * qs[..., :3]
+    w = np.exp2(s - s.max(axis=-1, keepdims=True))
+    w /= w.sum(axis=-1, keepdims=True)
+    out = (w * np.array([0.0, 8.0, -8.0])).sum(axis=-1)
+    bound = 2.0 ** -11 * (w * np.abs(np.array([0.0, 8.0, -8.0]) - out[..., None])).sum(axis=-1) + 2e-6
+    d = np.abs(got.astype(np.float64) - want).reshape(n_tok, n_head, hd).max(axis=-1)
+    say(f"  max-abs {d.max():.3e}; largest error / bound {(d / bound).max():.3f}; largest bound {bound.max():.3e}")
+    assert np.all(d <= bound)
+    assert d.max() <= 5e-3
+
+
 def test_fp16_shadow_follows_current_contents(monkeypatch):
     """V's fp16 copy counts its elements beyond its limit as they are written
     and replaced: once the ring row holding such a value is overwritten (by a
@@ -311,7 +362,8 @@ def test_fp16_shadow_follows_current_contents(monkeypatch):
 
 
 def test_f32_batch_uses_exact_path(orc):
-    """F32 K/V batches run the split-K kernel per token: the F32 bound holds."""
+    """F32 K/V batches above 16 tokens run the tiled fp32-MFMA kernel (exact
+    fp32 products): the F32 bound holds."""
     cfg = synth.CONFIGS["A"]
     got, want = run_case(orc, cfg, 2, n_seq=1024, pos0=1000, n_tok=24)
     assert errors(got, want)[0] <= 1e-3
