@@ -277,7 +277,6 @@ namespace nnchip
 			if (!row_ok) return;
 			if (p.n_split > 1)
 			{
-				const int PL = hd + 4;
 				float* gp = tiled_partial(p, G, hd, t, kvh, split, h);
 #pragma unroll
 				for (int d = 0; d < DT; ++d)
