@@ -6,8 +6,9 @@
 // major, so the heads of a GQA group sit in adjacent rows and share every key
 // the work-group reads. Grid: n_kv * n_qtiles work-groups. A work-group owns
 // RG row groups of 32 rows (RG = 2 at head_dim 64 and 128: 64 rows, eight
-// wavefronts, one work-group per CU; RG = 1 at head_dim 256: 32 rows, four
-// wavefronts) and walks its key range in steps of 128 keys. Wavefront
+// wavefronts, one work-group per CU; head_dim 256 runs prefill16_kernel
+// below, two row groups of 16 rows) and walks its key range in steps of 128
+// keys. Wavefront
 // (g, r) takes keys 32 g .. 32 g + 31 of each step for the 32 rows of row
 // group r, so every product is one 32 x 32 tile (v_mfma_f32_32x32x16, which
 // one wavefront keeps near the matrix peak); the row groups share each key
@@ -646,6 +647,408 @@ namespace nnchip
 			}
 		}
 
+		// head_dim 256 in 16-row tiles. 32 rows of 256 need 128 accumulator
+		// registers per lane in 32 x 32 tiles, which leaves one wavefront per
+		// SIMD; 16-row tiles on v_mfma_f32_16x16x32 need 64, so a work-group
+		// of eight wavefronts — four key groups times two row groups of 16
+		// rows — holds two per SIMD, Q (hi + lo) in registers, and the two
+		// row groups share every K and V tile (loaded once per 32 rows, as
+		// in the 32-row form; each row group issues half of every tile's
+		// DMAs). LDS: one stage of tiles (128 KiB; two would not fit beside
+		// Q's staging area), so a step waits for its tiles (barrier), takes
+		// its scores and its V^T registers, waits until every wavefront has
+		// (barrier), issues the next step's DMAs, and runs its softmax and
+		// P.V from registers while they land.
+		//   S^T = K . Q^T  per 16-key half t: lane l holds keys 16 t + 4 (l / 16)
+		//                  + i of row l % 16 (two halves, 8 scores);
+		//   P^T            the lane's 8 weights are the B operand of a 32-key
+		//                  product as they sit (k-slot 8 (l / 16) + j holds key
+		//                  4 (l / 16) + j, j < 4, and 16 + 4 (l / 16) + j - 4
+		//                  after), and V^T is read (ds_read_b64_tr_b16) in that
+		//                  key order;
+		//   O^T += V^T . P^T  16 tiles of 16 elements: lane l holds elements
+		//                  16 dt + 4 (l / 16) + i of row l % 16.
+		// The softmax, the lazy offset, V's fp16 copy and the final merge of
+		// the key groups follow the 32-row kernel. (Measured against this
+		// form on E's prefill, 25.8 ms: the tile halves pipelined — each
+		// released and reloaded by its row group while the other half runs —
+		// 53.6 ms with 23 registers spilled, whose reloads wait behind the
+		// in-flight DMAs on the shared vector-memory count, and 28.0 ms
+		// without spills, with each half's softmax and P.V on
+		// v_mfma_f32_16x16x16; K released after the scores and V after P.V
+		// in separate stages of one buffer 28.3 ms. A copy without the step
+		// DMAs ran 16.9 ms.)
+		constexpr int kH16 = 256;
+		constexpr int kRows16 = 32, kWaves16 = 8;
+		constexpr int kTile16 = kWK * kH16 * 2; // bytes of one K (or V) tile
+		constexpr int kStage16 = kKG * 2 * kTile16; // 128 KiB
+		constexpr int kQ16 = kRows16 * kH16 * 2; // one bf16 half of Q
+		constexpr int kLds16 = kStage16 + 2 * kQ16; // 160 KiB
+		constexpr int kOPitch16 = kH16 + 4;
+		constexpr int kStats16 = kLds16 - 2 * kWaves16 * 16 * 4;
+		static_assert(kWaves16 * 16 * kOPitch16 * 4 <= kStats16, "merge buffer layout");
+
+		// 16-byte slot swizzle of V tile rows for the 16-row form: the
+		// transposing reads of a 16-lane group cover 32 bytes of each of four
+		// consecutive rows, and the four groups rows 4 apart; (row ^ row / 4)
+		// % 4 puts all 16 rows' reads in distinct 64-byte bank groups.
+		__device__ __forceinline__ int vswz16(int row) { return 4 * ((row ^ (row >> 2)) & 3); }
+
+		template <int G>
+		__global__ __launch_bounds__(64 * kWaves16) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill16_kernel(
+			const prefill_params p)
+		{
+			constexpr int HD = kH16, KT = HD / 32, DT = HD / 16, LPK = HD / 8, KPL = 64 / LPK, NV = kWK / KPL,
+			              ND = NV / 2;
+			__shared__ __attribute__((aligned(16))) unsigned char s_raw[kLds16];
+
+			const int lane = threadIdx.x & 63;
+			const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+			const int kg = wave % kKG, rg = wave / kKG;
+			const int r16 = lane & 15, g4 = lane >> 4;
+
+			int bid = blockIdx.x;
+			const int n_wg = gridDim.x;
+			if ((n_wg & 7) == 0) bid = (bid & 7) * (n_wg >> 3) + (bid >> 3);
+			const int kvh = bid / p.n_qtiles;
+			const int j = bid % p.n_qtiles, half = (p.n_qtiles + 1) / 2;
+			const int qt = j < half ? p.n_qtiles - 1 - j : j - half;
+
+			const int n_rows = p.n_tok * G;
+			const int row0 = qt * kRows16;
+			const size_t q_stride = static_cast<size_t>(p.n_head) * HD;
+
+			int kmin, kmax, first_hi, last_lo;
+			{
+				const int t0 = row0 / G, t1 = min(p.n_tok - 1, (row0 + kRows16 - 1) / G);
+				attn_span(p.causal, p.window, p.pos0 + t0, p.n_seq, kmin, last_lo);
+				attn_span(p.causal, p.window, p.pos0 + t1, p.n_seq, first_hi, kmax);
+			}
+			const int my_row = row0 + 16 * rg + r16;
+			int rfirst = 1, rlast = 0;
+			if (my_row < n_rows) attn_span(p.causal, p.window, p.pos0 + my_row / G, p.n_seq, rfirst, rlast);
+
+			const int span = kmax >= kmin ? kmax - kmin + 1 : 0;
+			const int rb0 = span > 0 ? kmin % p.rows : 0;
+			const int len1 = min(span, p.rows - rb0);
+			const int len2 = span - len1;
+			const int n1 = (len1 + kStep - 1) / kStep;
+			const int n_steps = n1 + (len2 + kStep - 1) / kStep;
+			const int wrap_key = kmin + len1;
+
+			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
+			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
+			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
+			const char* vbase = static_cast<const char*>(use16 ? p.V16 : p.V) + head_bytes;
+
+			auto step_key = [&](int i, int& seg_last) __attribute__((always_inline)) -> int
+			{
+				const bool second = i >= n1;
+				seg_last = second ? kmax : wrap_key - 1;
+				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + kg * kWK;
+			};
+			const uint32_t step_bytes = static_cast<uint32_t>(kStep) * row_bytes;
+			const uint32_t seg1_off = static_cast<uint32_t>(rb0 + kg * kWK) * row_bytes;
+			const uint32_t seg2_off = static_cast<uint32_t>(kg * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
+			const uint32_t seg1_end = static_cast<uint32_t>(rb0 + len1 - 1) * row_bytes + HD * 2;
+			const uint32_t seg2_end = static_cast<uint32_t>(kmax - wrap_key) * row_bytes + HD * 2;
+			auto step_rsrc = [&](int i, const char* base) __attribute__((always_inline))
+			{
+				const bool second = i >= n1;
+				const uint32_t off = (second ? seg2_off : seg1_off) + static_cast<uint32_t>(i) * step_bytes;
+				const uint32_t end = second ? seg2_end : seg1_end;
+				const uint32_t n = __builtin_amdgcn_readfirstlane(end > off ? end - off : 0u);
+				return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + off), 0, static_cast<int>(n),
+				                                         kBufferFlags);
+			};
+
+			// The key group's K tile, then its V tile; the two row groups split
+			// each tile's DMAs (row group rg: rows 16 rg .. 16 rg + 15).
+			const int t_row = lane / LPK;
+			uint16_t* const kt = reinterpret_cast<uint16_t*>(s_raw) + kg * 2 * kWK * HD;
+			uint16_t* const vt = kt + kWK * HD;
+			auto load_tiles = [&](int i) __attribute__((always_inline))
+			{
+				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
+				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
+#pragma unroll
+				for (int e = 0; e < 2 * ND; ++e)
+				{
+					const bool is_v = e >= ND;
+					const int jj = rg * ND + (is_v ? e - ND : e);
+					const int row = jj * KPL + t_row;
+					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
+					if (is_v)
+						load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz16(row)));
+					else
+						load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
+				}
+			};
+			if (n_steps > 0) load_tiles(0);
+
+			// Q, pre-scaled into log2 units, as bf16 hi + lo in LDS (the K
+			// tiles' layout): thread t converts the sixteenth t % 16 of row t / 16.
+			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + kStage16);
+			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + kStage16 + kQ16);
+			{
+				constexpr int E = HD / 16;
+				const int qr = threadIdx.x >> 4, qseg = threadIdx.x & 15;
+				const int grow = row0 + qr;
+				const bool ok = grow < n_rows;
+				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
+				                                  static_cast<size_t>(kvh * G + grow % G) * HD + qseg * E
+				                            : 0);
+#pragma unroll
+				for (int c = 0; c < E / 8; ++c)
+				{
+					float xq[8];
+#pragma unroll
+					for (int u = 0; u < 2; ++u)
+					{
+						const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 8 * c + 4 * u)
+						                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+						xq[4 * u] = a.x * p.qscale;
+						xq[4 * u + 1] = a.y * p.qscale;
+						xq[4 * u + 2] = a.z * p.qscale;
+						xq[4 * u + 3] = a.w * p.qscale;
+					}
+					const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
+					bf16x8 hi, lo;
+					split_bf16x8(xq, hi, lo);
+					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
+					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
+				}
+			}
+			__syncthreads();
+			// Q^T as the B operand of k-step kk: lane l holds row l % 16 of the
+			// row group, elements 32 kk + 8 (l / 16) .. + 8.
+			bf16x8 qhi[KT], qlo[KT];
+			{
+				const int qrow = 16 * rg + r16;
+#pragma unroll
+				for (int kk = 0; kk < KT; ++kk)
+				{
+					const int off = qrow * HD + 8 * ((4 * kk + g4) ^ kswz<HD>(qrow));
+					qhi[kk] = *reinterpret_cast<const bf16x8*>(s_qhi + off);
+					qlo[kk] = *reinterpret_cast<const bf16x8*>(s_qlo + off);
+				}
+			}
+
+			f32x4 acc_o[DT];
+#pragma unroll
+			for (int d = 0; d < DT; ++d) acc_o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+			float l_acc = 0.0f, m_off = -INFINITY, c_init = 0.0f;
+			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+
+			// V^T for O^T tile dt, from tile rows r0 .. r0 + 15: keys r0 +
+			// 4 (l / 16) .. + 3 of element 16 dt + l % 16 (r0 = 0: k-slots
+			// 8 (l / 16) .. + 3 of the product; r0 = 16: the next four).
+			auto vt_half = [&](int dt, int r0) __attribute__((always_inline)) -> u32x2
+			{
+				const int col = 16 * dt + 4 * (r16 & 3);
+				const int slot = col >> 3, in = col & 7;
+				const int ra = r0 + 4 * g4 + (r16 >> 2);
+				return tr_read(vt + ra * HD + 8 * (slot ^ vswz16(ra)) + in);
+			};
+
+			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
+			{
+				constexpr bool F16 = decltype(f16_tag)::value;
+				for (int i = 0; i < n_steps; ++i)
+				{
+					int seg_last;
+					const int kw0 = step_key(i, seg_last);
+					dma_done();
+					__syncthreads(); // every DMA of this step has landed
+
+					f32x4 sc[2];
+					u32x4 vta[DT];
+					__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+					for (int t = 0; t < 2; ++t)
+					{
+						sc[t] = f32x4{c_init, c_init, c_init, c_init};
+						const int krow = 16 * t + r16;
+#pragma unroll
+						for (int kk = 0; kk < KT; ++kk)
+						{
+							const bf16x8 a =
+								*reinterpret_cast<const bf16x8*>(kt + krow * HD + 8 * ((4 * kk + g4) ^ kswz<HD>(krow)));
+							sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
+							sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
+						}
+					}
+#pragma unroll
+					for (int d = 0; d < DT; ++d)
+					{
+						const u32x2 lo = vt_half(d, 0), hi = vt_half(d, 16);
+						vta[d] = u32x4{lo.x, lo.y, hi.x, hi.y};
+					}
+					__builtin_amdgcn_s_setprio(0);
+					lds_reads_done();
+					__syncthreads(); // every wavefront is done with this stage
+					if (i + 1 < n_steps) load_tiles(i + 1);
+
+					// Mask keys outside the row's span or past the segment (only
+					// on steps that cross an edge).
+					if (kw0 < first_hi || kw0 + kWK - 1 > min(last_lo, seg_last))
+					{
+						const int hi_key = min(rlast, seg_last);
+#pragma unroll
+						for (int t = 0; t < 2; ++t)
+#pragma unroll
+							for (int e = 0; e < 4; ++e)
+							{
+								const int k = kw0 + 16 * t + 4 * g4 + e;
+								if (k < rfirst || k > hi_key) sc[t][e] = -INFINITY;
+							}
+					}
+					float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+					                 fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+					{
+						const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false,
+						                                                false);
+						mx = max_with_other_half(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+					}
+					const bool grow = mx > kLazy || (m_off == -INFINITY && mx != -INFINITY);
+					if (__builtin_amdgcn_ballot_w64(grow) != 0)
+					{
+						const bool fresh = m_off == -INFINITY;
+						const float d = grow ? mx - kBias : 0.0f;
+						const float alpha = fresh ? 0.0f : fast_exp2(-d);
+						if (grow) m_off = (fresh ? 0.0f : m_off) + d;
+						c_init = m_off == -INFINITY ? 0.0f : -m_off;
+#pragma unroll
+						for (int dd = 0; dd < DT; ++dd) acc_o[dd] *= alpha;
+						l_acc *= alpha;
+						sc[0] -= d;
+						sc[1] -= d;
+					}
+
+					if constexpr (F16)
+					{
+						u32x4 pw;
+#pragma unroll
+						for (int q = 0; q < 4; ++q)
+						{
+							const int t = q >> 1, e = 2 * (q & 1);
+							const uint32_t w2 = pack_f16x2(fast_exp2(sc[t][e]), fast_exp2(sc[t][e + 1]));
+							pw[q] = w2;
+							l_acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one2, l_acc, false);
+						}
+						const f16x8 pb = as_f16x8(pw);
+						__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+						for (int d = 0; d < DT; ++d) acc_o[d] = mfma16x16x32(as_f16x8(vta[d]), pb, acc_o[d]);
+						__builtin_amdgcn_s_setprio(0);
+					}
+					else
+					{
+						float w[8];
+#pragma unroll
+						for (int q = 0; q < 8; ++q)
+						{
+							w[q] = fast_exp2(sc[q >> 2][q & 3]);
+							l_acc += w[q];
+						}
+						bf16x8 phi, plo;
+						split_bf16x8(w, phi, plo);
+						__builtin_amdgcn_s_setprio(1);
+#pragma unroll
+						for (int d = 0; d < DT; ++d)
+						{
+							acc_o[d] = mfma16x16x32(as_bf16x8(vta[d]), phi, acc_o[d]);
+							acc_o[d] = mfma16x16x32(as_bf16x8(vta[d]), plo, acc_o[d]);
+						}
+						__builtin_amdgcn_s_setprio(0);
+					}
+				}
+			};
+			if (use16)
+				key_loop(std::true_type{});
+			else
+				key_loop(std::false_type{});
+
+			// Merge the key groups of each row group (as the 32-row kernel).
+			float* s_m = reinterpret_cast<float*>(s_raw + kStats16); // [kWaves16][16]
+			float* s_l = s_m + kWaves16 * 16;
+			const float l_row = add_with_other_half(add_with_other_row(l_acc));
+			__syncthreads(); // the tiles and Q's staging area are free
+			if (g4 == 0)
+			{
+				s_m[wave * 16 + r16] = m_off;
+				s_l[wave * 16 + r16] = l_row;
+			}
+			__syncthreads();
+			float* s_o = reinterpret_cast<float*>(s_raw);
+			{
+				const float* sm = s_m + rg * kKG * 16 + r16;
+				const float* sl = s_l + rg * kKG * 16 + r16;
+				float M = sm[0];
+#pragma unroll
+				for (int w = 1; w < kKG; ++w) M = fmaxf(M, sm[w * 16]);
+				float L = 0.0f, f_own = 0.0f;
+#pragma unroll
+				for (int w = 0; w < kKG; ++w)
+				{
+					const float mw = sm[w * 16];
+					const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+					L = fmaf(sl[w * 16], f, L);
+					if (w == kg) f_own = f;
+				}
+				const float sc_own = L > 0.0f ? f_own / L : 0.0f;
+				float* orow = s_o + (wave * 16 + r16) * kOPitch16 + 4 * g4;
+#pragma unroll
+				for (int d = 0; d < DT; ++d)
+					*reinterpret_cast<float4*>(orow + 16 * d) =
+						make_float4(acc_o[d][0] * sc_own, acc_o[d][1] * sc_own, acc_o[d][2] * sc_own, acc_o[d][3] * sc_own);
+			}
+			__syncthreads();
+			constexpr int Q4 = HD / 4;
+			for (int idx = threadIdx.x; idx < kRows16 * Q4; idx += 64 * kWaves16)
+			{
+				const int r = idx / Q4, d4 = idx % Q4;
+				const int gr = row0 + r;
+				if (gr >= n_rows) continue;
+				// row r is row r % 16 of row group r / 16, kept by its kKG wavefronts
+				const float* o0 = s_o + ((r / 16) * kKG * 16 + r % 16) * kOPitch16 + 4 * d4;
+				float4 acc = *reinterpret_cast<const float4*>(o0);
+#pragma unroll
+				for (int w = 1; w < kKG; ++w)
+				{
+					const float4 v = *reinterpret_cast<const float4*>(o0 + w * 16 * kOPitch16);
+					acc.x += v.x;
+					acc.y += v.y;
+					acc.z += v.z;
+					acc.w += v.w;
+				}
+				const size_t oi = static_cast<size_t>(gr / G) * q_stride + static_cast<size_t>(kvh * G + gr % G) * HD + 4 * d4;
+				if (p.gate)
+				{
+					acc.x = gated(acc.x, p.gate, oi);
+					acc.y = gated(acc.y, p.gate, oi + 1);
+					acc.z = gated(acc.z, p.gate, oi + 2);
+					acc.w = gated(acc.w, p.gate, oi + 3);
+				}
+				*reinterpret_cast<float4*>(p.out + oi) = acc;
+			}
+		}
+
+		bool launch_hd256_16(prefill_params p, int group, hipStream_t stream)
+		{
+			p.n_qtiles = (p.n_tok * group + kRows16 - 1) / kRows16;
+			const dim3 grid(p.n_qtiles * p.n_kv), block(64 * kWaves16);
+			switch (group)
+			{
+			case 1: prefill16_kernel<1><<<grid, block, 0, stream>>>(p); return true;
+			case 2: prefill16_kernel<2><<<grid, block, 0, stream>>>(p); return true;
+			case 4: prefill16_kernel<4><<<grid, block, 0, stream>>>(p); return true;
+			case 8: prefill16_kernel<8><<<grid, block, 0, stream>>>(p); return true;
+			default: return false;
+			}
+		}
+
 		template <int HD, int RG>
 		bool launch_hd(prefill_params p, int group, hipStream_t stream)
 		{
@@ -670,7 +1073,7 @@ namespace nnchip
 		{
 		case 64: return launch_hd<64, 2>(p, group, stream);
 		case 128: return launch_hd<128, 2>(p, group, stream);
-		case 256: return launch_hd<256, 1>(p, group, stream);
+		case 256: return launch_hd256_16(p, group, stream);
 		default: return false;
 		}
 	}
