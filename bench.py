@@ -117,9 +117,10 @@ def cpu_baseline(cache_l0, target_s: float, samples: dict) -> dict:
     reference nn_ops.cpp:865-879) and nproc capped at 64 (nn_ops.cpp:786),
     the latter also held to the CPUs this process may use. The first is the
     reported value. Prefill: chunk 7 of layer 0 (512 tokens at keys 0 ..
-    4095), the GPU's output of the same call. B decode at 16384 keys and C's
-    26-layer decode step at 8192 (22 windowed local layers, 4 global), on
-    synthetic rows of their shapes, at the default setting."""
+    4095), the GPU's output of the same call. B decode at 16384 keys, C's
+    26-layer decode step at 8192 (22 windowed local layers, 4 global), A's
+    F32 decode step and E's decode step after its prompt, on synthetic rows
+    of their shapes, at the default setting."""
     import oracle
 
     K, V = cache_l0
@@ -165,11 +166,13 @@ def cpu_baseline(cache_l0, target_s: float, samples: dict) -> dict:
     rng = np.random.default_rng(5)
 
     def decode_layer_s(cfg, rows, window, span_keys):
-        Kb = nh_bf16(rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32))
-        Vb = nh_bf16(rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32))
+        Kb = rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32)
+        Vb = rng.standard_normal((rows, cfg.kv_dim)).astype(np.float32)
+        if cfg.kv_bf16:
+            Kb, Vb = nh_bf16(Kb), nh_bf16(Vb)
         q = rng.standard_normal((1, cfg.n_head * cfg.head_dim)).astype(np.float32)
-        kw = dict(kv_bf16=True, rows=rows, pos0=span_keys - 1, n_seq=span_keys, window=window, n_head=cfg.n_head,
-                  n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+        kw = dict(kv_bf16=cfg.kv_bf16, rows=rows, pos0=span_keys - 1, n_seq=span_keys, window=window,
+                  n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
         return best_of(t_default, 1.0, q, Kb, Vb, **kw)[1]
 
     B, Cc = synth.CONFIGS["B"], synth.CONFIGS["C"]
@@ -181,6 +184,18 @@ def cpu_baseline(cache_l0, target_s: float, samples: dict) -> dict:
     c_step = n_local * c_local + (Cc.n_layer - n_local) * c_global
     c_bytes = sum(decode_layer_bytes(int(layer_spans(Cc, li, 8191, 1)[0]), Cc.n_kv, Cc.head_dim, Cc.n_head, 2)
                   for li in range(Cc.n_layer))
+    # A's decode step (F32, 18 layers at 1024 keys) and one of E's 256 decode
+    # steps after the 16384-token prompt (at position 16511, the middle one)
+    A, E = synth.CONFIGS["A"], synth.CONFIGS["E"]
+    a_step = A.n_layer * decode_layer_s(A, 1024, 0, 1024)
+    a_bytes = A.n_layer * decode_layer_bytes(1024, A.n_kv, A.head_dim, A.n_head, 4)
+    e_pos, e_ctx = 16511, 16384 + 256
+    e_local_n = sum(1 for li in range(E.n_layer) if E.layer_window(li) > 0)
+    e_local = decode_layer_s(E, E.layer_rows(0, e_ctx, 1024), E.window, e_pos + 1)
+    e_global = decode_layer_s(E, e_ctx, 0, e_pos + 1)
+    e_step = e_local_n * e_local + (E.n_layer - e_local_n) * e_global
+    e_bytes = sum(decode_layer_bytes(int(layer_spans(E, li, e_pos, 1)[0]), E.n_kv, E.head_dim, E.n_head, 2)
+                  for li in range(E.n_layer))
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": t_default, "kind": kind,
             "sample": f"decode of one Qwen3-4B layer at {CTX} keys (layer 0 of the timed step), best of {n} runs "
                       f"over {target_s:.0f} s (the reference's kernels and worker pool)",
@@ -196,6 +211,13 @@ def cpu_baseline(cache_l0, target_s: float, samples: dict) -> dict:
                               "ms_per_step": round(c_step * 1e3, 3),
                               "sample": f"{n_local} local (window {Cc.window}) and {Cc.n_layer - n_local} global "
                                         f"Gemma-3-1B layers at 8192, synthetic rows"},
+            "A_decode_1024": {"value": round(a_bytes / a_step / 1e9, 2), "unit": "GB/s", "cores": t_default,
+                              "ms_per_step": round(a_step * 1e3, 3),
+                              "sample": "18 Gemma-3-270M layers (F32 K/V) at 1024 keys, synthetic rows"},
+            "E_decode_256": {"value": round(e_bytes / e_step / 1e9, 2), "unit": "GB/s", "cores": t_default,
+                             "ms_per_step": round(e_step * 1e3, 3),
+                             "sample": f"the decode step at position {e_pos}: {e_local_n} local (window {E.window}) and "
+                                       f"{E.n_layer - e_local_n} global Gemma-3-4B layers, synthetic rows"},
             "parity": {"against": kind, "rel": "|d| / (1 + |ref|)",
                        "decode_layer0_32768": parity_of(samples["decode_out"], ref_dec),
                        "prefill_layer0_chunk7": parity_of(samples["prefill_out"], ref_pre),
