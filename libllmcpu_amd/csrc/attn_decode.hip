@@ -429,9 +429,10 @@ namespace nnchip
 		// o * (1 / l) (0 when l == 0, reference nn_ops.cpp:492), columns
 		// COLS * slice .. + COLS - 1 of it. Lane t owns float4 column
 		// COLS * slice + t % COLS of o for the splits of part t / COLS, whose
-		// o, m and l it loads together (16 splits per batch), so the common
-		// case is one round trip to memory and one barrier. Every element goes
-		// through the same operations whatever SLICES is.
+		// o, m and l it loads together (B splits per batch: 16, or 32 when a
+		// part has more than 16), so the common case is one round trip to
+		// memory and one barrier. Every element goes through the same
+		// operations whatever SLICES and B are.
 		// (For one token, four one-wavefront work-groups per head spread the
 		// reads over more CUs than one 256-thread work-group: 0.5 us less per
 		// call at 64 splits; for 16 tokens they are 2.9 us slower.) A split belongs to part (its absolute number,
@@ -442,12 +443,12 @@ namespace nnchip
 		// and the parts are fixed by the absolute split grid, so a token's
 		// result depends only on its own splits, whatever else the launch
 		// covered.
-		template <int HD, int G, int SLICES>
+		template <int HD, int G, int SLICES, int B>
 		__device__ __forceinline__ void merge_splits(const decode_params& p, int tok, int qh, int slice,
 		                                             merge_lds<HD, SLICES>& sh)
 		{
 			using S = merge_lds<HD, SLICES>;
-			constexpr int PL = part_pitch<HD>(), COLS = S::COLS, PARTS = S::PARTS, B = 16;
+			constexpr int PL = part_pitch<HD>(), COLS = S::COLS, PARTS = S::PARTS;
 			const int kvh = qh / G, h = qh % G;
 			const int ns = p.n_split;
 			const int c = threadIdx.x % COLS, part = threadIdx.x / COLS, d4 = COLS * slice + c;
@@ -472,12 +473,22 @@ namespace nnchip
 					ml[u] = *reinterpret_cast<const float2*>(sp + HD);
 				}
 			};
+			// The part's largest m: the first batch's, then the further
+			// splits' in batches of B independent loads (one round trip each).
 			load_batch(0);
 			float mp = -INFINITY;
 #pragma unroll
 			for (int u = 0; u < B; ++u)
 				if (u < n_mine) mp = fmaxf(mp, ml[u].x);
-			for (int i = B; i < n_mine; ++i) mp = fmaxf(mp, hp[(s_first + PARTS * i) * sstride + HD]);
+			for (int b0 = B; b0 < n_mine; b0 += B)
+			{
+				float mb[B];
+#pragma unroll
+				for (int u = 0; u < B; ++u) mb[u] = hp[min(s_first + PARTS * (b0 + u), ns - 1) * sstride + HD];
+#pragma unroll
+				for (int u = 0; u < B; ++u)
+					if (b0 + u < n_mine) mp = fmaxf(mp, mb[u]);
+			}
 			const float m_use = mp == -INFINITY ? 0.0f : mp;
 			float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 			float L = 0.0f;
@@ -541,11 +552,24 @@ namespace nnchip
 		// device-coherent loads, measured slower: 35 vs 32 us per call at 32k
 		// keys, the coherent loads and the polling being slower than the
 		// launch boundary.)
-		template <int HD, int G, int SLICES>
+		template <int HD, int G, int SLICES, int B>
 		__global__ __launch_bounds__(256 / SLICES) void decode_merge_kernel(const decode_params p)
 		{
 			__shared__ merge_lds<HD, SLICES> sh;
-			merge_splits<HD, G, SLICES>(p, blockIdx.y, blockIdx.x / SLICES, blockIdx.x % SLICES, sh);
+			merge_splits<HD, G, SLICES, B>(p, blockIdx.y, blockIdx.x / SLICES, blockIdx.x % SLICES, sh);
+		}
+
+		// The merge over (n_kv * G * SLICES, n_tok) work-groups, 32 splits per
+		// batch when a part has more than 16 (one round trip fewer per 32).
+		template <int HD, int G, int SLICES>
+		void launch_merge(const decode_params& p, int n_tok, hipStream_t stream)
+		{
+			constexpr int PARTS = 1024 / HD;
+			const dim3 grid(p.n_kv * G * SLICES, n_tok);
+			if (p.n_split > 16 * PARTS)
+				decode_merge_kernel<HD, G, SLICES, 32><<<grid, merge_lds<HD, SLICES>::THREADS, 0, stream>>>(p);
+			else
+				decode_merge_kernel<HD, G, SLICES, 16><<<grid, merge_lds<HD, SLICES>::THREADS, 0, stream>>>(p);
 		}
 
 		// F32 K/V: scores on MFMA with both operands split into bf16 hi + lo
@@ -1467,10 +1491,9 @@ namespace nnchip
 			if (fused_merge_on(p))
 				return;
 			if (p.n_split > 1 && p.n_kv * G * n_tok <= 64)
-				decode_merge_kernel<HD, G, 4>
-					<<<dim3(p.n_kv * G * 4, n_tok), merge_lds<HD, 4>::THREADS, 0, stream>>>(p);
+				launch_merge<HD, G, 4>(p, n_tok, stream);
 			else if (p.n_split > 1)
-				decode_merge_kernel<HD, G, 1><<<dim3(p.n_kv * G, n_tok), merge_lds<HD, 1>::THREADS, 0, stream>>>(p);
+				launch_merge<HD, G, 1>(p, n_tok, stream);
 		}
 
 		template <int HD, bool BF16>
@@ -1496,6 +1519,18 @@ namespace nnchip
 		case 64: return lanes * (bf16 ? bf16_chunk(64) : f32_shape<64>::CH);
 		case 128: return lanes * (bf16 ? bf16_chunk(128) : f32_shape<128>::CH);
 		case 256: return lanes * (bf16 ? bf16_chunk(256) : f32_shape<256>::CH);
+		default: return 0;
+		}
+	}
+
+	int decode_chunk_keys(int head_dim, int group, bool bf16)
+	{
+		if (!mfma_shape(head_dim, group)) return 256;
+		switch (head_dim)
+		{
+		case 64: return bf16 ? bf16_chunk(64) : f32_shape<64>::CH;
+		case 128: return bf16 ? bf16_chunk(128) : f32_shape<128>::CH;
+		case 256: return bf16 ? bf16_chunk(256) : f32_shape<256>::CH;
 		default: return 0;
 		}
 	}

@@ -74,6 +74,10 @@ namespace nnchip
 	// generic kernels).
 	int decode_groups(int n_kv, bool bf16, int head_dim, int group);
 	int decode_wg_keys(int head_dim, int group, bool bf16, int n_kv);
+	// Keys of one wavefront chunk: a split may be any multiple of it (a
+	// split shorter than decode_wg_keys leaves some wavefronts without a
+	// chunk).
+	int decode_chunk_keys(int head_dim, int group, bool bf16);
 
 	// Launches the decode kernel over an (n_split, head groups, token groups)
 	// grid, then (n_split > 1) the split merge over (n_kv * group * slices, n_tok);

@@ -365,17 +365,32 @@ namespace
 		return NNC_OK;
 	}
 
+	// Shortest split, in wavefront chunks: what one CU keeps in flight
+	// bounds a work-group's loads (about 17 bytes per clock measured with
+	// 128 KiB per CU), so a short span goes to more work-groups with fewer
+	// keys each rather than to fewer CUs.
+	constexpr int kSplitFloorChunks = 1;
+	// Most splits of one (token, head group): more work-groups than this
+	// cost more in the merge than they gain (a one-KV-head layer at 8192
+	// keys: 12.5 us with 128 splits, 15.5 with 256).
+	constexpr long long kSplitsPerGroupMax = 128;
+
 	// Keys per decode work-group for the span [kmin, kmax] shared out over
-	// `pairs` (token, head group) pairs: about one work-group per CU, a
-	// multiple of what one work-group iteration consumes, at most
-	// kDecodeMaxSplits splits.
-	int split_keys_for(const nnc_hip_kv* kv, int kmin, int kmax, long long pairs, int wgk)
+	// `pairs` (token, head group) pairs: about one work-group per CU (at
+	// most kSplitsPerGroupMax per pair), a multiple of what one work-group
+	// iteration consumes (wgk) or, for short spans, of one wavefront chunk
+	// (unit), at most kDecodeMaxSplits splits.
+	int split_keys_for(const nnc_hip_kv* kv, int kmin, int kmax, long long pairs, int wgk, int unit)
 	{
 		const int span = std::max(1, kmax - kmin + 1);
-		const long long want = std::max<long long>(1, 1LL * kv->n_cu / std::max<long long>(pairs, 1));
+		const long long want =
+			std::min(kSplitsPerGroupMax, std::max<long long>(1, 1LL * kv->n_cu / std::max<long long>(pairs, 1)));
 		long long sk = (span + want - 1) / want;
-		sk = std::max<long long>(wgk, (sk + wgk - 1) / wgk * wgk);
-		while ((kmax / sk) - (kmin / sk) + 1 > nnchip::kDecodeMaxSplits) sk += wgk;
+		if (sk < wgk)
+			sk = std::min<long long>(wgk, std::max<long long>(kSplitFloorChunks * unit, (sk + unit - 1) / unit * unit));
+		else
+			sk = (sk + wgk - 1) / wgk * wgk;
+		while ((kmax / sk) - (kmin / sk) + 1 > nnchip::kDecodeMaxSplits) sk += sk < wgk ? unit : wgk;
 		return static_cast<int>(sk);
 	}
 
@@ -518,6 +533,7 @@ namespace
 	                 int32_t n_kv, int32_t head_dim, int group, std::vector<decode_plan>& plan)
 	{
 		const int wgk = nnchip::decode_wg_keys(head_dim, group, kv->bf16, n_kv);
+		const int unit = nnchip::decode_chunk_keys(head_dim, group, kv->bf16);
 		const int groups = nnchip::decode_groups(n_kv, kv->bf16, head_dim, group);
 		auto span_of = [&](int32_t t, int& first, int& last)
 		{ nnchip::attn_span(causal ? 1 : 0, window, pos0 + t, n_seq, first, last); };
@@ -525,7 +541,7 @@ namespace
 		{
 			int first, last;
 			span_of(t, first, last);
-			return split_keys_for(kv, first, last, groups, wgk);
+			return split_keys_for(kv, first, last, groups, wgk, unit);
 		};
 		for (int32_t t = 0; t < n_tok;)
 		{
@@ -558,7 +574,8 @@ namespace
 			nnchip::attn_span(causal ? 1 : 0, window, pos0 + t0 + nt - 1, n_seq, unused, kmax);
 			const int sk =
 				split_keys_for(kv, kmin, kmax, static_cast<long long>(nt) * nnchip::decode_groups(n_kv, kv->bf16, head_dim, group),
-				               nnchip::decode_wg_keys(head_dim, group, kv->bf16, n_kv));
+				               nnchip::decode_wg_keys(head_dim, group, kv->bf16, n_kv),
+				               nnchip::decode_chunk_keys(head_dim, group, kv->bf16));
 			plan.push_back({t0, nt, sk});
 		}
 	}
