@@ -1262,36 +1262,44 @@ namespace nnchip
 				}
 			};
 
+			// Q^T of every tile of each head into LDS as the B operands, scaled
+			// into log2 units and split into bf16 hi + lo (entry (head, tl, kk, l)
+			// is lane l's 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
+			// Every Q load goes out first, then the first chunk's K and V rows,
+			// so the conversion waits for Q alone (loads complete in order) and
+			// nothing waits for a round trip per entry.
+			constexpr int kQItems = HPW * NTL * KK * 64 / (64 * W);
+			static_assert(kQItems * 64 * W == HPW * NTL * KK * 64, "Q entries per thread");
+			float4 qa[kQItems], qb[kQItems];
+#pragma unroll
+			for (int u = 0; u < kQItems; ++u)
+			{
+				const int i = threadIdx.x + u * 64 * W;
+				const int l = i & 63, kk = (i >> 6) % KK, tl = ((i >> 6) / KK) % NTL, qh = (i >> 6) / (KK * NTL);
+				const int gc = 16 * tl + (l & 15), tt = gc / G;
+				// (a column past the batch reads its group's first token and is zeroed below)
+				const float* qp = p.q +
+				                  (static_cast<size_t>(tok0 + (tt < n_tt ? tt : 0)) * p.n_head +
+				                   head_of<HPW>(hg, qh, p.n_kv) * G + gc % G) * HD +
+				                  32 * kk + 8 * (l >> 4);
+				qa[u] = *reinterpret_cast<const float4*>(qp);
+				qb[u] = *reinterpret_cast<const float4*>(qp + 4);
+			}
 			if (has_chunk)
 			{
 				load_k(c_wave);
 				load_v(c_wave);
 			}
-
-			// Q^T of every tile of each head into LDS as the B operands, scaled
-			// into log2 units and split into bf16 hi + lo (entry (head, tl, kk, l)
-			// is lane l's 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
-			for (int i = threadIdx.x; i < HPW * NTL * KK * 64; i += 64 * W)
+#pragma unroll
+			for (int u = 0; u < kQItems; ++u)
 			{
+				const int i = threadIdx.x + u * 64 * W;
 				const int l = i & 63, kk = (i >> 6) % KK, tl = ((i >> 6) / KK) % NTL, qh = (i >> 6) / (KK * NTL);
-				const int gc = 16 * tl + (l & 15), tt = gc / G;
-				float x[8];
-				if (tt < n_tt)
-				{
-					const float* qp = p.q + (static_cast<size_t>(tok0 + tt) * p.n_head + head_of<HPW>(hg, qh, p.n_kv) * G + gc % G) * HD +
-					                  32 * kk + 8 * (l >> 4);
-					const float4 a = *reinterpret_cast<const float4*>(qp);
-					const float4 b = *reinterpret_cast<const float4*>(qp + 4);
-					x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-					x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+				const int tt = (16 * tl + (l & 15)) / G;
+				const bool real = tt < n_tt;
+				float x[8] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w, qb[u].x, qb[u].y, qb[u].z, qb[u].w};
 #pragma unroll
-					for (int j = 0; j < 8; ++j) x[j] *= p.qscale;
-				}
-				else
-				{
-#pragma unroll
-					for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-				}
+				for (int j = 0; j < 8; ++j) x[j] = real ? x[j] * p.qscale : 0.0f;
 				bf16x8 hi, lo;
 				split_bf16x8(x, hi, lo);
 				s_q[qh][tl][kk][0][l] = __builtin_bit_cast(u32x4, hi);
