@@ -625,7 +625,7 @@ namespace nnchip
 				cbase = sbase + c * CH;
 				clo = max(s0, cbase);
 				chi = min(s1, cbase + CH - 1);
-				rb = clo % p.rows;
+				rb = clo < p.rows ? clo : clo % p.rows; // (no division unless the buffer is a ring that wrapped)
 			};
 			auto load_k = [&](int cbase, int clo, int chi, int rb) __attribute__((always_inline))
 			{
@@ -939,7 +939,17 @@ namespace nnchip
 			const int hh = wave % HPW, hlane = wave / HPW; // this wavefront's head in the work-group, its lane
 			const int n_hg = p.n_kv / HPW, n_zg = (p.n_tok + T - 1) / T;
 			int hg, split, zg;
-			wg_coords(blockIdx.x, p.n_split, n_hg, n_zg, hg, split, zg);
+			if constexpr (T == 1)
+			{
+				// One token: a (head group, split) grid, head groups fastest in
+				// dispatch order as wg_coords deals them, without its divisions.
+				hg = blockIdx.x;
+				split = blockIdx.y;
+				zg = 0;
+				(void)n_zg;
+			}
+			else
+				wg_coords(blockIdx.x, p.n_split, n_hg, n_zg, hg, split, zg);
 			const int kvh = head_of<HPW>(hg, hh, p.n_kv);
 			const int tok0 = zg * T;
 			const int n_tt = min(T, p.n_tok - tok0); // tokens of this work-group
@@ -978,7 +988,7 @@ namespace nnchip
 				cbase = sbase + c * CH;
 				clo = max(s0, cbase);
 				chi = min(s1, cbase + CH - 1);
-				rb = clo % p.rows;
+				rb = clo < p.rows ? clo : clo % p.rows; // (no division unless the buffer is a ring that wrapped)
 			};
 			using regs = chunk_regs<NT, KK, NV>;
 			// The i-th chunk of the wavefront (dead past its last one).
@@ -1228,7 +1238,7 @@ namespace nnchip
 				cbase = sbase + c * CH;
 				clo = max(s0, cbase);
 				chi = min(s1, cbase + CH - 1);
-				rb = clo % p.rows;
+				rb = clo < p.rows ? clo : clo % p.rows; // (no division unless the buffer is a ring that wrapped)
 			};
 			// Loads are never under a branch (a conditional load makes the
 			// compiler wait for it, or move the buffer out of registers, where
@@ -1469,7 +1479,7 @@ namespace nnchip
 					constexpr int HPW = decltype(hpw_tag)::value;
 					const int n_hg = p.n_kv / HPW;
 					if (n_tok == 1)
-						decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1, HPW><<<p.n_split * n_hg, 256, 0, stream>>>(p);
+						decode_bf16_kernel<HD, G, 4, bf16_chunk(HD), 1, HPW><<<dim3(n_hg, p.n_split), 256, 0, stream>>>(p);
 					else
 					{
 						bool multi = false;
