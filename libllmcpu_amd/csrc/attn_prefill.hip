@@ -643,7 +643,9 @@ namespace nnchip
 					acc.z = gated(acc.z, p.gate, oi + 2);
 					acc.w = gated(acc.w, p.gate, oi + 3);
 				}
-				*reinterpret_cast<float4*>(p.out + oi) = acc;
+				// non-temporal: written toward HBM as each work-group finishes,
+				// not left dirty in L2 for the end of the kernel to write back
+				store_stream(p.out + oi, acc);
 			}
 		}
 
@@ -1031,7 +1033,9 @@ namespace nnchip
 					acc.z = gated(acc.z, p.gate, oi + 2);
 					acc.w = gated(acc.w, p.gate, oi + 3);
 				}
-				*reinterpret_cast<float4*>(p.out + oi) = acc;
+				// non-temporal: written toward HBM as each work-group finishes,
+				// not left dirty in L2 for the end of the kernel to write back
+				store_stream(p.out + oi, acc);
 			}
 		}
 
