@@ -1238,7 +1238,7 @@ namespace nnchip
 				cbase = sbase + c * CH;
 				clo = max(s0, cbase);
 				chi = min(s1, cbase + CH - 1);
-				rb = clo < p.rows ? clo : clo % p.rows; // (no division unless the buffer is a ring that wrapped)
+				rb = clo % p.rows; // (a select here costs this kernel registers it does not have)
 			};
 			// Loads are never under a branch (a conditional load makes the
 			// compiler wait for it, or move the buffer out of registers, where
