@@ -34,6 +34,13 @@ CASES = [
     (synth.CONFIGS["A"], 0, 1000, 16),  # F32 K/V
     (G8, 0, 3000, 16),
     (G1, 0, 1500, 16),
+    # batches across a change of split size where short spans take splits of
+    # one wavefront chunk (one-token split at the first span, a longer one at
+    # the last)
+    (synth.CONFIGS["D"], 3, 4088, 16),  # 64-key splits up to 4096 keys, 128 after
+    (synth.CONFIGS["B"], 1, 4090, 16),  # hd 64: 64 -> 128
+    (synth.CONFIGS["C"], 11, 4090, 9),  # hd 256, one KV head: 32 -> 64
+    (synth.CONFIGS["A"], 1, 2040, 16),  # F32 hd 256: 16 -> 32
 ]
 
 
