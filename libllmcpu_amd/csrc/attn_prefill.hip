@@ -29,14 +29,18 @@
 //     bf16 hi + lo, two MFMAs per product, near-fp32.
 // Per step, a key group's 32 K rows and 32 V rows arrive in its LDS tiles
 // by LDS-DMA (buffer_load ... lds, 16 bytes per lane, rows XOR-swizzled in
-// 16-byte slots so the reads below are conflict-free), issued during the
-// previous step (RG = 2: two stages, the DMAs split between the row groups,
-// one barrier per step; RG = 1: each wavefront's own tiles, one stage):
+// 16-byte slots so the reads below are conflict-free; the fp16 copy's tile
+// is one 32-row group of its blocked layout, f16_copy_index, as it lies),
+// issued during the previous step (RG = 2: two stages, the DMAs split
+// between the row groups, one barrier per step; RG = 1: each wavefront's
+// own tiles, one stage). With the copy the walk starts at the key range's
+// first key rounded down to 32, so every tile is a whole group:
 //   S^T = K . Q^T      v_mfma_f32_32x32x16, K rows as the A operand and Q^T
 //                      as B. The accumulator starts at -m (the row's running
 //                      offset), so the scores come out already shifted.
-//                      Meanwhile V^T is read back transposed
-//                      (ds_read_b64_tr_b16) into registers;
+//                      Meanwhile V^T is read into registers: from the
+//                      copy's blocks with plain 16-byte reads, from the bf16
+//                      V transposed (ds_read_b64_tr_b16);
 //   softmax            in fp32 and log2 units, weights exp2(s - m) with the
 //                      row's offset m set 8 below its largest score so far:
 //                      m is raised only when a score passes it by more than
@@ -234,25 +238,37 @@ namespace nnchip
 			int rfirst = 1, rlast = 0; // no key
 			if (my_row < n_rows) attn_span(p.causal, p.window, p.pos0 + my_row / G, p.n_seq, rfirst, rlast);
 
-			// The key range as contiguous segments of rows: keys kmin .. from row
+			// V's fp16 copy when the buffer has one and every value now in it
+			// is within the copy's limit (and, in a buffer whose rows are not a
+			// whole number of the copy's 32-row groups, the range does not
+			// wrap); else the bf16 V itself. The copy's tiles are whole groups,
+			// so with it the walk starts at kmin rounded down to 32 (the keys
+			// before kmin are masked like any outside a row's span).
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0 &&
+			                   ((p.rows & 31) == 0 || kmax < p.rows);
+			const int kbeg = use16 ? kmin & ~31 : kmin;
+
+			// The key range as contiguous segments of rows: keys kbeg .. from row
 			// rb0 up to the buffer's end, then (a ring that wraps) the rest from
-			// row 0. The host guarantees the range is shorter than the buffer.
-			const int span = kmax >= kmin ? kmax - kmin + 1 : 0;
-			const int rb0 = span > 0 ? kmin % p.rows : 0;
+			// row 0. The host guarantees the range is shorter than the buffer
+			// (kmin .. kmax; the keys before kmin may alias rows of the last
+			// ones, and are masked).
+			const int span = kmax >= kmin ? kmax - kbeg + 1 : 0;
+			const int rb0 = span > 0 ? kbeg % p.rows : 0;
 			const int len1 = min(span, p.rows - rb0);
 			const int len2 = span - len1;
 			const int n1 = (len1 + kStep - 1) / kStep;
 			const int n_steps = n1 + (len2 + kStep - 1) / kStep;
-			const int wrap_key = kmin + len1; // segment 2's first key
+			const int wrap_key = kbeg + len1; // segment 2's first key
 
 			// Byte offsets are 32-bit (the host keeps a buffer under 2 GiB).
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
-			// V's fp16 copy when the buffer has one and every value now in it
-			// is within the copy's limit; else the bf16 V itself.
-			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
 			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
-			const char* vbase = static_cast<const char*>(use16 ? p.V16 : p.V) + head_bytes;
+			// (the copy's blocks hold 8 rows of each column: a head's columns
+			// start 8 times as far in)
+			const char* vbase = use16 ? static_cast<const char*>(p.V16) + 8 * head_bytes
+			                          : static_cast<const char*>(p.V) + head_bytes;
 
 			// Step i of the wavefront: its first key and the last key of its
 			// segment; its descriptors are based at the block's first row and in
@@ -261,7 +277,7 @@ namespace nnchip
 			{
 				const bool second = i >= n1;
 				seg_last = second ? kmax : wrap_key - 1;
-				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + kg * kWK;
+				return (second ? wrap_key + (i - n1) * kStep : kbeg + i * kStep) + kg * kWK;
 			};
 			// In bytes from the buffer's start: the wavefront's block at step i
 			// is at seg_off + i * step_bytes (seg_off per segment: the block of
@@ -273,11 +289,21 @@ namespace nnchip
 			const uint32_t seg2_off = static_cast<uint32_t>(kg * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
 			const uint32_t seg1_end = static_cast<uint32_t>(rb0 + len1 - 1) * row_bytes + HD * 2;
 			const uint32_t seg2_end = static_cast<uint32_t>(kmax - wrap_key) * row_bytes + HD * 2; // used when len2 > 0
-			auto step_rsrc = [&](int i, const char* base) __attribute__((always_inline))
+			// The same in the fp16 copy: a 32-row group takes the bytes of 32
+			// rows, so a group starts where its first row would; a segment
+			// ends with its last group's last block (rows past the segment in
+			// that group are read and masked).
+			auto group_end = [&](int last_row) __attribute__((always_inline)) -> uint32_t
+			{
+				return static_cast<uint32_t>(last_row >> 5) * 32 * row_bytes + 48 * row_bytes / 2 + 16 * HD;
+			};
+			const uint32_t v_seg1_end = use16 ? group_end(rb0 + len1 - 1) : seg1_end;
+			const uint32_t v_seg2_end = use16 ? group_end(kmax - wrap_key) : seg2_end;
+			auto step_rsrc = [&](int i, const char* base, bool is_v) __attribute__((always_inline))
 			{
 				const bool second = i >= n1;
 				const uint32_t off = (second ? seg2_off : seg1_off) + static_cast<uint32_t>(i) * step_bytes;
-				const uint32_t end = second ? seg2_end : seg1_end;
+				const uint32_t end = is_v ? (second ? v_seg2_end : v_seg1_end) : (second ? seg2_end : seg1_end);
 				// (the clamp becomes a VALU saturating subtract: readfirstlane keeps
 				// the descriptor in SGPRs)
 				const uint32_t n = __builtin_amdgcn_readfirstlane(end > off ? end - off : 0u);
@@ -299,10 +325,16 @@ namespace nnchip
 			// DMAs e0 .. e1 - 1 of this wavefront's 2 ND for step i: its K DMAs,
 			// then its V DMAs (so a step's loads can be spread over the step).
 			constexpr int ND = NV / RG;
-			auto load_part = [&](int i, int e0, int e1) __attribute__((always_inline))
+			// In the fp16 copy, tile byte 1024 jj + 16 l (DMA jj) is byte w of
+			// block b = jj / (HD / 64) (a block is 16 HD bytes), which lies
+			// 16 kv_dim b + w past the group's start.
+			static_assert(16 * HD % 1024 == 0, "the fp16 copy's blocks are whole DMAs");
+			constexpr int DPB = 16 * HD / 1024; // DMAs per block of the copy
+			auto load_part = [&](auto f16_tag, int i, int e0, int e1) __attribute__((always_inline))
 			{
-				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
-				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
+				constexpr bool F16 = decltype(f16_tag)::value;
+				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase, false);
+				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase, true);
 				uint16_t* kt = k_tile(i);
 				uint16_t* vt = kt + kWK * HD;
 				// Each group of four DMAs shares one LDS base (the instruction
@@ -315,15 +347,23 @@ namespace nnchip
 					const int jj = rg * ND + (is_v ? e - ND : e);
 					const int row = jj * KPL + t_row;
 					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					if (is_v)
+					if (is_v && F16)
+						load_lds16_grouped(rv, vt, jj, (jj / DPB) * 8 * row_bytes + 1024u * (jj % DPB) + 16u * lane);
+					else if (is_v)
 						load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz<HD>(row)));
 					else
 						load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
 				}
 			};
-			auto load_tiles = [&](int i) __attribute__((always_inline)) { load_part(i, 0, 2 * ND); };
+			auto load_tiles = [&](auto f16_tag, int i) __attribute__((always_inline)) { load_part(f16_tag, i, 0, 2 * ND); };
 			// The first step's tiles go out before Q is read, so the latencies overlap.
-			if (n_steps > 0) load_tiles(0);
+			if (n_steps > 0)
+			{
+				if (use16)
+					load_tiles(std::true_type{}, 0);
+				else
+					load_tiles(std::false_type{}, 0);
+			}
 
 			// Q, pre-scaled into log2 units and split into bf16 hi + lo (two
 			// MFMAs against the exact bf16 K give near-fp32 scores), in LDS in
@@ -408,8 +448,9 @@ namespace nnchip
 			// wavefront in one of its MFMA phases raises its issue priority, so
 			// the other wavefront of the SIMD fills the matrix core's shadow with
 			// its softmax (measured: 4.6 % faster per prefill step).
-			auto qk_phase = [&](int i, f32x16& sc, u32x4 (&vta)[2][DBK]) __attribute__((always_inline))
+			auto qk_phase = [&](auto f16_tag, int i, f32x16& sc, u32x4 (&vta)[2][DBK]) __attribute__((always_inline))
 			{
+				constexpr bool F16 = decltype(f16_tag)::value;
 				const uint16_t* kt = k_tile(i);
 				const uint16_t* vt = kt + kWK * HD;
 				__builtin_amdgcn_s_setprio(1);
@@ -430,10 +471,18 @@ namespace nnchip
 						sc = mfma32x32x16(a, *reinterpret_cast<const bf16x8*>(s_qlo + 32 * rg * HD + q_slot(t)), sc);
 					}
 				}
+				// fp16 copy: block 2 c + h of the tile holds those eight keys of
+				// every element, 16 bytes each: one plain read per operand.
 #pragma unroll
 				for (int c = 0; c < 2; ++c)
 #pragma unroll
-					for (int b = 0; b < DBK; ++b) vta[c][b] = vt_pair(vt, c, b);
+					for (int b = 0; b < DBK; ++b)
+					{
+						if constexpr (F16)
+							vta[c][b] = *reinterpret_cast<const u32x4*>(vt + ((2 * c + h) * HD + 32 * b + r32) * 8);
+						else
+							vta[c][b] = vt_pair(vt, c, b);
+					}
 				__builtin_amdgcn_s_setprio(0);
 			};
 
@@ -547,22 +596,22 @@ namespace nnchip
 						// step): the next step's loads go there.
 						lds_reads_done();
 						__syncthreads();
-						if (i + 1 < n_steps) load_part(i + 1, 0, ND);
+						if (i + 1 < n_steps) load_part(f16_tag, i + 1, 0, ND);
 					}
 					f32x16 sc;
 					u32x4 vta[2][DBK]; // fp16 (the copy) or bf16 elements
-					qk_phase(i, sc, vta);
+					qk_phase(f16_tag, i, sc, vta);
 					if (i + 1 < n_steps)
 					{
 						if constexpr (RG > 1)
-							load_part(i + 1, ND, 2 * ND);
+							load_part(f16_tag, i + 1, ND, 2 * ND);
 						else
 						{
 							// Both tiles are read: the next step's rows. A DMA's LDS
 							// write is not ordered after earlier LDS reads still in
 							// flight, so those complete first.
 							lds_reads_done();
-							load_tiles(i + 1);
+							load_tiles(f16_tag, i + 1);
 						}
 					}
 					soft_phase(f16_tag, kw0, seg_last, sc, vta);
@@ -661,13 +710,15 @@ namespace nnchip
 		// its scores and its V^T registers, waits until every wavefront has
 		// (barrier), issues the next step's DMAs, and runs its softmax and
 		// P.V from registers while they land.
-		//   S^T = K . Q^T  per 16-key half t: lane l holds keys 16 t + 4 (l / 16)
-		//                  + i of row l % 16 (two halves, 8 scores);
+		//   S^T = K . Q^T  per 16-key tile t: lane l holds keys key16(4 (l / 16)
+		//                  + i) + 8 t of row l % 16 (two tiles, 8 scores);
 		//   P^T            the lane's 8 weights are the B operand of a 32-key
 		//                  product as they sit (k-slot 8 (l / 16) + j holds key
-		//                  4 (l / 16) + j, j < 4, and 16 + 4 (l / 16) + j - 4
-		//                  after), and V^T is read (ds_read_b64_tr_b16) in that
-		//                  key order;
+		//                  key16(4 (l / 16)) + j, j < 4, and that + 8 after), the
+		//                  key order of block l / 16 of V's fp16 copy, whose
+		//                  16 bytes per element are V^T's operand (one plain
+		//                  LDS read); the bf16 V is read (ds_read_b64_tr_b16)
+		//                  in that key order;
 		//   O^T += V^T . P^T  16 tiles of 16 elements: lane l holds elements
 		//                  16 dt + 4 (l / 16) + i of row l % 16.
 		// The softmax, the lazy offset, V's fp16 copy and the final merge of
@@ -695,6 +746,18 @@ namespace nnchip
 		// consecutive rows, and the four groups rows 4 apart; (row ^ row / 4)
 		// % 4 puts all 16 rows' reads in distinct 64-byte bank groups.
 		__device__ __forceinline__ int vswz16(int row) { return 4 * ((row ^ (row >> 2)) & 3); }
+
+		// The score tiles' key order: tile t's row x (x < 16) is key key16(x) +
+		// 8 t of the 32-key tile, i.e. tile 0 takes keys 0-7 and 16-23, tile 1
+		// keys 8-15 and 24-31. Lane l then holds keys key16(4 (l / 16)) + i
+		// (tile 0) and 8 more (tile 1), i < 4: the eight keys of block l / 16
+		// of V's fp16 copy (f16_copy_index), which its P . V product takes as
+		// they sit.
+		__device__ __forceinline__ int key16(int x) { return x + 8 * (x >> 3); }
+		// Tile rows swizzle as rows remap16(row) of a 16-row tile: the 16 rows
+		// a score tile reads (and the V^T reads of a half-wavefront) fall on
+		// 16 distinct ones.
+		__device__ __forceinline__ int remap16(int row) { return (row & 7) | ((row >> 1) & 8); }
 
 		template <int G>
 		__global__ __launch_bounds__(64 * kWaves16) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill16_kernel(
@@ -730,36 +793,47 @@ namespace nnchip
 			int rfirst = 1, rlast = 0;
 			if (my_row < n_rows) attn_span(p.causal, p.window, p.pos0 + my_row / G, p.n_seq, rfirst, rlast);
 
-			const int span = kmax >= kmin ? kmax - kmin + 1 : 0;
-			const int rb0 = span > 0 ? kmin % p.rows : 0;
+			// V's fp16 copy, and the walk from kmin rounded down to 32, as in the
+			// 32-row kernel.
+			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0 &&
+			                   ((p.rows & 31) == 0 || kmax < p.rows);
+			const int kbeg = use16 ? kmin & ~31 : kmin;
+			const int span = kmax >= kmin ? kmax - kbeg + 1 : 0;
+			const int rb0 = span > 0 ? kbeg % p.rows : 0;
 			const int len1 = min(span, p.rows - rb0);
 			const int len2 = span - len1;
 			const int n1 = (len1 + kStep - 1) / kStep;
 			const int n_steps = n1 + (len2 + kStep - 1) / kStep;
-			const int wrap_key = kmin + len1;
+			const int wrap_key = kbeg + len1;
 
 			const uint32_t row_bytes = static_cast<uint32_t>(p.kv_dim) * 2;
 			const uint32_t head_bytes = static_cast<uint32_t>(kvh) * HD * 2;
-			const bool use16 = p.V16 != nullptr && __builtin_amdgcn_readfirstlane(*p.n_bad) == 0;
 			const char* kbase = static_cast<const char*>(p.K) + head_bytes;
-			const char* vbase = static_cast<const char*>(use16 ? p.V16 : p.V) + head_bytes;
+			const char* vbase = use16 ? static_cast<const char*>(p.V16) + 8 * head_bytes
+			                          : static_cast<const char*>(p.V) + head_bytes;
 
 			auto step_key = [&](int i, int& seg_last) __attribute__((always_inline)) -> int
 			{
 				const bool second = i >= n1;
 				seg_last = second ? kmax : wrap_key - 1;
-				return (second ? wrap_key + (i - n1) * kStep : kmin + i * kStep) + kg * kWK;
+				return (second ? wrap_key + (i - n1) * kStep : kbeg + i * kStep) + kg * kWK;
 			};
 			const uint32_t step_bytes = static_cast<uint32_t>(kStep) * row_bytes;
 			const uint32_t seg1_off = static_cast<uint32_t>(rb0 + kg * kWK) * row_bytes;
 			const uint32_t seg2_off = static_cast<uint32_t>(kg * kWK) * row_bytes - static_cast<uint32_t>(n1) * step_bytes;
 			const uint32_t seg1_end = static_cast<uint32_t>(rb0 + len1 - 1) * row_bytes + HD * 2;
 			const uint32_t seg2_end = static_cast<uint32_t>(kmax - wrap_key) * row_bytes + HD * 2;
-			auto step_rsrc = [&](int i, const char* base) __attribute__((always_inline))
+			auto group_end = [&](int last_row) __attribute__((always_inline)) -> uint32_t
+			{
+				return static_cast<uint32_t>(last_row >> 5) * 32 * row_bytes + 24 * row_bytes + 16 * HD;
+			};
+			const uint32_t v_seg1_end = use16 ? group_end(rb0 + len1 - 1) : seg1_end;
+			const uint32_t v_seg2_end = use16 ? group_end(kmax - wrap_key) : seg2_end;
+			auto step_rsrc = [&](int i, const char* base, bool is_v) __attribute__((always_inline))
 			{
 				const bool second = i >= n1;
 				const uint32_t off = (second ? seg2_off : seg1_off) + static_cast<uint32_t>(i) * step_bytes;
-				const uint32_t end = second ? seg2_end : seg1_end;
+				const uint32_t end = is_v ? (second ? v_seg2_end : v_seg1_end) : (second ? seg2_end : seg1_end);
 				const uint32_t n = __builtin_amdgcn_readfirstlane(end > off ? end - off : 0u);
 				return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + off), 0, static_cast<int>(n),
 				                                         kBufferFlags);
@@ -767,13 +841,16 @@ namespace nnchip
 
 			// The key group's K tile, then its V tile; the two row groups split
 			// each tile's DMAs (row group rg: rows 16 rg .. 16 rg + 15).
+			// (tile rows swizzle as rows remap16(row): see the score tiles' key
+			// order below)
 			const int t_row = lane / LPK;
 			uint16_t* const kt = reinterpret_cast<uint16_t*>(s_raw) + kg * 2 * kWK * HD;
 			uint16_t* const vt = kt + kWK * HD;
-			auto load_tiles = [&](int i) __attribute__((always_inline))
+			auto load_tiles = [&](auto f16_tag, int i) __attribute__((always_inline))
 			{
-				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase);
-				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase);
+				constexpr bool F16 = decltype(f16_tag)::value;
+				const __amdgpu_buffer_rsrc_t rk = step_rsrc(i, kbase, false);
+				const __amdgpu_buffer_rsrc_t rv = step_rsrc(i, vbase, true);
 #pragma unroll
 				for (int e = 0; e < 2 * ND; ++e)
 				{
@@ -781,13 +858,24 @@ namespace nnchip
 					const int jj = rg * ND + (is_v ? e - ND : e);
 					const int row = jj * KPL + t_row;
 					const uint32_t rb = static_cast<uint32_t>(row) * row_bytes;
-					if (is_v)
-						load_lds16_grouped(rv, vt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz16(row)));
+					if (is_v && F16) // tile byte 1024 jj + 16 l: block jj / 4, 16 kv_dim bytes per block
+						load_lds16_grouped(rv, vt, jj, (jj >> 2) * 8 * row_bytes + 1024u * (jj & 3) + 16u * lane);
+					else if (is_v)
+						load_lds16_grouped(rv, vt, jj,
+						                   rb + 16u * static_cast<uint32_t>((lane % LPK) ^ vswz16(remap16(row))));
 					else
-						load_lds16_grouped(rk, kt, jj, rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(row)));
+						load_lds16_grouped(rk, kt, jj,
+						                   rb + 16u * static_cast<uint32_t>((lane % LPK) ^ kswz<HD>(remap16(row))));
 				}
 			};
-			if (n_steps > 0) load_tiles(0);
+			static_assert(16 * HD == 4096, "the fp16 copy's DMA offsets assume 4 KiB blocks");
+			if (n_steps > 0)
+			{
+				if (use16)
+					load_tiles(std::true_type{}, 0);
+				else
+					load_tiles(std::false_type{}, 0);
+			}
 
 			// Q, pre-scaled into log2 units, as bf16 hi + lo in LDS (the K
 			// tiles' layout): thread t converts the sixteenth t % 16 of row t / 16.
@@ -843,15 +931,16 @@ namespace nnchip
 			float l_acc = 0.0f, m_off = -INFINITY, c_init = 0.0f;
 			const f16x2 one2 = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-			// V^T for O^T tile dt, from tile rows r0 .. r0 + 15: keys r0 +
-			// 4 (l / 16) .. + 3 of element 16 dt + l % 16 (r0 = 0: k-slots
-			// 8 (l / 16) .. + 3 of the product; r0 = 16: the next four).
-			auto vt_half = [&](int dt, int r0) __attribute__((always_inline)) -> u32x2
+			// V^T for O^T tile dt (bf16 V): keys key16(4 (l / 16)) + r_off .. + 3
+			// of element 16 dt + l % 16 (r_off = 0: k-slots 8 (l / 16) .. + 3 of
+			// the product; r_off = 8: the next four).
+			auto vt_half = [&](int dt, int r_off) __attribute__((always_inline)) -> u32x2
 			{
 				const int col = 16 * dt + 4 * (r16 & 3);
 				const int slot = col >> 3, in = col & 7;
-				const int ra = r0 + 4 * g4 + (r16 >> 2);
-				return tr_read(vt + ra * HD + 8 * (slot ^ vswz16(ra)) + in);
+				// (remap16(ra) is 4 (l / 16) + (l % 16) / 4 for both r_off)
+				const int ra = key16(4 * g4) + r_off + (r16 >> 2);
+				return tr_read(vt + ra * HD + 8 * (slot ^ vswz16(4 * g4 + (r16 >> 2))) + in);
 			};
 
 			auto key_loop = [&](auto f16_tag) __attribute__((always_inline))
@@ -871,12 +960,14 @@ namespace nnchip
 					for (int t = 0; t < 2; ++t)
 					{
 						sc[t] = f32x4{c_init, c_init, c_init, c_init};
-						const int krow = 16 * t + r16;
+						// (remap16(krow) is r16 in both tiles, so the row's swizzle
+						// is kswz(r16))
+						const int krow = key16(r16) + 8 * t;
 #pragma unroll
 						for (int kk = 0; kk < KT; ++kk)
 						{
 							const bf16x8 a =
-								*reinterpret_cast<const bf16x8*>(kt + krow * HD + 8 * ((4 * kk + g4) ^ kswz<HD>(krow)));
+								*reinterpret_cast<const bf16x8*>(kt + krow * HD + 8 * ((4 * kk + g4) ^ kswz<HD>(r16)));
 							sc[t] = mfma16x16x32(a, qhi[kk], sc[t]);
 							sc[t] = mfma16x16x32(a, qlo[kk], sc[t]);
 						}
@@ -884,13 +975,18 @@ namespace nnchip
 #pragma unroll
 					for (int d = 0; d < DT; ++d)
 					{
-						const u32x2 lo = vt_half(d, 0), hi = vt_half(d, 16);
-						vta[d] = u32x4{lo.x, lo.y, hi.x, hi.y};
+						if constexpr (F16) // block l / 16 of the copy's tile: one plain read
+							vta[d] = *reinterpret_cast<const u32x4*>(vt + (g4 * HD + 16 * d + r16) * 8);
+						else
+						{
+							const u32x2 lo = vt_half(d, 0), hi = vt_half(d, 8);
+							vta[d] = u32x4{lo.x, lo.y, hi.x, hi.y};
+						}
 					}
 					__builtin_amdgcn_s_setprio(0);
 					lds_reads_done();
 					__syncthreads(); // every wavefront is done with this stage
-					if (i + 1 < n_steps) load_tiles(i + 1);
+					if (i + 1 < n_steps) load_tiles(f16_tag, i + 1);
 
 					// Mask keys outside the row's span or past the segment (only
 					// on steps that cross an edge).
@@ -902,7 +998,7 @@ namespace nnchip
 #pragma unroll
 							for (int e = 0; e < 4; ++e)
 							{
-								const int k = kw0 + 16 * t + 4 * g4 + e;
+								const int k = kw0 + key16(4 * g4 + e) + 8 * t;
 								if (k < rfirst || k > hi_key) sc[t][e] = -INFINITY;
 							}
 					}

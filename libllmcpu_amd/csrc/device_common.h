@@ -209,6 +209,26 @@ namespace nnchip
 		return (now == kF16Bad ? 1 : 0) - (was == kF16Bad ? 1 : 0);
 	}
 
+	// Layout of V's fp16 copy: blocked so that the prefill kernels' P.V
+	// products read their V^T operand with plain 16-byte LDS reads instead of
+	// transposing ones. Rows go in groups of 32 (the buffer is allocated to a
+	// whole number of groups); group g holds four blocks of [kv_dim][8]
+	// halves. Row p of the group (p = 16 c + s) sits in block 2 c + ((s >> 2)
+	// & 1), slot (s & 3) + 4 (s >> 3): block 2 c + h holds rows 16 c + 4 h +
+	// j in slots j and rows 16 c + 8 + 4 h + j in slots 4 + j (j < 4), the
+	// eight keys whose weights one lane holds for one 16- or 32-key product
+	// (the score tiles' key order). So the 16 bytes of column d of a block
+	// are one lane's V^T operand, and a 32-row group of one head is four
+	// contiguous runs of 16 * head_dim bytes, kv_dim * 16 bytes apart
+	// (f16_copy_bytes in kernels.h: the buffer's size).
+	__device__ __forceinline__ size_t f16_copy_index(int row, int col, int kv_dim)
+	{
+		const int p = row & 31;
+		const int blk = ((p >> 4) << 1) | ((p >> 2) & 1);
+		const int slot = (p & 3) | ((p >> 1) & 4);
+		return ((static_cast<size_t>(row >> 5) * 4 + blk) * kv_dim + col) * 8 + slot;
+	}
+
 	// Qwen3.5's output gate on one attention output (reference
 	// model.cpp:1759-1760, nn_ops.cpp:1731-1742): y * (1 / (1 + e^-g)).
 	__device__ __forceinline__ float gated(float y, const float* gate, size_t i)

@@ -115,7 +115,7 @@ namespace nnchip
 		const float* gate; // [n_tok][n_head * head_dim], or null: out *= sigmoid(gate) (Qwen3.5)
 		const void* K; // [rows][kv_dim]
 		const void* V;
-		const void* V16; // fp16 copy of V, or null
+		const void* V16; // fp16 copy of V (blocked: f16_copy_index), or null
 		const int* n_bad; // elements of the copy marked kF16Bad (beyond kF16CopyMax); not 0: use V
 		int rows, kv_dim, n_head, n_kv;
 		int n_tok, pos0, n_seq, window;
@@ -125,6 +125,13 @@ namespace nnchip
 	};
 
 	bool launch_prefill(prefill_params p, int head_dim, int group, bool bf16, hipStream_t stream);
+
+	// Bytes of a buffer's fp16 copy of V: its rows rounded up to whole groups
+	// of 32 (the copy's blocked layout, f16_copy_index in device_common.h).
+	inline size_t f16_copy_bytes(int rows, int kv_dim)
+	{
+		return static_cast<size_t>((rows + 31) / 32) * 32 * static_cast<size_t>(kv_dim) * 2;
+	}
 
 	// F32 rows -> the cache's element type, row (pos0 + t) % rows.
 	constexpr int kPrepMaxPairs = 256; // RoPE pairs per head (head_dim up to 512)

@@ -12,8 +12,9 @@ namespace nnchip
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
 		// With a shadow (V16 not null) the fp16 copy of the same V rows is
-		// written too, and `n_bad` (the copy's count of kF16Bad elements,
-		// values beyond kF16CopyMax) follows the elements replaced and written.
+		// written too (in its blocked layout, f16_copy_index), and `n_bad` (the
+		// copy's count of kF16Bad elements, values beyond kF16CopyMax) follows
+		// the elements replaced and written.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
 		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* V16,
 		                                   int* n_bad)
@@ -31,9 +32,10 @@ namespace nnchip
 				V[dst] = static_cast<uint16_t>(vb);
 				if (V16)
 				{
+					const size_t d16 = f16_copy_index((pos0 + t) % rows, c, kv_dim);
 					const uint16_t v16 = bf16_to_f16_bits(vb);
-					delta += bad_delta(V16[dst], v16);
-					V16[dst] = v16;
+					delta += bad_delta(V16[d16], v16);
+					V16[d16] = v16;
 				}
 			}
 			if (delta != 0) atomicAdd(n_bad, delta);
@@ -51,10 +53,11 @@ namespace nnchip
 			{
 				const int t = static_cast<int>(i / kv_dim);
 				const int c = static_cast<int>(i % kv_dim);
-				const size_t dst = static_cast<size_t>((pos0 + t) % rows) * kv_dim + c;
-				const uint16_t v16 = bf16_to_f16_bits(V[dst]);
-				delta += bad_delta(V16[dst], v16);
-				V16[dst] = v16;
+				const int row = (pos0 + t) % rows;
+				const size_t d16 = f16_copy_index(row, c, kv_dim);
+				const uint16_t v16 = bf16_to_f16_bits(V[static_cast<size_t>(row) * kv_dim + c]);
+				delta += bad_delta(V16[d16], v16);
+				V16[d16] = v16;
 			}
 			if (delta != 0) atomicAdd(n_bad, delta);
 		}

@@ -314,8 +314,10 @@ namespace nnchip
 				}
 				if (p.bf16 && p.V16 && kind == 2)
 				{
-					// V's fp16 copy of the same row (from its BF16 value).
-					uint16_t* sh = static_cast<uint16_t*>(p.V16) + off;
+					// V's fp16 copy of the same row (from its BF16 value), in its
+					// blocked layout (f16_copy_index).
+					uint16_t* sh = static_cast<uint16_t*>(p.V16);
+					const int row = (p.pos0 + t) % p.rows;
 					int delta = 0;
 #pragma unroll
 					for (int j = 0; j < NJ; ++j)
@@ -323,9 +325,10 @@ namespace nnchip
 						const int i = pos(j);
 						if (i < hd)
 						{
+							const size_t d16 = f16_copy_index(row, head * hd + i, static_cast<int>(kv_dim));
 							const uint16_t s16 = bf16_to_f16_bits(f32_to_bf16_bits(xr[j]));
-							delta += bad_delta(sh[i], s16);
-							sh[i] = s16;
+							delta += bad_delta(sh[d16], s16);
+							sh[d16] = s16;
 						}
 					}
 					if (delta != 0) atomicAdd(p.n_bad, delta);

@@ -812,10 +812,13 @@ nnc_status nnc_hip_kv_create(int32_t n_buf, const int32_t* rows, const int32_t* 
 		if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, n, kv->stream);
 		if (shadow)
 		{
-			if (e == hipSuccess) e = hipMalloc(&b.v16_alloc, n + kVOffset);
+			// zeroed: rows never written hold finite values, which the prefill
+			// kernels may read (and weigh 0) beside a group's written rows
+			const size_t n16 = nnchip::f16_copy_bytes(rows[i], kv_dim[i]);
+			if (e == hipSuccess) e = hipMalloc(&b.v16_alloc, n16 + kVOffset);
 			if (e == hipSuccess) b.v16 = static_cast<char*>(b.v16_alloc) + kVOffset;
-			if (e == hipSuccess) e = hipMemsetAsync(b.v16, 0, n, kv->stream);
-			kv->bytes += n;
+			if (e == hipSuccess) e = hipMemsetAsync(b.v16, 0, n16, kv->stream);
+			kv->bytes += n16;
 		}
 		if (e != hipSuccess) return bail(hip_fail(e, "K/V allocation"));
 		kv->bytes += 2 * n;

@@ -132,6 +132,50 @@ def test_prefill_parity(orc, key, layer, n_seq, chunk):
     assert ea <= cfg.tol, (key, layer, ea)
 
 
+_EDGE = synth.AttnConfig(7, "edge", 8, 2, 128, 1, window=300, swa_period=6)
+
+
+@pytest.mark.parametrize("cfg,layer,rows,n_seq,chunk", [
+    (synth.CONFIGS["D"], 0, 1000, 1000, 300),   # rows not a multiple of 32: the copy's last group runs past them
+    (synth.CONFIGS["B"], 0, 1000, 1000, 389),   # the same at hd 64
+    (synth.CONFIGS["C"], 0, 1000, 1000, 300),   # hd 256, window 512: the span starts mid-group
+    (_EDGE, 0, 512, 1700, 200),                 # hd 128, window 300, a 512-row ring wrapping mid-span
+])
+def test_prefill_fp16_copy_groups(orc, cfg, layer, rows, n_seq, chunk):
+    """The prefill kernels read V's fp16 copy in whole 32-row groups, from
+    the span's first key rounded down to 32 (keys before it masked), up to
+    the end of the group of its last key. Spans that start mid-group, end in
+    a group past the buffer's rows, and wrap a ring, against the oracle."""
+    got, want = run_case(orc, cfg, layer, n_seq=n_seq, pos0=n_seq - chunk, n_tok=chunk, rows=rows)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= cfg.tol, (cfg.name, rows, n_seq, ea)
+
+
+@pytest.mark.parametrize("key,chunk", [("C", 300), ("D", 200)])
+def test_prefill_ring_rows_not_whole_groups(orc, key, chunk):
+    """A 1000-row ring (rows not a multiple of 32) whose span wraps: the
+    prefill kernels take the bf16 V there (the fp16 copy's groups do not tile
+    such a ring). nnc sizes every ring in multiples of 256 rows
+    (model.cpp:1936-1957), and the oracle's restatement of its dispatch
+    assumes that, so the check is against the double-precision textbook."""
+    cfg = synth.AttnConfig(10, f"ring 1000 {key}", synth.CONFIGS[key].n_head, synth.CONFIGS[key].n_kv,
+                           synth.CONFIGS[key].head_dim, 1, window=512, swa_period=6)
+    rows, n_seq = 1000, 1600
+    pos0 = n_seq - chunk
+    K, V = synth.cache_buffer(cfg, 0, rows, n_seq)
+    q = synth.qk_rows(cfg, 0, 0, np.arange(pos0, n_seq), cfg.n_head)
+    kw = dict(window=512, causal=True, n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+    say(f"case {cfg.name}: {chunk} tokens at {pos0}, keys wrap the ring")
+    with nh.KVCache([rows], [cfg.kv_dim]) as kv:
+        kv.append(0, 0, K, V)
+        got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+    want = orc.textbook(q, K, V, kv_bf16=True, rows=rows, pos0=pos0, n_seq=n_seq, **kw)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= 5e-3
+
+
 def test_prefill_odd_batches(orc):
     """Batches of 2 and 5 tokens (session-sized: the split-K kernel), 17 and 37
     (the prefill kernel, rows that do not fill a tile), and a bidirectional
