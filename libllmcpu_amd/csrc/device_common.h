@@ -229,6 +229,59 @@ namespace nnchip
 		return ((static_cast<size_t>(row >> 5) * 4 + blk) * kv_dim + col) * 8 + slot;
 	}
 
+	// Writing the copy for positions pos0 .. pos0 + n_tok - 1 one 16-byte slot
+	// set at a time (one thread per block and column: the eight rows' values
+	// read coalesced across columns, one 16-byte store) instead of 2 bytes per
+	// element, for batches of at least kF16BlockMinTok. Valid when a
+	// position's row keeps its place in a 32-row group (rows a multiple of 32,
+	// or no wrap) and no row is written twice.
+	constexpr int kF16BlockMinTok = 16;
+	__host__ __device__ inline bool f16_blocks_ok(int rows, int pos0, int n_tok)
+	{
+		return n_tok >= kF16BlockMinTok && n_tok <= rows && ((rows & 31) == 0 || pos0 + n_tok <= rows);
+	}
+	__host__ __device__ inline int f16_block_items(int pos0, int n_tok, int kv_dim)
+	{
+		return n_tok > 0 ? (((pos0 + n_tok - 1) >> 5) - (pos0 >> 5) + 1) * 4 * kv_dim : 0;
+	}
+	// Item i of f16_block_items: column i % kv_dim of block (i / kv_dim) % 4 of
+	// the 32-position group (pos0 >> 5) + i / (4 kv_dim). src(t, col) gives
+	// the BF16 bits of position pos0 + t, which also go to V (row-major, when
+	// not null); positions outside the batch keep their slots. Returns the
+	// change in the copy's count of kF16Bad elements.
+	template <class Src>
+	__device__ __forceinline__ int f16_block_item(uint16_t* V16, uint16_t* V, int rows, int kv_dim, int pos0,
+	                                              int n_tok, int i, Src src)
+	{
+		const int d = i % kv_dim, rest = i / kv_dim, blk = rest & 3;
+		const int g = (pos0 >> 5) + (rest >> 2);
+		const int row0 = (32 * g) % rows; // the group's first row (a multiple of 32)
+		const int p0 = 16 * (blk >> 1) + 4 * (blk & 1); // slots 0-3: group rows p0 .. p0 + 3, 4-7: p0 + 8 ..
+		const int t0 = 32 * g + p0 - pos0;
+		if (t0 + 11 < 0 || t0 >= n_tok || (t0 + 3 < 0 && t0 + 8 >= n_tok)) return 0; // none of the batch
+		uint4* dst = reinterpret_cast<uint4*>(V16 + ((static_cast<size_t>(row0 >> 5) * 4 + blk) * kv_dim + d) * 8);
+		uint4 w = *dst;
+		uint16_t h[8];
+		__builtin_memcpy(h, &w, 16);
+		int delta = 0;
+#pragma unroll
+		for (int s = 0; s < 8; ++s)
+		{
+			const int off = (s & 3) + 8 * (s >> 2), t = t0 + off;
+			if (t >= 0 && t < n_tok)
+			{
+				const uint32_t b = src(t, d);
+				if (V) V[static_cast<size_t>(row0 + p0 + off) * kv_dim + d] = static_cast<uint16_t>(b);
+				const uint16_t v16 = bf16_to_f16_bits(b);
+				delta += bad_delta(h[s], v16);
+				h[s] = v16;
+			}
+		}
+		__builtin_memcpy(&w, h, 16);
+		*dst = w;
+		return delta;
+	}
+
 	// Qwen3.5's output gate on one attention output (reference
 	// model.cpp:1759-1760, nn_ops.cpp:1731-1742): y * (1 / (1 + e^-g)).
 	__device__ __forceinline__ float gated(float y, const float* gate, size_t i)

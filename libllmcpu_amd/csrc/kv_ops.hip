@@ -12,23 +12,29 @@ namespace nnchip
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
 		// With a shadow (V16 not null) the fp16 copy of the same V rows is
-		// written too (in its blocked layout, f16_copy_index), and `n_bad` (the
-		// copy's count of kF16Bad elements, values beyond kF16CopyMax) follows
-		// the elements replaced and written.
+		// written too (in its blocked layout, f16_copy_index): when
+		// f16_blocks_ok by whole 16-byte slot sets after the element loop
+		// (f16_block_item, which writes the V rows too), else element by
+		// element; `n_bad` (the copy's count of kF16Bad
+		// elements, values beyond kF16CopyMax) follows the elements replaced and
+		// written.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
 		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* V16,
 		                                   int* n_bad)
 		{
 			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+			const bool blocks = V16 && f16_blocks_ok(rows, pos0, n_tok);
+			const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+			const size_t first = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
 			int delta = 0;
-			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
-			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
+			for (size_t i = first; i < n; i += stride)
 			{
 				const int t = static_cast<int>(i / kv_dim);
 				const int c = static_cast<int>(i % kv_dim);
 				const size_t dst = static_cast<size_t>((pos0 + t) % rows) * kv_dim + c;
 				const uint32_t kb = f32_to_bf16_bits(k_rows[i]), vb = f32_to_bf16_bits(v_rows[i]);
 				K[dst] = static_cast<uint16_t>(kb);
+				if (blocks) continue; // V goes with its copy below
 				V[dst] = static_cast<uint16_t>(vb);
 				if (V16)
 				{
@@ -38,6 +44,13 @@ namespace nnchip
 					V16[d16] = v16;
 				}
 			}
+			if (blocks)
+			{
+				auto src = [&](int t, int c) { return f32_to_bf16_bits(v_rows[static_cast<size_t>(t) * kv_dim + c]); };
+				const int items = f16_block_items(pos0, n_tok, kv_dim);
+				for (size_t i = first; i < static_cast<size_t>(items); i += stride)
+					delta += f16_block_item(V16, V, rows, kv_dim, pos0, n_tok, static_cast<int>(i), src);
+			}
 			if (delta != 0) atomicAdd(n_bad, delta);
 		}
 
@@ -46,18 +59,29 @@ namespace nnchip
 		__global__ void shadow_rows_kernel(const uint16_t* V, uint16_t* V16,
 		                                   int* n_bad, int rows, int kv_dim, int pos0, int n_tok)
 		{
-			const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+			const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+			const size_t first = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
 			int delta = 0;
-			for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
-			     i += static_cast<size_t>(gridDim.x) * blockDim.x)
+			if (f16_blocks_ok(rows, pos0, n_tok))
 			{
-				const int t = static_cast<int>(i / kv_dim);
-				const int c = static_cast<int>(i % kv_dim);
-				const int row = (pos0 + t) % rows;
-				const size_t d16 = f16_copy_index(row, c, kv_dim);
-				const uint16_t v16 = bf16_to_f16_bits(V[static_cast<size_t>(row) * kv_dim + c]);
-				delta += bad_delta(V16[d16], v16);
-				V16[d16] = v16;
+				auto src = [&](int t, int c) -> uint32_t { return V[static_cast<size_t>((pos0 + t) % rows) * kv_dim + c]; };
+				const int items = f16_block_items(pos0, n_tok, kv_dim);
+				for (size_t i = first; i < static_cast<size_t>(items); i += stride)
+					delta += f16_block_item(V16, nullptr, rows, kv_dim, pos0, n_tok, static_cast<int>(i), src);
+			}
+			else
+			{
+				const size_t n = static_cast<size_t>(n_tok) * kv_dim;
+				for (size_t i = first; i < n; i += stride)
+				{
+					const int t = static_cast<int>(i / kv_dim);
+					const int c = static_cast<int>(i % kv_dim);
+					const int row = (pos0 + t) % rows;
+					const size_t d16 = f16_copy_index(row, c, kv_dim);
+					const uint16_t v16 = bf16_to_f16_bits(V[static_cast<size_t>(row) * kv_dim + c]);
+					delta += bad_delta(V16[d16], v16);
+					V16[d16] = v16;
+				}
 			}
 			if (delta != 0) atomicAdd(n_bad, delta);
 		}

@@ -119,6 +119,24 @@ namespace nnchip
 			const int hd = p.head_dim;
 			const int n_hrows = p.n_head + 2 * p.n_kv;
 			const size_t q_dim = static_cast<size_t>(p.n_head) * hd, kv_dim = static_cast<size_t>(p.n_kv) * hd;
+			// V rows without a norm into a BF16 cache with a copy (f16_blocks_ok):
+			// the launch's last column of work-groups writes them with V's fp16
+			// copy by whole 16-byte slot sets, from the V inputs (the rows only
+			// round to BF16), and the head-row work-groups take Q and K only.
+			const bool v_blocks = p.bf16 && p.V16 && !p.v_norm && f16_blocks_ok(p.rows, p.pos0, gridDim.y);
+			const int n_rows_here = v_blocks ? p.n_head + p.n_kv : n_hrows;
+			if (v_blocks && static_cast<int>(blockIdx.x) == static_cast<int>(gridDim.x) - 1)
+			{
+				const int n_tok = gridDim.y, kvd = static_cast<int>(kv_dim);
+				auto src = [&](int tt, int c) { return f32_to_bf16_bits(p.v[static_cast<size_t>(tt) * kv_dim + c]); };
+				const int items = f16_block_items(p.pos0, n_tok, kvd);
+				int delta = 0;
+				for (int i = t * 64 * kWaves + threadIdx.x; i < items; i += n_tok * 64 * kWaves)
+					delta += f16_block_item(static_cast<uint16_t*>(p.V16), static_cast<uint16_t*>(p.V), p.rows, kvd,
+					                        p.pos0, n_tok, i, src);
+				if (delta != 0) atomicAdd(p.n_bad, delta);
+				return;
+			}
 			const int half = p.n_rot / 2;
 			// Element j of this lane in a row: NJ consecutive values per lane for a
 			// full row (one wide load or store per row), else strided by 64.
@@ -140,7 +158,7 @@ namespace nnchip
 			{
 				const int hrow = blockIdx.x * kRowsPerGroup + r * kWaves + wave;
 				int kind, head;
-				const float* src = hrow < n_hrows ? row_src(hrow, kind, head) : nullptr;
+				const float* src = hrow < n_rows_here ? row_src(hrow, kind, head) : nullptr;
 				if constexpr (FULL)
 					load_row<NJ>(src, lane, x[r]);
 				else
@@ -187,7 +205,7 @@ namespace nnchip
 			for (int r = 0; r < kRowsPerWave; ++r)
 			{
 				const int hrow = blockIdx.x * kRowsPerGroup + r * kWaves + wave;
-				if (hrow >= n_hrows) break; // uniform over the wavefront
+				if (hrow >= n_rows_here) break; // uniform over the wavefront
 				int kind, head;
 				(void)row_src(hrow, kind, head);
 				float* xr = x[r];
@@ -344,7 +362,11 @@ namespace nnchip
 		{
 			constexpr int RPW = decltype(rpw_tag)::value;
 			const int rows = p.n_head + 2 * p.n_kv;
-			const dim3 grid((rows + kWaves * RPW - 1) / (kWaves * RPW), n_tok);
+			// V rows with V's fp16 copy by slot sets: Q and K rows, then one
+			// more column of work-groups (the kernel's v_blocks)
+			const bool blocks = p.bf16 && p.V16 && !p.v_norm && f16_blocks_ok(p.rows, p.pos0, n_tok);
+			const int hrows = blocks ? p.n_head + p.n_kv : rows;
+			const dim3 grid((hrows + kWaves * RPW - 1) / (kWaves * RPW) + (blocks ? 1 : 0), n_tok);
 			const dim3 block(64 * kWaves);
 			switch (p.head_dim)
 			{

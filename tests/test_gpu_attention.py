@@ -176,6 +176,41 @@ def test_prefill_ring_rows_not_whole_groups(orc, key, chunk):
     assert ea <= 5e-3
 
 
+def test_fp16_copy_same_bits_by_any_append():
+    """V's fp16 copy is written by whole 32-row slot sets for batches of 16
+    rows or more and element by element for fewer; through F32 rows and BF16
+    rows (a plain copy, then the copy's own pass). Caches filled in one or
+    two appends and in pieces of every kind — ring wraps and groups shared
+    with earlier pieces included — must hold the same copy: a prefill batch
+    over each gives the same bits."""
+    rng = np.random.default_rng(17)
+    n_head, n_kv, hd, rows, n = 8, 2, 128, 512, 700
+    kv_dim = n_kv * hd
+    k = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    kb = nh.bf16_round(k)
+    vb = nh.bf16_round(v)
+    q = rng.standard_normal((100, n_head * hd)).astype(np.float32)
+    kw = dict(pos0=600, n_seq=n, window=200, n_head=n_head, n_kv=n_kv, head_dim=hd, scale=0.09)
+    pieces = [(0, 1), (1, 1), (2, 37), (39, 5), (44, 300), (344, 17), (361, 3), (364, 336)]
+    outs = []
+    for label in ("f32 in two", "f32 in pieces", "bf16 in pieces"):
+        say(f"case fp16 copy writes: {label}")
+        with nh.KVCache([rows], [kv_dim]) as kv:
+            if label == "f32 in two":
+                kv.append_f32(0, 0, k[:400], v[:400])
+                kv.append_f32(0, 400, k[400:], v[400:])
+            else:
+                for p0, m in pieces:
+                    if label.startswith("f32"):
+                        kv.append_f32(0, p0, k[p0:p0 + m], v[p0:p0 + m])
+                    else:
+                        kv.append(0, p0, kb[p0:p0 + m], vb[p0:p0 + m])
+            outs.append(kv.attend(0, q, **kw))
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
 def test_prefill_odd_batches(orc):
     """Batches of 2 and 5 tokens (session-sized: the split-K kernel), 17 and 37
     (the prefill kernel, rows that do not fill a tile), and a bidirectional

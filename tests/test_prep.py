@@ -180,6 +180,8 @@ PREP_CASES = {
     "gemma4_partial_ff_vnorm_ring": (8, 4, 256, 12, 250, 256, True, dict(qg=True, kg=True, v_norm=True, n_rot=64,
                                                                           base=10000.0, mode=0, ff=True)),
     "f32_cache_one_token": (16, 4, 128, 1, 32767, 32768, False, dict(kg=True, n_rot=128, base=10000.0, mode=1)),
+    # 40 tokens wrapping a 256-row ring: V and its fp16 copy by 32-row groups, partial at both ends
+    "ring_wrap_groups": (8, 2, 128, 40, 250, 256, True, dict(qg=True, kg=True, n_rot=128, base=10000.0, mode=0)),
     "no_rope_hd80": (6, 2, 80, 3, 5, 16, True, dict(qg=True, kg=True, n_rot=0)),
     # a head size with a tail past the last run of eight, NORM pairs with factors, far positions in a ring
     "hd100_tail_norm_ff_far": (4, 2, 100, 5, 131000, 256, True, dict(qg=True, kg=True, v_norm=True, n_rot=100,
@@ -253,12 +255,14 @@ def test_hip_prep_rope_tables_follow_each_call(orc):
 
 
 @pytest.mark.gpu
-def test_hip_prep_then_attend_matches_oracle(orc):
+@pytest.mark.parametrize("n_past,n_tok", [(448, 64), (445, 67)])
+def test_hip_prep_then_attend_matches_oracle(orc, n_past, n_tok):
     """Prep + attention on the device against the oracle's prep + attention,
-    for a 64-token Qwen3-shaped batch appended after 448 cached positions."""
+    for a Qwen3-shaped batch appended after cached positions: 64 tokens after
+    448, and 67 after 445, whose first and last 32-row groups of V's fp16
+    copy are shared with rows outside the batch."""
     rng = np.random.default_rng(5)
     n_head, n_kv, hd, rows = 32, 8, 128, 1024
-    n_past, n_tok = 448, 64
     kw = dict(n_rot=128, base=1000000.0, mode=0, pos_scale=1.0, eps=1e-6,
               q_gamma=rng.uniform(0.5, 1.5, hd).astype(np.float32), k_gamma=rng.uniform(0.5, 1.5, hd).astype(np.float32))
     q = rng.standard_normal((n_past + n_tok, n_head * hd)).astype(np.float32)
@@ -273,7 +277,7 @@ def test_hip_prep_then_attend_matches_oracle(orc):
     scale = 1.0 / np.sqrt(hd)
     want = orc.attend_layer(qo, K, V, kv_bf16=True, rows=rows, pos0=n_past, n_head=n_head, n_kv=n_kv, head_dim=hd,
                             scale=scale)
-    say("case prep + attend: 448 cached + 64 new tokens, qwen3 shape")
+    say(f"case prep + attend: {n_past} cached + {n_tok} new tokens, qwen3 shape")
     with nh.KVCache([rows], [n_kv * hd], bf16=True) as kv:
         kv.prep_append(0, q[:n_past], k[:n_past], v[:n_past], pos0=0, n_head=n_head, n_kv=n_kv, head_dim=hd, **kw)
         qg = kv.prep_append(0, q[n_past:], k[n_past:], v[n_past:], pos0=n_past, n_head=n_head, n_kv=n_kv, head_dim=hd,
