@@ -12,12 +12,11 @@ namespace nnchip
 		// to row (pos0 + t) % rows; BF16 rounds to nearest even on the bit
 		// pattern (reference runtime.h:106-113). Two 16-bit outputs per thread.
 		// With a shadow (V16 not null) the fp16 copy of the same V rows is
-		// written too (in its blocked layout, f16_copy_index): when
-		// f16_blocks_ok by whole 16-byte slot sets after the element loop
-		// (f16_block_item, which writes the V rows too), else element by
-		// element; `n_bad` (the copy's count of kF16Bad
-		// elements, values beyond kF16CopyMax) follows the elements replaced and
-		// written.
+		// written too, in its blocked layout (f16_copy_index): by whole
+		// 16-byte slot sets after the element loop when f16_blocks_ok
+		// (f16_block_item, which then writes the V rows as well), else element
+		// by element. `n_bad` (the copy's count of kF16Bad elements, values
+		// beyond kF16CopyMax) follows the elements replaced and written.
 		__global__ void append_bf16_kernel(uint16_t* K, uint16_t* V, const float* k_rows, const float* v_rows,
 		                                   int rows, int kv_dim, int pos0, int n_tok, uint16_t* V16,
 		                                   int* n_bad)
