@@ -35,6 +35,12 @@ namespace nnchip
 		// 90.3 / 87.7; 12 was slower still than 8).
 		template <int F>
 		constexpr int kAhead = F == kGemvBf16 ? 4 : 2;
+		// BF16 instead issues every weight load of its K split (at most
+		// kGemvBf16Blocks blocks, 16 bytes per lane each) before X^T is staged, and
+		// runs its blocks unrolled with no load left to wait for (a 16-vector
+		// Qwen3-4B layer 86.9 -> 77.8 us; the quantised layouts, whose loads are
+		// 8 and 4 bytes, ran 8 % slower that way: 92.1 and 94.5 us).
+		constexpr int kGemvBf16Blocks = 16;
 		// 16-byte loads in flight per lane of the one-vector kernel, per layout
 		// (a one-vector Qwen3-4B layer, us, at 8 / 6 / 4: BF16 55.7 / 56.1 /
 		// 59.2, Q8_0 48.7 / 48.9 / 48.4, Q4_S 51.5 / 50.9 / 48.4; 16 slower).
@@ -161,9 +167,10 @@ namespace nnchip
 			const int ra = mr.r + min(col, max(m_rows - 1, 0)); // this lane's A row in the matrix (clamped; not stored)
 			const int n_mine = m_rows > 0 ? nblk : 0; // blocks of this wavefront
 			auto my_block = [&](int i) { return b0 + min(i, max(n_mine - 1, 0)); };
-			a_block<F> ab[kAhead<F>];
+			constexpr int NA = F == kGemvBf16 ? kGemvBf16Blocks : kAhead<F>; // loads in flight
+			a_block<F> ab[NA];
 #pragma unroll
-			for (int j = 0; j < kAhead<F>; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
+			for (int j = 0; j < NA; ++j) ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(j), p.cols / 32 - 1), grp);
 
 			// X^T of the range, four columns per piece (consecutive threads read
 			// consecutive 16 bytes of a token's row), loads issued eight at a time.
@@ -247,17 +254,18 @@ namespace nnchip
 
 			f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc_b = {0.0f, 0.0f, 0.0f, 0.0f};
 			const bf16x8 zero8 = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
-			for (int i0 = 0; i0 < n_mine; i0 += kAhead<F>)
+			for (int i0 = 0; i0 < n_mine; i0 += NA)
 			{
 #pragma unroll
-				for (int j = 0; j < kAhead<F>; ++j)
+				for (int j = 0; j < NA; ++j)
 				{
 					const int i = i0 + j;
 					const int bl = my_block(i) - b0; // block within the range
 					const bf16x8 a = a_operand<F>(ab[j]);
 					// The next load into this slot, kAhead blocks on (clamped: a
-					// load is never under a branch).
-					ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(i + kAhead<F>), nb_all - 1), grp);
+					// load is never under a branch); BF16 has all of its loads out.
+					if constexpr (F != kGemvBf16)
+						ab[j] = load_a<F>(mr.m.w, p.cols, ra, min(my_block(i + kAhead<F>), nb_all - 1), grp);
 					if (i < n_mine) // uniform
 					{
 						const size_t at = (static_cast<size_t>(bl) * nt + col) * 32 + 8 * grp;
@@ -726,7 +734,9 @@ namespace nnchip
 		// As few K splits as the LDS copy of X^T allows (one for a single
 		// vector at every nnc shape), the splits equal in size.
 		int max_blocks = 1;
-		while (max_blocks < nb && gemv_lds_bytes(max_blocks + 1, n_batch) <= gemv_batch_lds(format)) ++max_blocks;
+		const int cap = format == kGemvBf16 ? kGemvBf16Blocks : nb;
+		while (max_blocks < std::min(nb, cap) && gemv_lds_bytes(max_blocks + 1, n_batch) <= gemv_batch_lds(format))
+			++max_blocks;
 		n_split = (nb + max_blocks - 1) / max_blocks;
 		split_blocks = (nb + n_split - 1) / n_split;
 	}
