@@ -17,7 +17,8 @@
 // wavefronts (two work-groups per CU) stages its K range of X^T (hi, lo, and
 // for Q4_S the block sums) in LDS once; each wavefront then streams the
 // weights of its own 16 rows block by block over the whole range, kAhead<F>
-// blocks of loads in flight. With one K split the rows go straight to Y; with
+// blocks of loads in flight (BF16: every block of its split, at most 16,
+// issued before X^T is staged). With one K split the rows go straight to Y; with
 // several, each split writes a partial and a second kernel adds the splits in
 // split order, so results are the same run to run.
 #include "device_common.h"
