@@ -116,6 +116,25 @@ def test_drafter_reads_target_cache(orc):
 
 # ---- prefill ----------------------------------------------------------------------------
 
+@pytest.mark.parametrize("key,window", [("D", 0), ("D", 300), ("C", 0), ("C", 512)])
+def test_prefill_batch_past_n_seq(orc, key, window):
+    """A batch on the prefill kernels whose last tokens sit past n_seq (keys
+    end at n_seq - 1 for them, as for a drafter reading its target's cache),
+    with and without a window, against the oracle."""
+    cfg = synth.CONFIGS[key]
+    rows, n_seq, pos0, n_tok = 2048, 1990, 1960, 40
+    K, V = synth.cache_buffer(cfg, 0, rows, n_seq)
+    q = synth.qk_rows(cfg, 0, 0, np.arange(pos0, pos0 + n_tok), cfg.n_head)
+    kw = dict(window=window, n_head=cfg.n_head, n_kv=cfg.n_kv, head_dim=cfg.head_dim, scale=cfg.attn_scale)
+    say(f"case prefill past n_seq: {key}, {n_tok} tokens at {pos0}, n_seq {n_seq}, window {window}")
+    with nh.KVCache([rows], [cfg.kv_dim]) as kv:
+        kv.append(0, 0, K, V)
+        got = kv.attend(0, q, pos0=pos0, n_seq=n_seq, **kw)
+    want = orc.attend_layer(q, K, V, kv_bf16=True, rows=rows, pos0=pos0, n_seq=n_seq, **kw)
+    ea, er = errors(got, want)
+    say(f"  max-abs {ea:.3e} max-rel {er:.3e}")
+    assert ea <= cfg.tol
+
 @pytest.mark.parametrize("key,layer,n_seq,chunk", [
     ("D", 0, 4096, 512),    # Qwen3-4B: the last 512-token chunk of a 4096 prompt
     ("D", 1, 512, 512),     # the first chunk: the causal triangle only
