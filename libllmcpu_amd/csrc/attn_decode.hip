@@ -1275,25 +1275,39 @@ namespace nnchip
 			// Q^T of every tile of each head into LDS as the B operands, scaled
 			// into log2 units and split into bf16 hi + lo (entry (head, tl, kk, l)
 			// is lane l's 8 elements 32 kk + 8 (l / 16) .. of column 16 tl + l % 16).
-			// Every Q load goes out first, then the first chunk's K and V rows,
-			// so the conversion waits for Q alone (loads complete in order) and
-			// nothing waits for a round trip per entry.
-			constexpr int kQItems = HPW * NTL * KK * 64 / (64 * W);
-			static_assert(kQItems * 64 * W == HPW * NTL * KK * 64, "Q entries per thread");
-			float4 qa[kQItems], qb[kQItems];
-#pragma unroll
-			for (int u = 0; u < kQItems; ++u)
+			// A wavefront load covers elements 32 kk .. 32 kk + 31 of 8 columns
+			// (whole 128-byte lines), 16 bytes per lane; each thread converts
+			// its 4 elements and writes their 8 bytes of each half. Every Q load
+			// goes out first, then the first chunk's K and V rows, so the
+			// conversion waits for Q alone (loads complete in order) and nothing
+			// waits for a round trip per entry.
+			constexpr int kQCols = HPW * 16 * NTL; // (head, column) pairs
+			constexpr int kQLoads = kQCols * HD / 4 / (64 * W);
+			static_assert(kQLoads * 64 * W * 4 == kQCols * HD && kQCols % 8 == 0, "Q float4s per thread");
+			// float4 f: element 4 (f % 8) of block kk = (f / 64) % KK, column
+			// 8 ((f / 64) / KK) + (f / 8) % 8 of the (head, column) pairs.
+			auto q_item = [&](int u, int& qh, int& gc, int& kk, int& j) __attribute__((always_inline))
 			{
-				const int i = threadIdx.x + u * 64 * W;
-				const int l = i & 63, kk = (i >> 6) % KK, tl = ((i >> 6) / KK) % NTL, qh = (i >> 6) / (KK * NTL);
-				const int gc = 16 * tl + (l & 15), tt = gc / G;
+				const int f = static_cast<int>(threadIdx.x) + u * 64 * W;
+				j = f & 7;
+				kk = (f >> 6) % KK;
+				const int r = 8 * ((f >> 6) / KK) + ((f >> 3) & 7);
+				qh = r / (16 * NTL);
+				gc = r % (16 * NTL);
+			};
+			float4 qv[kQLoads];
+#pragma unroll
+			for (int u = 0; u < kQLoads; ++u)
+			{
+				int qh, gc, kk, j;
+				q_item(u, qh, gc, kk, j);
+				const int tt = gc / G;
 				// (a column past the batch reads its group's first token and is zeroed below)
 				const float* qp = p.q +
 				                  (static_cast<size_t>(tok0 + (tt < n_tt ? tt : 0)) * p.n_head +
 				                   head_of<HPW>(hg, qh, p.n_kv) * G + gc % G) * HD +
-				                  32 * kk + 8 * (l >> 4);
-				qa[u] = *reinterpret_cast<const float4*>(qp);
-				qb[u] = *reinterpret_cast<const float4*>(qp + 4);
+				                  32 * kk + 4 * j;
+				qv[u] = *reinterpret_cast<const float4*>(qp);
 			}
 			if (has_chunk)
 			{
@@ -1301,19 +1315,18 @@ namespace nnchip
 				load_v(c_wave);
 			}
 #pragma unroll
-			for (int u = 0; u < kQItems; ++u)
+			for (int u = 0; u < kQLoads; ++u)
 			{
-				const int i = threadIdx.x + u * 64 * W;
-				const int l = i & 63, kk = (i >> 6) % KK, tl = ((i >> 6) / KK) % NTL, qh = (i >> 6) / (KK * NTL);
-				const int tt = (16 * tl + (l & 15)) / G;
-				const bool real = tt < n_tt;
-				float x[8] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w, qb[u].x, qb[u].y, qb[u].z, qb[u].w};
-#pragma unroll
-				for (int j = 0; j < 8; ++j) x[j] = real ? x[j] * p.qscale : 0.0f;
-				bf16x8 hi, lo;
-				split_bf16x8(x, hi, lo);
-				s_q[qh][tl][kk][0][l] = __builtin_bit_cast(u32x4, hi);
-				s_q[qh][tl][kk][1][l] = __builtin_bit_cast(u32x4, lo);
+				int qh, gc, kk, j;
+				q_item(u, qh, gc, kk, j);
+				const bool real = gc / G < n_tt;
+				const float4 x = make_float4(real ? qv[u].x * p.qscale : 0.0f, real ? qv[u].y * p.qscale : 0.0f,
+				                             real ? qv[u].z * p.qscale : 0.0f, real ? qv[u].w * p.qscale : 0.0f);
+				u32x2 hi, lo;
+				split_bf16x4(x, hi, lo);
+				const int l = (gc & 15) + 16 * (j >> 1), tl = gc >> 4;
+				reinterpret_cast<u32x2*>(&s_q[qh][tl][kk][0][l])[j & 1] = hi;
+				reinterpret_cast<u32x2*>(&s_q[qh][tl][kk][1][l])[j & 1] = lo;
 			}
 			__syncthreads();
 

@@ -191,6 +191,43 @@ namespace nnchip
 			__builtin_amdgcn_sched_barrier(0);
 		}
 
+		// Q rows row0 .. row0 + ROWS - 1 of KV head kvh (row r: token r / G,
+		// query head kvh * G + r % G), pre-scaled into log2 units and split
+		// into bf16 hi + lo, into LDS in the K tiles' layout (row r, 16-byte
+		// slot s at s ^ kswz(r)); rows from n_rows on are zero. Thread t
+		// loads float4s t, t + NTHR, ... of the rows taken in order, so one
+		// wavefront load covers whole rows (a token's G query heads are
+		// adjacent in memory: whole cache lines, contiguous runs), and writes
+		// the 8 bytes of each half that its float4 gives. All loads go out
+		// before the first conversion.
+		template <int HD, int G, int ROWS, int NTHR>
+		__device__ __forceinline__ void stage_q(const float* q, size_t q_stride, float qscale, int kvh, int row0,
+		                                        int n_rows, uint16_t* s_qhi, uint16_t* s_qlo)
+		{
+			constexpr int F4 = HD / 4, N = ROWS * F4 / NTHR;
+			static_assert(N * NTHR == ROWS * F4, "Q float4s per thread");
+			float4 a[N];
+#pragma unroll
+			for (int u = 0; u < N; ++u)
+			{
+				const int f = u * NTHR + static_cast<int>(threadIdx.x), grow = row0 + f / F4;
+				a[u] = grow < n_rows ? *reinterpret_cast<const float4*>(
+										   q + static_cast<size_t>(grow / G) * q_stride +
+										   static_cast<size_t>(kvh * G + grow % G) * HD + 4 * (f % F4))
+				                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+			}
+#pragma unroll
+			for (int u = 0; u < N; ++u)
+			{
+				const int f = u * NTHR + static_cast<int>(threadIdx.x), r = f / F4, c4 = f % F4;
+				u32x2 hi, lo;
+				split_bf16x4(make_float4(a[u].x * qscale, a[u].y * qscale, a[u].z * qscale, a[u].w * qscale), hi, lo);
+				const int off = r * HD + 8 * ((c4 >> 1) ^ kswz<HD>(r)) + 4 * (c4 & 1);
+				*reinterpret_cast<u32x2*>(s_qhi + off) = hi;
+				*reinterpret_cast<u32x2*>(s_qlo + off) = lo;
+			}
+		}
+
 		template <int HD, int G, int RG>
 		__global__ __launch_bounds__(64 * kKG * RG)
 			__attribute__((amdgpu_waves_per_eu(HD == 256 ? 1 : 2, HD == 256 ? 1 : 2))) void prefill_kernel(
@@ -367,39 +404,10 @@ namespace nnchip
 
 			// Q, pre-scaled into log2 units and split into bf16 hi + lo (two
 			// MFMAs against the exact bf16 K give near-fp32 scores), in LDS in
-			// the K tiles' layout (row r, 16-byte slot s at s ^ kswz(r)): thread
-			// t converts the eighth t % 8 of row t / 8.
+			// the K tiles' layout.
 			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + S::kQlo);
 			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + S::kQhi);
-			{
-				constexpr int E = HD / 8; // elements per thread
-				const int qr = threadIdx.x >> 3, qseg = threadIdx.x & 7;
-				const int grow = row0 + qr;
-				const bool ok = grow < n_rows;
-				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
-				                                  static_cast<size_t>(kvh * G + grow % G) * HD + qseg * E
-				                            : 0);
-#pragma unroll
-				for (int c = 0; c < E / 8; ++c)
-				{
-					float xq[8];
-#pragma unroll
-					for (int u = 0; u < 2; ++u)
-					{
-						const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 8 * c + 4 * u)
-						                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-						xq[4 * u] = a.x * p.qscale;
-						xq[4 * u + 1] = a.y * p.qscale;
-						xq[4 * u + 2] = a.z * p.qscale;
-						xq[4 * u + 3] = a.w * p.qscale;
-					}
-					const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
-					bf16x8 hi, lo;
-					split_bf16x8(xq, hi, lo);
-					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
-					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
-				}
-			}
+			stage_q<HD, G, kRows, 64 * kWaves>(p.q, q_stride, p.qscale, kvh, row0, n_rows, s_qhi, s_qlo);
 			__syncthreads();
 			// Q^T as the B operand: lane l holds row l % 32, elements 16 t + 8 h .. + 8.
 			auto q_slot = [&](int t) __attribute__((always_inline)) -> int
@@ -878,38 +886,10 @@ namespace nnchip
 			}
 
 			// Q, pre-scaled into log2 units, as bf16 hi + lo in LDS (the K
-			// tiles' layout): thread t converts the sixteenth t % 16 of row t / 16.
+			// tiles' layout).
 			uint16_t* s_qhi = reinterpret_cast<uint16_t*>(s_raw + kStage16);
 			uint16_t* s_qlo = reinterpret_cast<uint16_t*>(s_raw + kStage16 + kQ16);
-			{
-				constexpr int E = HD / 16;
-				const int qr = threadIdx.x >> 4, qseg = threadIdx.x & 15;
-				const int grow = row0 + qr;
-				const bool ok = grow < n_rows;
-				const float* qp = p.q + (ok ? static_cast<size_t>(grow / G) * q_stride +
-				                                  static_cast<size_t>(kvh * G + grow % G) * HD + qseg * E
-				                            : 0);
-#pragma unroll
-				for (int c = 0; c < E / 8; ++c)
-				{
-					float xq[8];
-#pragma unroll
-					for (int u = 0; u < 2; ++u)
-					{
-						const float4 a = ok ? *reinterpret_cast<const float4*>(qp + 8 * c + 4 * u)
-						                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-						xq[4 * u] = a.x * p.qscale;
-						xq[4 * u + 1] = a.y * p.qscale;
-						xq[4 * u + 2] = a.z * p.qscale;
-						xq[4 * u + 3] = a.w * p.qscale;
-					}
-					const int off = qr * HD + 8 * ((qseg * (E / 8) + c) ^ kswz<HD>(qr));
-					bf16x8 hi, lo;
-					split_bf16x8(xq, hi, lo);
-					*reinterpret_cast<bf16x8*>(s_qhi + off) = hi;
-					*reinterpret_cast<bf16x8*>(s_qlo + off) = lo;
-				}
-			}
+			stage_q<HD, G, kRows16, 64 * kWaves16>(p.q, q_stride, p.qscale, kvh, row0, n_rows, s_qhi, s_qlo);
 			__syncthreads();
 			// Q^T as the B operand of k-step kk: lane l holds row l % 16 of the
 			// row group, elements 32 kk + 8 (l / 16) .. + 8.

@@ -152,6 +152,15 @@ namespace nnchip
 		lo = as_bf16x8(l);
 	}
 
+	// The same split of 4 values (the bits split_bf16x8 gives them), as two
+	// packed dwords per half.
+	__device__ __forceinline__ void split_bf16x4(const float4& x, u32x2& hi, u32x2& lo)
+	{
+		const uint32_t h0 = cvt_pk_bf16(x.x, x.y), h1 = cvt_pk_bf16(x.z, x.w);
+		hi = u32x2{h0, h1};
+		lo = u32x2{cvt_pk_bf16(x.x - bf16_lo(h0), x.y - bf16_hi(h0)), cvt_pk_bf16(x.z - bf16_lo(h1), x.w - bf16_hi(h1))};
+	}
+
 	// Orders one wavefront's LDS writes before its own later reads of other
 	// lanes' values (LDS executes a wavefront's operations in order; this
 	// keeps the compiler from moving them).
