@@ -16,9 +16,9 @@
 // wavefront keeps its own online softmax, and the four key groups of a row
 // group merge once, in LDS, at the end.
 //
-// The work-group first stages its Q rows through LDS (each thread loads one
-// eighth of a row once, pre-scaled into log2 units and split into bf16 hi +
-// lo, so two MFMAs against the exact bf16 K give near-fp32 scores); every
+// The work-group first stages its Q rows through LDS (whole rows per
+// wavefront load, pre-scaled into log2 units and split into bf16 hi + lo, so
+// two MFMAs against the exact bf16 K give near-fp32 scores); every
 // wavefront then keeps both halves of its B operand in registers (at
 // head_dim 256 it reads them from LDS). V comes from one of two copies:
 //   - an fp16 copy (exact copies of the bf16 values, kept beside the cache
