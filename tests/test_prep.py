@@ -189,8 +189,41 @@ PREP_CASES = {
 }
 
 
+def _sweep_cases(n: int, seed: int = 31337) -> dict:
+    """Seeded shapes beside the named ones: even head sizes up to 512 (with
+    tails past the last run of eight), groups 1-8, whole and partial RoPE in
+    both pair layouts with and without frequency factors, norms on or off,
+    1 to 512 tokens at far positions, plain buffers and wrapping rings, BF16
+    and F32 caches."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for i in range(n):
+        hd = int(rng.choice([36, 64, 80, 96, 100, 128, 256, 512]))
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        while (n_kv * hd) % 8:  # the cache's rows are whole 16-byte runs
+            n_kv *= 2
+        group = int(rng.choice([1, 2, 4, 8]))
+        n_rot = int(rng.choice([0, hd, 2 * (hd // 4), min(64, hd)]))
+        o = dict(qg=bool(rng.random() < 0.7), kg=bool(rng.random() < 0.7), v_norm=bool(rng.random() < 0.3), n_rot=n_rot,
+                 base=float(rng.choice([10000.0, 500000.0, 1000000.0])), mode=int(rng.integers(0, 2)),
+                 pos_scale=float(rng.choice([1.0, 1.0, 0.25])), ff=bool(n_rot >= 8 and rng.random() < 0.3))
+        n_tok = int(rng.choice([1, 3, 16, 17, 100, 512]))
+        pos0 = int(rng.choice([0, int(rng.integers(1, 5000)), int(rng.integers(5000, 140000))]))
+        if rng.random() < 0.4:
+            rows = 256 * int(rng.integers((n_tok + 255) // 256, (n_tok + 255) // 256 + 3))  # a ring
+        else:
+            pos0 = min(pos0, 9000)
+            rows = pos0 + n_tok + int(rng.integers(0, 40))
+        out[f"sweep{i:02d}_hd{hd}_g{group}_t{n_tok}"] = (n_kv * group, n_kv, hd, n_tok, pos0, rows,
+                                                         bool(rng.random() < 0.75), o)
+    return out
+
+
+SWEEP_CASES = _sweep_cases(16)
+
+
 def prep_case(name, orc):
-    n_head, n_kv, hd, n_tok, pos0, rows, bf16, o = PREP_CASES[name]
+    n_head, n_kv, hd, n_tok, pos0, rows, bf16, o = {**PREP_CASES, **SWEEP_CASES}[name]
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     q = (rng.standard_normal((n_tok, n_head * hd)) * 2.0).astype(np.float32)
     k = (rng.standard_normal((n_tok, n_kv * hd)) * 2.0).astype(np.float32)
@@ -212,7 +245,7 @@ def prep_case(name, orc):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", sorted(PREP_CASES))
+@pytest.mark.parametrize("name", sorted(PREP_CASES) + sorted(SWEEP_CASES))
 def test_hip_prep_matches_oracle(orc, name):
     (n_head, n_kv, hd, n_tok, pos0, rows, bf16), q, k, v, kw, (want_q, want_K, want_V) = prep_case(name, orc)
     say(f"case prep {name}: {n_tok} tokens at {pos0}, heads {n_head}/{n_kv} x {hd}, rows {rows}, bf16 {bf16}")
