@@ -135,6 +135,9 @@ GPU_SHAPES = [
     (72, 96, 3),        # rows not a multiple of 16, three blocks
     (9728, 2560, 16),   # MLP gate / up
 ]
+# seeded shapes beside them: any row count, columns any multiple of 32, 1-16 vectors
+_rng = np.random.default_rng(2560)
+GPU_SHAPES += [(int(_rng.integers(1, 3000)), 32 * int(_rng.integers(1, 320)), int(_rng.integers(1, 17))) for _ in range(8)]
 
 
 @pytest.mark.gpu
